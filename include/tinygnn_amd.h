@@ -1,0 +1,264 @@
+/*
+ * tinygnn_amd.h -- C-ABI of the MI355X (gfx950) TinyGNN sparse-inference path.
+ *
+ * This is the drop-in boundary: plain C, POD arguments, device pointers,
+ * int64 sizes, an int status, and a HIP stream passed as `tg_stream_t`
+ * (a hipStream_t; NULL = the default stream).  No exception crosses it.
+ *
+ * Each entry point names the reference interface it replaces
+ * (AnubhavChoudhery/TinyGNN, path:line).  Layout conventions match the
+ * reference `Tensor` (include/tinygnn/tensor.hpp:14-93): dense matrices are
+ * row-major fp32 with a leading dimension (ld >= cols); CSR matrices are
+ * row_ptr int32[rows+1], col_ind int32[nnz], val fp32[nnz].
+ *
+ * Status codes map onto the exceptions the reference throws:
+ *   TG_ERR_INVALID_ARGUMENT -> std::invalid_argument (format/shape errors)
+ *   TG_ERR_RUNTIME          -> std::runtime_error    (I/O, empty Model)
+ *   TG_ERR_OUT_OF_RANGE     -> std::out_of_range
+ * and tg_last_error() returns the message (thread-local, reference text).
+ *
+ * Unless stated otherwise calls are asynchronous on `stream`; inputs must
+ * stay valid until the stream reaches the call.  Entry points that must
+ * report a data-dependent error the reference raises (edge_list_to_csr's
+ * endpoint check, CSR validation) synchronise the stream, and say so.
+ */
+#ifndef TINYGNN_AMD_H
+#define TINYGNN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* tg_stream_t; /* hipStream_t */
+
+enum {
+    TG_OK = 0,
+    TG_ERR_INVALID_ARGUMENT = 1,
+    TG_ERR_RUNTIME = 2,
+    TG_ERR_OUT_OF_RANGE = 3,
+    TG_ERR_HIP = 4,
+    TG_ERR_ALLOC = 5
+};
+
+/* Activation applied by a layer (layers.hpp:Activation {None=0, ReLU=1}). */
+enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1 };
+/* Post-layer activation (model.hpp:92-96 InterActivation {None, ReLU, ELU}). */
+enum { TG_POST_NONE = 0, TG_POST_RELU = 1, TG_POST_ELU = 2 };
+/* SAGE aggregator (layers.hpp:250-253 {Mean=0, Max=1}). */
+enum { TG_AGG_MEAN = 0, TG_AGG_MAX = 1 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tg_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int tg_version(void);
+
+/* ------------------------------------------------------------------------
+ * CSR construction -- replaces GraphLoader::edge_list_to_csr
+ * (src/graph_loader.cpp:211-281, include/tinygnn/graph_loader.hpp:74-76).
+ * Row = source.  Output is bit-identical to the reference: out-degree
+ * row_ptr, each row's destinations sorted ascending with duplicates kept,
+ * values 1.0f.  row_ptr has n_nodes+1 entries, col_ind/val n_edges.
+ * Endpoints outside [0, n_nodes) fail with TG_ERR_INVALID_ARGUMENT naming
+ * the first bad edge (this check synchronises `stream`).
+ * `workspace` may be NULL (the library then allocates and frees it).
+ * ------------------------------------------------------------------------ */
+size_t tg_edge_list_to_csr_workspace_size(int64_t n_nodes, int64_t n_edges);
+int tg_edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src,
+                        const int32_t* dst, int32_t* row_ptr, int32_t* col_ind,
+                        float* val, void* workspace, size_t workspace_bytes,
+                        tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * CSR validation -- replaces the checks of Tensor::sparse_csr
+ * (src/tensor.cpp:41-96): col_ind within [0, n_cols), row_ptr
+ * non-decreasing, row_ptr[n_rows] == nnz.  Synchronises `stream`.
+ * ------------------------------------------------------------------------ */
+int tg_csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz,
+                    const int32_t* row_ptr, const int32_t* col_ind,
+                    tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Self-loops and symmetric normalisation -- replace add_self_loops
+ * (src/layers.cpp:71-144) and gcn_norm (src/layers.cpp:158-208).
+ * A must be square (n x n).  Outputs need capacity nnz + n; the produced
+ * nnz' = row_ptr_out[n] (= nnz + number of rows without a diagonal).
+ * Structure, values, degrees and 1/sqrt(deg) are bit-identical to the
+ * reference.  deg_out / dis_out (length n) may be NULL.
+ * ------------------------------------------------------------------------ */
+size_t tg_self_loops_workspace_size(int64_t n);
+int tg_add_self_loops(int64_t n, int64_t nnz, const int32_t* row_ptr,
+                      const int32_t* col_ind, const float* val,
+                      int32_t* row_ptr_out, int32_t* col_ind_out, float* val_out,
+                      void* workspace, size_t workspace_bytes, tg_stream_t stream);
+int tg_gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr,
+                const int32_t* col_ind, const float* val, int32_t* row_ptr_out,
+                int32_t* col_ind_out, float* val_out, float* deg_out,
+                float* dis_out, void* workspace, size_t workspace_bytes,
+                tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * CSR SpMM -- replaces tinygnn::spmm (src/ops.cpp:198-297, ops.hpp:112):
+ * C[m x f] = A[m x k] * B[k x f].
+ *
+ * A plan holds the degree-binned row schedule of one CSR structure
+ * (row_ptr): rows are cut into chunks of at most `chunk_nnz` nonzeros
+ * (0 = default), chunks are ordered longest first, and rows of more than
+ * one chunk are finished by an in-order reduction of per-chunk partials.
+ * Rows of at most chunk_nnz nonzeros are bit-identical to the reference
+ * (one lane per output element, fma in nonzero order); longer rows differ
+ * only by the regrouping of their sum.  `nnz_bound` >= the actual nnz
+ * (row_ptr[m]); `max_f` bounds the feature width of later executes.
+ * Plan creation allocates device memory and synchronises `stream` once.
+ * ------------------------------------------------------------------------ */
+typedef struct tg_spmm_plan_s* tg_spmm_plan_t;
+int tg_spmm_plan_create(int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                        int64_t max_f, int64_t chunk_nnz, tg_stream_t stream,
+                        tg_spmm_plan_t* plan_out);
+int tg_spmm_plan_destroy(tg_spmm_plan_t plan);
+/* Number of chunks and of multi-chunk rows (diagnostics). */
+int tg_spmm_plan_info(tg_spmm_plan_t plan, int64_t* n_chunks, int64_t* n_split_rows,
+                      int64_t* n_partials);
+int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f,
+                    const int32_t* row_ptr, const int32_t* col_ind, const float* val,
+                    const float* b, int64_t ldb, float* c, int64_t ldc,
+                    tg_stream_t stream);
+/* One-shot form: builds a plan, executes, frees it (allocates; synchronises). */
+int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+            const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
+            float* c, int64_t ldc, tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Dense transform -- replaces tinygnn::matmul (src/ops.cpp:70-162,
+ * ops.hpp:76): C[m x n] = A[m x k] * B[k x n], with an optional fused
+ * epilogue (bias add, then activation) that equals calling add_bias
+ * (ops.cpp:622) and relu_inplace / elu_inplace afterwards.
+ * algo: TG_GEMM_AUTO picks fp32 MFMA when n >= 64 and k >= 32, else the
+ * in-order kernel; TG_GEMM_INORDER is bit-identical to the reference
+ * (fma over k ascending from 0); TG_GEMM_MFMA uses v_mfma_f32_32x32x2f32.
+ * ------------------------------------------------------------------------ */
+enum { TG_GEMM_AUTO = 0, TG_GEMM_INORDER = 1, TG_GEMM_MFMA = 2 };
+enum { TG_EPI_NONE = 0, TG_EPI_RELU = 1, TG_EPI_ELU = 2 };
+int tg_matmul(int64_t m, int64_t k, int64_t n, const float* a, int64_t lda,
+              const float* b, int64_t ldb, float* c, int64_t ldc,
+              const float* bias, int epilogue, int algo, tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Epilogues -- replace the in-place activations and add_bias
+ * (src/ops.cpp:328-661).  Dense row-major, contiguous.
+ * ------------------------------------------------------------------------ */
+int tg_relu(int64_t n, float* x, tg_stream_t stream);
+int tg_leaky_relu(int64_t n, float* x, float alpha, tg_stream_t stream);
+int tg_elu(int64_t n, float* x, float alpha, tg_stream_t stream);
+int tg_sigmoid(int64_t n, float* x, tg_stream_t stream);
+int tg_tanh(int64_t n, float* x, tg_stream_t stream);
+int tg_gelu(int64_t n, float* x, tg_stream_t stream);
+int tg_softmax(int64_t rows, int64_t cols, float* x, tg_stream_t stream);
+int tg_log_softmax(int64_t rows, int64_t cols, float* x, tg_stream_t stream);
+int tg_add_bias(int64_t rows, int64_t cols, float* x, const float* bias,
+                tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * edge_softmax -- replaces tinygnn::edge_softmax (src/layers.cpp:768-822):
+ * row softmax over the CSR values; structure unchanged; empty rows kept.
+ * ------------------------------------------------------------------------ */
+int tg_edge_softmax(int64_t n_rows, const int32_t* row_ptr, const float* val,
+                    float* val_out, tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * GraphSAGE -- replaces SAGELayer::forward (src/layers.cpp:538-752) and
+ * sage_max_aggregate (src/layers.cpp:359-435).
+ * tg_sage_aggregate writes AGG[n x f]: the mean (sum in nonzero order,
+ * times 1.0f/deg; edge values ignored; duplicates counted) or the
+ * element-wise max (0 for rows without neighbours).  Uses `plan` for A.
+ * tg_sage_forward computes out = act(AGG*Wn + H*Ws + b):
+ *   dataflow TG_SAGE_CONCAT aggregates H at f_in, then one GEMM over the
+ *     concatenation [AGG | H] against [Wn ; Ws]  (needs workspace for AGG);
+ *   dataflow TG_SAGE_TRANSFORM_FIRST computes T = H*[Ws | Wn] first and
+ *     aggregates T's neighbour half at f_out (mean only; fewer bytes).
+ * ------------------------------------------------------------------------ */
+enum { TG_SAGE_AUTO = 0, TG_SAGE_CONCAT = 1, TG_SAGE_TRANSFORM_FIRST = 2 };
+int tg_sage_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t f, int agg,
+                      const int32_t* row_ptr, const int32_t* col_ind,
+                      const float* h, int64_t ldh, float* out, int64_t ldo,
+                      tg_stream_t stream);
+size_t tg_sage_forward_workspace_size(int64_t n, int64_t f_in, int64_t f_out,
+                                      int agg, int dataflow);
+int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
+                    int agg, const int32_t* row_ptr, const int32_t* col_ind,
+                    const float* h, const float* w_neigh, const float* w_self,
+                    const float* bias, int act, int post, int dataflow,
+                    float* out, void* workspace, size_t workspace_bytes,
+                    tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * GAT, all heads of one layer at once -- replaces GATLayer::forward
+ * (src/layers.cpp:945-1129) run per head plus Model's head concat/average
+ * (src/model.cpp:312-354, :403-421).
+ * wh: [n x heads*f] (head-major columns, ld = ldwh), the transformed
+ * features of every head.  att_l / att_r / bias: [heads x f].
+ * tg_gat_scores: src[i*heads+h] = a_l(h).Wh_i(h), dst likewise with a_r, in
+ * the reference's operation order (layers.cpp:991-1026).
+ * tg_gat_aggregate: per row i and head h, e_ij = LeakyReLU(src_i + dst_j),
+ * softmax over the row, out_i(h) = sum alpha_ij Wh_j(h) + b(h), then the
+ * layer activation `act` and the model's post activation `post`; heads are
+ * concatenated (out is [n x heads*f]) or averaged (concat = 0, [n x f]).
+ * The nnz x heads attention matrix is never stored.
+ * ------------------------------------------------------------------------ */
+int tg_gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh,
+                  int64_t ldwh, const float* att_l, const float* att_r, float* src,
+                  float* dst, tg_stream_t stream);
+size_t tg_gat_workspace_size(int64_t n, int64_t heads);
+int tg_gat_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
+                     const int32_t* row_ptr, const int32_t* col_ind, const float* wh,
+                     int64_t ldwh, const float* src, const float* dst, float slope,
+                     const float* bias, int act, int post, int concat, float* out,
+                     int64_t ldo, void* workspace, size_t workspace_bytes,
+                     tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Model -- replaces tinygnn::Model (include/tinygnn/model.hpp:89-164,
+ * src/model.cpp:191-439): a sequential GCN / SAGE / GAT layer graph with
+ * device-resident weights.
+ *   tg_model_add_*_layer  <- Model::add_{gcn,sage,gat}_layer (:191-247)
+ *   tg_model_set_tensor   <- one WeightFile entry (model.hpp:76-79);
+ *                            host data, copied.  Names as model.hpp:131-135.
+ *   tg_model_load_weights <- Model::load_weights(const WeightFile&) (:258-305)
+ *   tg_model_forward      <- Model::forward (:359-439).  adjacency: raw CSR
+ *     (no self-loops) on the device; x: [n x f_in] device features; out:
+ *     [n x out_cols] device.  mode TG_FORWARD_REFERENCE recomputes gcn_norm /
+ *     add_self_loops on every call as the reference does; TG_FORWARD_CACHED
+ *     reuses them (and the SpMM plans) while the adjacency pointers and
+ *     sizes are unchanged.  The model owns its intermediate buffers.
+ * ------------------------------------------------------------------------ */
+typedef struct tg_model_s* tg_model_t;
+enum { TG_FORWARD_REFERENCE = 0, TG_FORWARD_CACHED = 1 };
+int tg_model_create(tg_model_t* model_out);
+int tg_model_destroy(tg_model_t model);
+int tg_model_add_gcn_layer(tg_model_t model, int64_t in_f, int64_t out_f, int bias,
+                           int act, int post, int64_t* index_out);
+int tg_model_add_sage_layer(tg_model_t model, int64_t in_f, int64_t out_f, int agg,
+                            int bias, int act, int post, int64_t* index_out);
+int tg_model_add_gat_layer(tg_model_t model, int64_t in_f, int64_t out_f,
+                           int64_t heads, int concat, float neg_slope, int bias,
+                           int act, int post, int64_t* index_out);
+int tg_model_num_layers(tg_model_t model, int64_t* n_out);
+int tg_model_output_cols(tg_model_t model, int64_t* cols_out);
+int tg_model_set_tensor(tg_model_t model, const char* name, int64_t rows,
+                        int64_t cols, const float* host_data);
+int tg_model_load_weights(tg_model_t model);
+/* SAGE dataflow used by the model's SAGE-mean layers (TG_SAGE_*). */
+int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);
+int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
+                     const int32_t* row_ptr, const int32_t* col_ind, const float* val,
+                     int64_t f_in, const float* x, float* out, int mode,
+                     tg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYGNN_AMD_H */

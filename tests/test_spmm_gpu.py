@@ -1,0 +1,97 @@
+"""CSR SpMM on the GPU vs the oracle (reference src/ops.cpp:198-297).
+
+Bar: rows processed as one chunk (<= chunk_nnz nonzeros) are bit-identical
+to the reference's fma chain; split rows (regrouped sum) and the whole
+output are within |got-want| <= 1e-5 + 1e-4*|want|.
+"""
+import numpy as np
+import pytest
+
+from helpers import bits, random_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, a, b, chunk=0, plan=True):
+    import tinygnn_amd as tg
+    da = tg.DeviceCSR.from_numpy(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, a.val)
+    db = gpu.from_numpy(b).cuda()
+    p = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, b.shape[1], chunk) if plan else None
+    out = tg.spmm(da, db, plan=p)
+    gpu.cuda.synchronize()
+    info = p.info() if p else None
+    return out.cpu().numpy(), info
+
+
+@pytest.mark.parametrize("f", [1, 2, 3, 7, 8, 16, 32, 41, 64, 100, 128, 256, 512, 602])
+def test_spmm_widths_bitexact(gpu, restate, f):
+    rng = np.random.default_rng(100 + f)
+    a = random_csr(rng, 700, 500, avg_deg=12, max_deg=300, empty_frac=0.05)
+    b = rng.standard_normal((500, f)).astype(np.float32)
+    want = restate.spmm(a, b)
+    got, info = _run(gpu, a, b, chunk=4096)
+    assert info["n_split_rows"] == 0
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 64, 256])
+@pytest.mark.parametrize("f", [4, 41, 128, 512])
+def test_spmm_split_rows(gpu, restate, f, chunk):
+    rng = np.random.default_rng(7 * f + chunk)
+    a = random_csr(rng, 400, 300, avg_deg=20, max_deg=2000, empty_frac=0.1)
+    b = rng.standard_normal((300, f)).astype(np.float32)
+    want = restate.spmm(a, b)
+    got, info = _run(gpu, a, b, chunk=chunk)
+    deg = np.diff(a.row_ptr)
+    single = deg <= chunk
+    np.testing.assert_array_equal(bits(got[single]), bits(want[single]))
+    assert info["n_split_rows"] == int((deg > chunk).sum())
+    # Split rows add per-chunk partials: a regrouped sum.  Both it and the
+    # reference's sequential sum obey the classic bound
+    # |fl(sum) - sum| <= n * 2^-24 * sum|terms| (n = roundings per element).
+    exact, absum = _exact_spmm(a, b)
+    n_round = (deg + np.ceil(deg / chunk) + 1)[:, None]
+    bound = n_round * 2.0 ** -24 * absum * 1.01 + 1e-30
+    for name, x in (("gpu", got), ("reference", want)):
+        err = np.abs(x.astype(np.float64) - exact)
+        assert (err <= bound).all(), (name, float((err / bound).max()))
+
+
+def _exact_spmm(a, b):
+    """fp64 product and sum of |terms| (brute force over the nonzeros)."""
+    exact = np.zeros((a.n_rows, b.shape[1]))
+    absum = np.zeros_like(exact)
+    rows = np.repeat(np.arange(a.n_rows), np.diff(a.row_ptr))
+    terms = a.val.astype(np.float64)[:, None] * b.astype(np.float64)[a.col_ind]
+    np.add.at(exact, rows, terms)
+    np.add.at(absum, rows, np.abs(terms))
+    return exact, absum
+
+
+def test_spmm_one_shot_and_empty(gpu, restate):
+    rng = np.random.default_rng(3)
+    a = random_csr(rng, 300, 200, avg_deg=5, empty_frac=0.3)
+    b = rng.standard_normal((200, 24)).astype(np.float32)
+    got, _ = _run(gpu, a, b, plan=False)
+    np.testing.assert_array_equal(bits(got), bits(restate.spmm(a, b)))
+    import oracle
+    z = oracle.CSR(5, 4, np.zeros(6, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+    got, _ = _run(gpu, z, np.ones((4, 3), np.float32), plan=False)
+    assert got.shape == (5, 3) and not got.any()
+
+
+def test_spmm_reference_known_answers(gpu):
+    """test_spmm.cpp:198-222 (3x3 with identity-like structure) and the
+    fractional / negative weights case (test_spmm.cpp:1029-1047)."""
+    import oracle
+    # A = [[1,0,2],[0,3,0],[4,0,5]], B = [[1,2],[3,4],[5,6]]
+    a = oracle.CSR(3, 3, np.array([0, 2, 3, 5], np.int32), np.array([0, 2, 1, 0, 2], np.int32),
+                   np.array([1, 2, 3, 4, 5], np.float32))
+    b = np.array([[1, 2], [3, 4], [5, 6]], np.float32)
+    got, _ = _run(gpu, a, b)
+    np.testing.assert_allclose(got, [[11, 14], [9, 12], [29, 38]], rtol=0, atol=1e-6)
+    a = oracle.CSR(2, 2, np.array([0, 2, 3], np.int32), np.array([0, 1, 1], np.int32),
+                   np.array([0.5, -1.5, 0.25], np.float32))
+    b = np.array([[2, -4], [1, 8]], np.float32)
+    got, _ = _run(gpu, a, b)
+    np.testing.assert_allclose(got, [[-0.5, -14.0], [0.25, 2.0]], rtol=0, atol=1e-6)

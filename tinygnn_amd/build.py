@@ -1,0 +1,86 @@
+"""Builds libtinygnn_amd.so (gfx950) in-tree with hipcc.
+
+Every ``csrc/*.hip`` and ``csrc/*.cpp`` file is compiled to an object under
+``tinygnn_amd/_build/obj`` (in parallel) and linked into
+``tinygnn_amd/_build/libtinygnn_amd.so``.  Device code is compiled for gfx950
+only, with packed-fp32 instructions disabled and floating-point contraction
+off, so that every fused multiply-add in the kernels is an explicit one.
+
+Usage: ``python -m tinygnn_amd.build [-j N] [--quiet]``.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import glob
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+OBJ = os.path.join(BUILD, "obj")
+LIB = os.path.join(BUILD, "libtinygnn_amd.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}",
+    "-ffp-contract=off",
+]
+DEVICE = [
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-gpu-rdc",
+]
+
+
+def _sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
+
+
+def _compile(src: str, quiet: bool) -> str:
+    obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+    cmd = [HIPCC] + COMMON + DEVICE
+    if src.endswith(".cpp"):
+        cmd += ["-x", "hip"]
+    cmd += ["-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    if not quiet:
+        msgs = [l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l]
+        if msgs:
+            print("\n".join(msgs), file=sys.stderr)
+    return obj
+
+
+def build(jobs: int | None = None, quiet: bool = True) -> str:
+    """Compiles every source and links the shared library; returns its path."""
+    os.makedirs(OBJ, exist_ok=True)
+    srcs = _sources()
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, quiet), srcs))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--quiet", action="store_true")
+    a = ap.parse_args()
+    print(build(a.j, a.quiet))
+
+
+if __name__ == "__main__":
+    main()

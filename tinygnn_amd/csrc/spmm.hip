@@ -1,0 +1,553 @@
+// spmm.hip -- CSR SpMM for gfx950 and the row-schedule plan it runs on.
+//
+// Replaces tinygnn::spmm (reference src/ops.cpp:198-297).  The reference
+// walks each row's nonzeros in order and does C[i,j] = fma(val, B[col,j],
+// C[i,j]) for every feature j.  Here one lane owns VEC consecutive features
+// of one row and performs exactly that fma chain, so a row handled as one
+// chunk reproduces the reference bit for bit.  What changes is the mapping:
+// rows are cut into bounded chunks, binned by length (longest first), and
+// LPR lanes (4..64) of a wavefront cover one chunk's feature tile, so a
+// wavefront works on 64/LPR rows of similar length at once and issues
+// U independent 128-bit gathers of B rows per lane before consuming them.
+#include "aggregate.hpp"
+#include "common.hpp"
+#include "device_utils.hpp"
+#include "spmm_plan.hpp"
+
+#include <algorithm>
+#include <memory>
+
+namespace tg {
+
+// ---------------------------------------------------------------------------
+// Plan construction
+// ---------------------------------------------------------------------------
+namespace {
+
+// Length bin, two per octave, larger bin = longer chunk.
+__device__ __forceinline__ int chunk_bin(int len) {
+    if (len <= 1) return len;  // 0 -> 0, 1 -> 1
+    int lg = 31 - __clz(len);  // floor(log2 len) >= 1
+    int half = (len >> (lg - 1)) & 1;  // second half of the octave
+    int b = 2 * lg + half;
+    return b < kPlanBins ? b : kPlanBins - 1;
+}
+
+__global__ __launch_bounds__(256) void plan_count_kernel(const int32_t* __restrict__ row_ptr,
+                                                         int64_t m, int chunk,
+                                                         int32_t* __restrict__ split_cnt,
+                                                         int32_t* __restrict__ is_split,
+                                                         int32_t* __restrict__ bin_count) {
+    __shared__ int32_t hist[kPlanBins];
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r < m) {
+        const int deg = row_ptr[r + 1] - row_ptr[r];
+        const int nch = deg <= chunk ? 1 : (deg + chunk - 1) / chunk;
+        split_cnt[r] = nch > 1 ? nch : 0;
+        is_split[r] = nch > 1 ? 1 : 0;
+        if (nch == 1) {
+            atomicAdd(&hist[chunk_bin(deg)], 1);
+        } else {
+            const int full = deg / chunk, rem = deg - full * chunk;
+            atomicAdd(&hist[chunk_bin(chunk)], full);
+            if (rem) atomicAdd(&hist[chunk_bin(rem)], 1);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+        if (hist[i]) atomicAdd(&bin_count[i], hist[i]);
+}
+
+// Turns bin counts into start cursors, longest bin first; writes totals.
+__global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
+                                 int32_t* __restrict__ bin_cursor,
+                                 const int32_t* __restrict__ slot_base,
+                                 const int32_t* __restrict__ split_pos, int64_t m,
+                                 int64_t* __restrict__ totals) {
+    if (threadIdx.x == 0) {
+        int64_t acc = 0;
+        for (int b = kPlanBins - 1; b >= 0; --b) {
+            bin_cursor[b] = static_cast<int32_t>(acc);
+            acc += bin_count[b];
+        }
+        totals[0] = acc;                 // chunks
+        totals[1] = split_pos[m];        // split rows
+        totals[2] = slot_base[m];        // partial slots
+    }
+}
+
+__global__ __launch_bounds__(256) void plan_scatter_kernel(
+    const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
+    const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
+    int32_t* __restrict__ bin_cursor, int4* __restrict__ chunks, int4* __restrict__ split) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= m) return;
+    const int b = row_ptr[r], e = row_ptr[r + 1];
+    const int deg = e - b;
+    const int row = static_cast<int>(r);
+    if (deg <= chunk) {
+        const int pos = atomicAdd(&bin_cursor[chunk_bin(deg)], 1);
+        chunks[pos] = make_int4(row, b, e, -1);
+        return;
+    }
+    const int nch = (deg + chunk - 1) / chunk;
+    const int slot0 = slot_base[r];
+    for (int c = 0; c < nch; ++c) {
+        const int cb = b + c * chunk;
+        const int ce = min(e, cb + chunk);
+        const int pos = atomicAdd(&bin_cursor[chunk_bin(ce - cb)], 1);
+        chunks[pos] = make_int4(row, cb, ce, slot0 + c);
+    }
+    split[split_pos[r]] = make_int4(row, slot0, nch, deg);
+}
+
+}  // namespace
+
+void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                int64_t max_f, int64_t chunk, hipStream_t s) {
+    require(m >= 0, "spmm plan: m must be >= 0");
+    require(m < (int64_t(1) << 31), "spmm plan: m must be < 2^31");
+    require(nnz_bound >= 0 && nnz_bound < (int64_t(1) << 31),
+            "spmm plan: nnz must be < 2^31 (int32 CSR)");
+    require(max_f >= 0, "spmm plan: max_f must be >= 0");
+    if (chunk <= 0) chunk = kDefaultChunk;
+    require(chunk <= (1 << 24), "spmm plan: chunk_nnz too large");
+    TG_HIP(hipGetDevice(&p.device));
+    p.m = m;
+    p.nnz_bound = nnz_bound;
+    p.max_f = max_f;
+    p.chunk = chunk;
+    p.row_ptr = row_ptr;
+    p.n_chunks = p.n_split = p.n_partials = 0;
+    if (m == 0) return;
+    require(row_ptr != nullptr, "spmm plan: row_ptr is null");
+
+    // temporaries: split_cnt[m], is_split[m], slot_base[m+1], split_pos[m+1],
+    // bin_count[64], bin_cursor[64], totals[3], scan temp
+    Carver cv(nullptr, 0);
+    cv.take<int32_t>(m);
+    cv.take<int32_t>(m);
+    cv.take<int32_t>(m + 1);
+    cv.take<int32_t>(m + 1);
+    cv.take<int32_t>(kPlanBins);
+    cv.take<int32_t>(kPlanBins);
+    cv.take<int64_t>(4);
+    cv.take<int64_t>(scan_temp_elems(m));
+    DeviceBuffer tmp(cv.bytes());
+    Carver c(tmp.get(), tmp.size());
+    int32_t* split_cnt = c.take<int32_t>(m);
+    int32_t* is_split = c.take<int32_t>(m);
+    int32_t* slot_base = c.take<int32_t>(m + 1);
+    int32_t* split_pos = c.take<int32_t>(m + 1);
+    int32_t* bin_count = c.take<int32_t>(kPlanBins);
+    int32_t* bin_cursor = c.take<int32_t>(kPlanBins);
+    int64_t* totals = c.take<int64_t>(4);
+    int64_t* scan_tmp = c.take<int64_t>(scan_temp_elems(m));
+
+    fill_i32(bin_count, kPlanBins, 0, s);
+    const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
+    plan_count_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), split_cnt,
+                                           is_split, bin_count);
+    TG_LAUNCH_CHECK();
+    exclusive_scan_i32(split_cnt, slot_base, m, scan_tmp, s);
+    exclusive_scan_i32(is_split, split_pos, m, scan_tmp, s);
+    plan_bins_kernel<<<1, 64, 0, s>>>(bin_count, bin_cursor, slot_base, split_pos, m, totals);
+    TG_LAUNCH_CHECK();
+    int64_t host_tot[3];
+    TG_HIP(hipMemcpyAsync(host_tot, totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
+    TG_HIP(hipStreamSynchronize(s));
+    p.n_chunks = host_tot[0];
+    p.n_split = host_tot[1];
+    p.n_partials = host_tot[2];
+
+    p.chunks.resize(static_cast<size_t>(p.n_chunks) * sizeof(int4));
+    p.split.resize(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
+    if (p.n_partials > 0 && max_f > 0)
+        p.partials.resize(static_cast<size_t>(p.n_partials) * static_cast<size_t>(max_f) *
+                          sizeof(float));
+    plan_scatter_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), slot_base,
+                                             split_pos, bin_cursor, p.chunks.as<int4>(),
+                                             p.split.as<int4>());
+    TG_LAUNCH_CHECK();
+    // `tmp` is released at scope exit; make sure the scatter has consumed it.
+    TG_HIP(hipStreamSynchronize(s));
+}
+
+LaneLayout choose_layout(int64_t f, int vec) {
+    LaneLayout L{};
+    L.vec = vec;
+    const int64_t nvec = ceil_div(std::max<int64_t>(f, 1), vec);
+    if (nvec <= 64) {
+        int lpr = 4;
+        while (lpr < nvec) lpr <<= 1;
+        L.lpr = lpr;
+        L.vpl = 1;
+    } else if (nvec <= 128) {
+        L.lpr = 64;
+        L.vpl = 2;
+    } else {
+        L.lpr = 64;
+        L.vpl = 4;
+    }
+    L.tile = L.lpr * L.vpl * L.vec;
+    L.n_tiles = static_cast<int>(ceil_div(std::max<int64_t>(f, 1), L.tile));
+    return L;
+}
+
+int pick_vec(int64_t f, std::initializer_list<int64_t> lds,
+             std::initializer_list<const void*> ptrs) {
+    for (int v : {4, 2}) {
+        bool ok = (f % v) == 0;
+        for (int64_t ld : lds) ok = ok && (ld % v) == 0;
+        for (const void* p : ptrs)
+            ok = ok && (reinterpret_cast<uintptr_t>(p) % (sizeof(float) * v)) == 0;
+        if (ok) return v;
+    }
+    return 1;
+}
+
+// ---------------------------------------------------------------------------
+// Aggregation kernels
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int VEC>
+struct VecOf;
+template <>
+struct VecOf<1> { using T = float; };
+template <>
+struct VecOf<2> { using T = float2; };
+template <>
+struct VecOf<4> { using T = float4; };
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(const float* p, float (&x)[VEC]) {
+    using T = typename VecOf<VEC>::T;
+    T t = *reinterpret_cast<const T*>(p);
+    const float* q = reinterpret_cast<const float*>(&t);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) x[k] = q[k];
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(float* p, const float (&x)[VEC]) {
+    using T = typename VecOf<VEC>::T;
+    T t;
+    float* q = reinterpret_cast<float*>(&t);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) q[k] = x[k];
+    *reinterpret_cast<T*>(p) = t;
+}
+
+__device__ __forceinline__ float apply_act(float x, int act, int post) {
+    if (act == TG_ACT_RELU) x = (0.0f < x) ? x : 0.0f;
+    if (post == TG_POST_RELU) {
+        x = (0.0f < x) ? x : 0.0f;
+    } else if (post == TG_POST_ELU) {
+        if (x < 0.0f) x = 1.0f * (expf(x) - 1.0f);
+    }
+    return x;
+}
+
+template <int VEC>
+__device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, int64_t fo,
+                                             float* __restrict__ c, int64_t ldc,
+                                             const AggEpilogue& epi) {
+    if (epi.mean && deg > 0) {
+        const float inv = 1.0f / static_cast<float>(deg);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) x[k] *= inv;
+    }
+    if (epi.self) {
+        float t[VEC];
+        load_vec<VEC>(epi.self + static_cast<int64_t>(row) * epi.ld_self + fo, t);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) x[k] += t[k];
+    }
+    if (epi.bias) {
+        float t[VEC];
+        load_vec<VEC>(epi.bias + fo, t);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) x[k] += t[k];
+    }
+    if (epi.act | epi.post) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) x[k] = apply_act(x[k], epi.act, epi.post);
+    }
+    store_vec<VEC>(c + static_cast<int64_t>(row) * ldc + fo, x);
+}
+
+template <int VPL>
+struct Unroll {
+    static constexpr int value = VPL == 1 ? 8 : (VPL == 2 ? 4 : 2);
+};
+
+template <int VEC, int LPR, int VPL, bool HAS_VAL>
+__global__ __launch_bounds__(256) void agg_chunk_kernel(
+    const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
+    const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
+    float* __restrict__ C, int64_t ldc, float* __restrict__ partials, int64_t ldp, int64_t f,
+    AggEpilogue epi) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int U = Unroll<VPL>::value;
+    constexpr int TILE = LPR * VPL * VEC;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (cid >= n_chunks) return;
+    const int4 ch = chunks[cid];
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+
+    int64_t fo[VPL];
+    bool ok[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
+        ok[v] = fo[v] < f;
+    }
+    float acc[VPL][VEC];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+
+    int nz = ch.y;
+    const int e = ch.z;
+    for (; nz + U <= e; nz += U) {
+        int col[U];
+        float w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            col[u] = ci[nz + u];
+            if constexpr (HAS_VAL) w[u] = av[nz + u];
+        }
+        float bv[U][VPL][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float* brow = B + static_cast<int64_t>(col[u]) * ldb;
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+                if (ok[v]) {
+                    load_vec<VEC>(brow + fo[v], bv[u][v]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) bv[u][v][k] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    if constexpr (HAS_VAL)
+                        acc[v][k] = __builtin_fmaf(w[u], bv[u][v][k], acc[v][k]);
+                    else
+                        acc[v][k] = acc[v][k] + bv[u][v][k];
+                }
+    }
+    for (; nz < e; ++nz) {
+        const int col = ci[nz];
+        float w = 1.0f;
+        if constexpr (HAS_VAL) w = av[nz];
+        const float* brow = B + static_cast<int64_t>(col) * ldb;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+            if (ok[v]) {
+                float t[VEC];
+                load_vec<VEC>(brow + fo[v], t);
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) {
+                    if constexpr (HAS_VAL)
+                        acc[v][k] = __builtin_fmaf(w, t[k], acc[v][k]);
+                    else
+                        acc[v][k] = acc[v][k] + t[k];
+                }
+            }
+        }
+    }
+
+    if (ch.w < 0) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], C, ldc, epi);
+    } else {
+        float* prow = partials + static_cast<int64_t>(ch.w) * ldp;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            if (ok[v]) store_vec<VEC>(prow + fo[v], acc[v]);
+    }
+}
+
+// Finishes split rows: partials of a row are added in chunk order.
+template <int VEC, int LPR, int VPL>
+__global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict__ split,
+                                                         int64_t n_split,
+                                                         const float* __restrict__ partials,
+                                                         int64_t ldp, float* __restrict__ C,
+                                                         int64_t ldc, int64_t f,
+                                                         AggEpilogue epi) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int TILE = LPR * VPL * VEC;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t sid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (sid >= n_split) return;
+    const int4 sp = split[sid];
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        const int64_t fo = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
+        if (fo >= f) continue;
+        float acc[VEC];
+        load_vec<VEC>(partials + static_cast<int64_t>(sp.y) * ldp + fo, acc);
+        for (int c = 1; c < sp.z; ++c) {
+            float t[VEC];
+            load_vec<VEC>(partials + static_cast<int64_t>(sp.y + c) * ldp + fo, t);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) acc[k] = acc[k] + t[k];
+        }
+        finish_store<VEC>(acc, sp.x, sp.w, fo, C, ldc, epi);
+    }
+}
+
+template <int VEC, int LPR, int VPL, bool HAS_VAL>
+void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
+                const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
+                const AggEpilogue& epi, hipStream_t s) {
+    constexpr int GPB = 256 / LPR;
+    float* partials = p.partials.as<float>();
+    const int64_t ldp = f;
+    if (p.n_chunks > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        agg_chunk_kernel<VEC, LPR, VPL, HAS_VAL><<<grid, 256, 0, s>>>(
+            p.chunks.as<int4>(), p.n_chunks, ci, av, B, ldb, C, ldc, partials, ldp, f, epi);
+        TG_LAUNCH_CHECK();
+    }
+    if (p.n_split > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        agg_reduce_kernel<VEC, LPR, VPL><<<grid, 256, 0, s>>>(p.split.as<int4>(), p.n_split,
+                                                             partials, ldp, C, ldc, f, epi);
+        TG_LAUNCH_CHECK();
+    }
+}
+
+template <int VEC, bool HAS_VAL>
+void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
+                  const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
+                  const AggEpilogue& epi, hipStream_t s) {
+#define TG_AGG_CASE(LPR_, VPL_)                                                          \
+    if (L.lpr == LPR_ && L.vpl == VPL_)                                                  \
+        return launch_agg<VEC, LPR_, VPL_, HAS_VAL>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    TG_AGG_CASE(4, 1)
+    TG_AGG_CASE(8, 1)
+    TG_AGG_CASE(16, 1)
+    TG_AGG_CASE(32, 1)
+    TG_AGG_CASE(64, 1)
+    TG_AGG_CASE(64, 2)
+    TG_AGG_CASE(64, 4)
+#undef TG_AGG_CASE
+    throw std::logic_error("aggregate: no kernel for this lane layout");
+}
+
+}  // namespace
+
+void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const float* av,
+                   const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
+                   hipStream_t s) {
+    if (p.m == 0 || f == 0) return;
+    require(ldb >= f && ldc >= f, "aggregate: leading dimension smaller than f");
+    require(epi.self == nullptr || epi.ld_self >= f, "aggregate: self ld smaller than f");
+    if (p.n_split > 0)
+        require(f <= p.max_f,
+                "aggregate: feature width " + std::to_string(f) +
+                    " exceeds the plan's max_f " + std::to_string(p.max_f));
+    const int vec = pick_vec(f, {ldb, ldc, epi.self ? epi.ld_self : 0},
+                             {B, C, epi.self, epi.bias});
+    const LaneLayout L = choose_layout(f, vec);
+    if (av) {
+        if (vec == 4) return dispatch_lpr<4, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+        if (vec == 2) return dispatch_lpr<2, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+        return dispatch_lpr<1, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    }
+    if (vec == 4) return dispatch_lpr<4, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    if (vec == 2) return dispatch_lpr<2, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    return dispatch_lpr<1, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+}
+
+}  // namespace tg
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+using tg::guard;
+using tg::require;
+
+extern "C" {
+
+int tg_spmm_plan_create(int64_t m, int64_t nnz_bound, const int32_t* row_ptr, int64_t max_f,
+                        int64_t chunk_nnz, tg_stream_t stream, tg_spmm_plan_t* plan_out) {
+    return guard([&] {
+        require(plan_out != nullptr, "tg_spmm_plan_create: plan_out is null");
+        auto p = std::make_unique<tg_spmm_plan_s>();
+        tg::build_plan(*p, m, nnz_bound, row_ptr, max_f, chunk_nnz,
+                       static_cast<hipStream_t>(stream));
+        *plan_out = p.release();
+    });
+}
+
+int tg_spmm_plan_destroy(tg_spmm_plan_t plan) {
+    return guard([&] { delete plan; });
+}
+
+int tg_spmm_plan_info(tg_spmm_plan_t plan, int64_t* n_chunks, int64_t* n_split_rows,
+                      int64_t* n_partials) {
+    return guard([&] {
+        require(plan != nullptr, "tg_spmm_plan_info: plan is null");
+        if (n_chunks) *n_chunks = plan->n_chunks;
+        if (n_split_rows) *n_split_rows = plan->n_split;
+        if (n_partials) *n_partials = plan->n_partials;
+    });
+}
+
+int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f, const int32_t* row_ptr,
+                    const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
+                    float* c, int64_t ldc, tg_stream_t stream) {
+    return guard([&] {
+        require(plan != nullptr, "tg_spmm_execute: plan is null");
+        require(row_ptr == plan->row_ptr,
+                "tg_spmm_execute: row_ptr differs from the one the plan was built for");
+        require(k >= 0 && f >= 0, "spmm: negative dimension");
+        require(val != nullptr, "spmm: val is null");
+        tg::AggEpilogue epi;
+        tg::run_aggregate(*plan, f, col_ind, val, b, ldb, c, ldc, epi,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
+int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+            const int32_t* col_ind, const float* val, const float* b, int64_t ldb, float* c,
+            int64_t ldc, tg_stream_t stream) {
+    return guard([&] {
+        require(m >= 0 && k >= 0 && f >= 0 && nnz >= 0, "spmm: negative dimension");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (m == 0 || f == 0) return;
+        if (nnz == 0) {
+            // ops.cpp:231-236: the result is the zero-initialised C.
+            tg::fill_zero_2d(c, m, f, ldc, s);
+            return;
+        }
+        tg_spmm_plan_s p;
+        tg::build_plan(p, m, nnz, row_ptr, f, 0, s);
+        tg::AggEpilogue epi;
+        tg::run_aggregate(p, f, col_ind, val, b, ldb, c, ldc, epi, s);
+        TG_HIP(hipStreamSynchronize(s));  // the plan's buffers are freed on return
+    });
+}
+
+}  // extern "C"

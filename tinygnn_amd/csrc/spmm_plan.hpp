@@ -1,0 +1,60 @@
+// spmm_plan.hpp -- the row schedule shared by every CSR aggregation kernel
+// (SpMM, SAGE aggregation, GAT aggregation).
+//
+// A plan cuts every row of a CSR structure into chunks of at most
+// `chunk` nonzeros (an empty row is one empty chunk, so it still writes its
+// zero output), and lists the chunks longest first in 64 length bins (two
+// per octave).  One lane group processes one chunk; consecutive groups
+// therefore get chunks of similar length.  A row of more than one chunk
+// ("split row") gets one partial-result slot per chunk; a second kernel
+// adds its partials in chunk order, so results are deterministic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "common.hpp"
+
+struct tg_spmm_plan_s {
+    int64_t m = 0;
+    int64_t nnz_bound = 0;
+    int64_t max_f = 0;
+    int64_t chunk = 0;
+    int64_t n_chunks = 0;
+    int64_t n_split = 0;
+    int64_t n_partials = 0;
+    int device = 0;
+    const int32_t* row_ptr = nullptr;   // the structure the plan was built for
+    tg::DeviceBuffer chunks;            // int4 {row, begin, end, slot (-1 = direct)}
+    tg::DeviceBuffer split;             // int4 {row, first slot, n chunks, degree}
+    tg::DeviceBuffer partials;          // float [n_partials x max_f]
+};
+
+namespace tg {
+
+constexpr int kPlanBins = 64;
+constexpr int64_t kDefaultChunk = 1024;
+
+// Builds the plan (allocates, synchronises `s` once).
+void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                int64_t max_f, int64_t chunk, hipStream_t s);
+
+// Lane layout for an aggregation of width f: each lane owns VPL vectors of
+// VEC consecutive floats, LPR lanes own one row's feature tile.
+struct LaneLayout {
+    int vec;     // 1, 2 or 4 floats per access
+    int lpr;     // lanes per row group: 4, 8, 16, 32 or 64
+    int vpl;     // vectors per lane: 1, 2 or 4
+    int tile;    // features covered by one group (lpr * vpl * vec)
+    int n_tiles; // feature tiles per row
+};
+
+LaneLayout choose_layout(int64_t f, int vec);
+
+// Largest access width (4, 2, 1) allowed by f, the leading dimensions and
+// the alignment of the pointers.
+int pick_vec(int64_t f, std::initializer_list<int64_t> lds,
+             std::initializer_list<const void*> ptrs);
+
+}  // namespace tg
