@@ -136,9 +136,11 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
  * ops.hpp:76): C[m x n] = A[m x k] * B[k x n], with an optional fused
  * epilogue (bias add, then activation) that equals calling add_bias
  * (ops.cpp:622) and relu_inplace / elu_inplace afterwards.
- * algo: TG_GEMM_AUTO picks fp32 MFMA when n >= 64 and k >= 32, else the
- * in-order kernel; TG_GEMM_INORDER is bit-identical to the reference
- * (fma over k ascending from 0); TG_GEMM_MFMA uses v_mfma_f32_32x32x2f32.
+ * algo: TG_GEMM_AUTO picks fp32 MFMA when n >= 64, k >= 32 and
+ * m*n*k >= 2^32, else the in-order kernel; TG_GEMM_INORDER is bit-identical
+ * to the reference (one fma chain over k ascending from 0 per output);
+ * TG_GEMM_MFMA uses v_mfma_f32_16x16x4f32 (regrouped sums: within
+ * tolerance, not bit-identical).
  * ------------------------------------------------------------------------ */
 enum { TG_GEMM_AUTO = 0, TG_GEMM_INORDER = 1, TG_GEMM_MFMA = 2 };
 enum { TG_EPI_NONE = 0, TG_EPI_RELU = 1, TG_EPI_ELU = 2 };
@@ -178,7 +180,12 @@ int tg_edge_softmax(int64_t n_rows, const int32_t* row_ptr, const float* val,
  *   dataflow TG_SAGE_CONCAT aggregates H at f_in, then one GEMM over the
  *     concatenation [AGG | H] against [Wn ; Ws]  (needs workspace for AGG);
  *   dataflow TG_SAGE_TRANSFORM_FIRST computes T = H*[Ws | Wn] first and
- *     aggregates T's neighbour half at f_out (mean only; fewer bytes).
+ *     aggregates T's neighbour half at f_out (mean only; fewer bytes);
+ *   TG_SAGE_AUTO takes transform-first for the mean aggregator when
+ *     f_out < f_in and nnz * f_in >= 2^26, else concat.
+ * With concat and the in-order GEMM (small products) the result is
+ * bit-identical to the reference for rows of at most one plan chunk.
+ * `nnz` of the workspace query is the adjacency's nonzero count.
  * ------------------------------------------------------------------------ */
 enum { TG_SAGE_AUTO = 0, TG_SAGE_CONCAT = 1, TG_SAGE_TRANSFORM_FIRST = 2 };
 int tg_sage_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t f, int agg,
@@ -186,7 +193,7 @@ int tg_sage_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t f, int agg,
                       const float* h, int64_t ldh, float* out, int64_t ldo,
                       tg_stream_t stream);
 size_t tg_sage_forward_workspace_size(int64_t n, int64_t f_in, int64_t f_out,
-                                      int agg, int dataflow);
+                                      int agg, int dataflow, int64_t nnz);
 int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
                     int agg, const int32_t* row_ptr, const int32_t* col_ind,
                     const float* h, const float* w_neigh, const float* w_self,
@@ -206,12 +213,18 @@ int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
  * softmax over the row, out_i(h) = sum alpha_ij Wh_j(h) + b(h), then the
  * layer activation `act` and the model's post activation `post`; heads are
  * concatenated (out is [n x heads*f]) or averaged (concat = 0, [n x f]).
- * The nnz x heads attention matrix is never stored.
+ * The nnz x heads attention matrix is never stored.  `plan` is the plan of
+ * A + I's structure (values are not read); its max_f must be >= heads*f
+ * when it has split rows.  The workspace (size from
+ * tg_gat_workspace_size; NULL = allocated by the call) holds per-chunk
+ * softmax statistics of split rows and, when heads are averaged, the
+ * per-head outputs.
  * ------------------------------------------------------------------------ */
 int tg_gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh,
                   int64_t ldwh, const float* att_l, const float* att_r, float* src,
                   float* dst, tg_stream_t stream);
-size_t tg_gat_workspace_size(int64_t n, int64_t heads);
+size_t tg_gat_workspace_size(tg_spmm_plan_t plan, int64_t n, int64_t heads,
+                             int64_t f, int concat);
 int tg_gat_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
                      const int32_t* row_ptr, const int32_t* col_ind, const float* wh,
                      int64_t ldwh, const float* src, const float* dst, float slope,

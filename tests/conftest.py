@@ -18,6 +18,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: full-size (BASELINE config) cases")
 
 
+def pytest_sessionstart(session):
+    """Builds the C oracle and the HIP library when they are missing and the
+    compilers are present (a fresh checkout); the GPU box receives both
+    prebuilt and never compiles here."""
+    import shutil
+    import subprocess
+    oracle_so = os.path.join(ROOT, "oracle", "_build", "libtgoracle.so")
+    if not os.path.exists(oracle_so) and shutil.which("gcc") and shutil.which("make"):
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "oracle"], check=True)
+    from tinygnn_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH) and os.path.exists("/opt/rocm/bin/hipcc"):
+        from tinygnn_amd import build
+        build.build()
+
+
 @pytest.fixture(scope="session")
 def restate():
     import oracle

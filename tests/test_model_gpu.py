@@ -1,0 +1,151 @@
+"""Model::forward on the GPU (reference src/model.cpp:359-439).
+
+Configs A/B/C (Cora-synth GCN / SAGE-mean / GAT) against the golden outputs
+of the compiled reference (tests/golden/cora_synth.npz), then the caller's
+log_softmax: logits within |err| <= 1e-5 + 1e-4|want| and the per-node
+argmax identical.  Random stacks (multi-head concat/average, SAGE-max, post
+activations) against the oracle, both forward modes, and the reference's
+error behaviour.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import assert_close, random_csr
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLDEN)
+from golden_inputs import cora_inputs  # noqa: E402
+
+from tinygnn_amd import synth  # noqa: E402
+
+
+def _t(gpu, x):
+    return gpu.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+@pytest.fixture(scope="module")
+def cora(gpu):
+    import tinygnn_amd as tg
+    g = np.load(os.path.join(GOLDEN, "cora_synth.npz"))
+    inp = cora_inputs()
+    s = gpu.from_numpy(inp["src"]).cuda()
+    d = gpu.from_numpy(inp["dst"]).cuda()
+    adj = tg.edge_list_to_csr(s, d, synth.CORA_NODES)
+    np.testing.assert_array_equal(adj.row_ptr.cpu().numpy(), g["row_ptr"])
+    np.testing.assert_array_equal(adj.col_ind.cpu().numpy(), g["col_ind"])
+    return g, inp, adj
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("model", ["gcn", "sage", "gat"])
+def test_cora_forward_golden(gpu, restate, cora, model, mode):
+    import tinygnn_amd as tg
+    g, inp, adj = cora
+    spec, w = inp["weights"][model]
+    m = tg.Model.from_spec(spec, w)
+    x = _t(gpu, inp["x"])
+    out = m.forward(adj, x, mode=mode)
+    out2 = m.forward(adj, x, mode=mode)  # second call: cached state reused
+    gpu.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), out2.cpu().numpy())
+    want = g[f"{model}_forward"]
+    assert_close(out.cpu().numpy(), want, what=f"{model} forward")
+    logits = tg.log_softmax_(out).cpu().numpy()
+    want_logits = restate.activation("log_softmax", want)
+    assert_close(logits, want_logits, what=f"{model} logits")
+    assert (logits.argmax(1) == want_logits.argmax(1)).all()
+
+
+def test_cora_gcn_sage_bitexact(gpu, cora):
+    """GCN and SAGE at Cora scale take only bit-exact kernels (in-order
+    GEMMs, unsplit rows, concat SAGE dataflow): outputs equal the
+    reference's bytes."""
+    import tinygnn_amd as tg
+    g, inp, adj = cora
+    for model in ("gcn", "sage"):
+        spec, w = inp["weights"][model]
+        out = tg.Model.from_spec(spec, w).forward(adj, _t(gpu, inp["x"])).cpu().numpy()
+        np.testing.assert_array_equal(out.view(np.int32), g[f"{model}_forward"].view(np.int32),
+                                      err_msg=model)
+
+
+def _random_spec():
+    return [dict(type="gat", **{"in": 12}, out=5, heads=3, concat=True, slope=0.2, act=0,
+                 post=2),
+            dict(type="gat", **{"in": 15}, out=4, heads=2, concat=False, slope=0.1, act=1,
+                 post=1),
+            dict(type="sage", **{"in": 4}, out=6, agg=1, act=1, post=0),
+            dict(type="gcn", **{"in": 6}, out=3, act=0, post=0)]
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_random_stack(gpu, restate, mode):
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(9)
+    n = 600
+    a = random_csr(rng, n, n, avg_deg=8, max_deg=2500, empty_frac=0.05)
+    x = rng.standard_normal((n, 12)).astype(np.float32)
+    spec = _random_spec()
+    w = synth.model_weights(spec, seed=5)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = rng.standard_normal(w[k].shape).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    got = tg.Model.from_spec(spec, w).forward(da, _t(gpu, x), mode=mode).cpu().numpy()
+    assert_close(got, want, what="random stack")
+
+
+def test_sage_dataflows_agree(gpu, restate):
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(12)
+    n = 2000
+    a = random_csr(rng, n, n, avg_deg=30, max_deg=5000, empty_frac=0.02)
+    spec = synth.spec_sage(96, 64, 10)
+    w = synth.model_weights(spec, seed=1)
+    x = rng.standard_normal((n, 96)).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    for df in (tg.SAGE_CONCAT, tg.SAGE_TRANSFORM_FIRST):
+        m = tg.Model.from_spec(spec, w)
+        m.set_sage_dataflow(df)
+        assert_close(m.forward(da, _t(gpu, x)).cpu().numpy(), want, what=f"dataflow {df}")
+
+
+def test_model_errors(gpu):
+    import tinygnn_amd as tg
+    da = tg.DeviceCSR.from_numpy(2, 2, np.array([0, 1, 2], np.int32), np.array([1, 0], np.int32),
+                                 np.ones(2, np.float32))
+    x = gpu.ones((2, 3), device="cuda")
+    with pytest.raises(tg.TgError, match="Model::forward: no layers configured."):
+        tg.Model().forward(da, x, out=gpu.empty((2, 1), device="cuda"))
+    m = tg.Model()
+    m.add_gcn_layer(4, 2)
+    with pytest.raises(tg.InvalidArgument,
+                       match="GCNLayer::forward: H has 3 columns but layer expects in_features=4"):
+        m.forward(da, x)
+    with pytest.raises(tg.TgError, match="Model::load_weights: missing tensor 'layer0.weight'"):
+        m.load_weights({})
+    with pytest.raises(tg.InvalidArgument,
+                       match=r"GCNLayer::set_weight: expected shape \(4×2\), got \(2×4\)"):
+        m.load_weights({"layer0.weight": np.zeros((2, 4), np.float32),
+                        "layer0.bias": np.zeros((1, 2), np.float32)})
+    with pytest.raises(tg.InvalidArgument, match="SAGELayer: in_features must be > 0."):
+        m.add_sage_layer(0, 3)
+
+
+def test_zero_weights_default(gpu):
+    """Layers start with zero weights and biases (layers.cpp:213-231): an
+    unloaded GCN model outputs ReLU(0) = 0."""
+    import tinygnn_amd as tg
+    m = tg.Model()
+    m.add_gcn_layer(3, 2)
+    da = tg.DeviceCSR.from_numpy(2, 2, np.array([0, 1, 2], np.int32), np.array([1, 0], np.int32),
+                                 np.ones(2, np.float32))
+    out = m.forward(da, gpu.ones((2, 3), device="cuda")).cpu().numpy()
+    assert not out.any()

@@ -108,9 +108,18 @@ class SpmmPlan:
             pass
 
 
+def _check_spmm_shapes(a: DeviceCSR, b):
+    # ops.cpp:219-229
+    if a.n_cols != b.shape[0]:
+        raise InvalidArgument(1, f"spmm: dimension mismatch — A is ({a.n_rows}×{a.n_cols}, "
+                                 f"SparseCSR) but B is ({b.shape[0]}×{b.shape[1]}, Dense). "
+                                 f"Required: A.cols() == B.rows() ({a.n_cols} vs {b.shape[0]}).")
+
+
 def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None):
     """C = A * B (reference ops.cpp:198-297)."""
     torch = _torch()
+    _check_spmm_shapes(a, b)
     f = b.shape[1]
     if out is None:
         out = torch.empty((a.n_rows, f), dtype=torch.float32, device=b.device)
@@ -123,3 +132,297 @@ def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None):
                                       dptr(a.val), dptr(b), b.stride(0), dptr(out),
                                       out.stride(0), s))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Graph preprocessing
+# ---------------------------------------------------------------------------
+def edge_list_to_csr(src, dst, n_nodes: int, stream=None) -> DeviceCSR:
+    """GraphLoader::edge_list_to_csr (graph_loader.cpp:211-281) on the device."""
+    torch = _torch()
+    dev = src.device
+    e = int(src.numel())
+    rp = torch.empty(n_nodes + 1, dtype=torch.int32, device=dev)
+    ci = torch.empty(max(e, 1), dtype=torch.int32, device=dev)[:e]
+    v = torch.empty(max(e, 1), dtype=torch.float32, device=dev)[:e]
+    lib.check(lib.tg_edge_list_to_csr(n_nodes, e, dptr(src, torch.int32), dptr(dst, torch.int32),
+                                      dptr(rp), ci.data_ptr(), v.data_ptr(), None, 0,
+                                      stream_handle(stream)))
+    return DeviceCSR(n_nodes, n_nodes, rp, ci, v)
+
+
+def csr_validate(a: DeviceCSR, stream=None) -> None:
+    """The checks of Tensor::sparse_csr (tensor.cpp:46-86); raises InvalidArgument."""
+    lib.check(lib.tg_csr_validate(a.n_rows, a.n_cols, a.nnz, dptr(a.row_ptr),
+                                  a.col_ind.data_ptr() if a.nnz else None, stream_handle(stream)))
+
+
+def _require_square(a: DeviceCSR, fn: str):
+    if a.n_rows != a.n_cols:
+        raise InvalidArgument(1, f"{fn}: A must be square — got ({a.n_rows}×{a.n_cols}).")
+
+
+def _self_loop_outputs(a: DeviceCSR):
+    torch = _torch()
+    dev = a.row_ptr.device
+    cap = a.nnz + a.n_rows
+    return (torch.empty(a.n_rows + 1, dtype=torch.int32, device=dev),
+            torch.empty(max(cap, 1), dtype=torch.int32, device=dev),
+            torch.empty(max(cap, 1), dtype=torch.float32, device=dev))
+
+
+def _trim(a: DeviceCSR, rp, ci, v) -> DeviceCSR:
+    nnz = int(rp[-1].item()) if a.n_rows else 0
+    return DeviceCSR(a.n_rows, a.n_cols, rp, ci[:nnz], v[:nnz])
+
+
+def add_self_loops(a: DeviceCSR, stream=None) -> DeviceCSR:
+    """add_self_loops (layers.cpp:71-144): A + I, bit-identical structure/values."""
+    _require_square(a, "add_self_loops")
+    rp, ci, v = _self_loop_outputs(a)
+    lib.check(lib.tg_add_self_loops(a.n_rows, a.nnz, dptr(a.row_ptr), a.col_ind.data_ptr(),
+                                    a.val.data_ptr(), dptr(rp), dptr(ci), dptr(v), None, 0,
+                                    stream_handle(stream)))
+    return _trim(a, rp, ci, v)
+
+
+def gcn_norm(a: DeviceCSR, with_degrees: bool = False, stream=None):
+    """gcn_norm (layers.cpp:158-208): D^-1/2 (A+I) D^-1/2."""
+    torch = _torch()
+    _require_square(a, "gcn_norm")
+    rp, ci, v = _self_loop_outputs(a)
+    deg = torch.empty(max(a.n_rows, 1), dtype=torch.float32, device=rp.device)
+    dis = torch.empty_like(deg)
+    lib.check(lib.tg_gcn_norm(a.n_rows, a.nnz, dptr(a.row_ptr), a.col_ind.data_ptr(),
+                              a.val.data_ptr(), dptr(rp), dptr(ci), dptr(v), dptr(deg), dptr(dis),
+                              None, 0, stream_handle(stream)))
+    out = _trim(a, rp, ci, v)
+    return (out, deg[:a.n_rows], dis[:a.n_rows]) if with_degrees else out
+
+
+def edge_softmax(a: DeviceCSR, stream=None) -> DeviceCSR:
+    """edge_softmax (layers.cpp:768-822)."""
+    torch = _torch()
+    v = torch.zeros_like(a.val)
+    lib.check(lib.tg_edge_softmax(a.n_rows, dptr(a.row_ptr), a.val.data_ptr(), v.data_ptr(),
+                                  stream_handle(stream)))
+    return DeviceCSR(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, v)
+
+
+# ---------------------------------------------------------------------------
+# Dense ops
+# ---------------------------------------------------------------------------
+def matmul(a, b, bias=None, epilogue: int = EPI_NONE, algo: int = GEMM_AUTO, out=None,
+           stream=None):
+    """matmul (ops.cpp:70-162) with an optional fused bias + activation."""
+    torch = _torch()
+    if a.shape[1] != b.shape[0]:
+        raise InvalidArgument(1, f"matmul: dimension mismatch — A is ({a.shape[0]}×{a.shape[1]})"
+                                 f" but B is ({b.shape[0]}×{b.shape[1]})")
+    m, k = a.shape
+    n = b.shape[1]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    lib.check(lib.tg_matmul(m, k, n, dptr(a), a.stride(0), dptr(b), b.stride(0), dptr(out),
+                            out.stride(0), dptr(bias), epilogue, algo, stream_handle(stream)))
+    return out
+
+
+def _unary(name, x, *extra, stream=None):
+    lib.check(getattr(lib, name)(x.numel(), dptr(x), *extra, stream_handle(stream)))
+    return x
+
+
+def relu_(x, stream=None):
+    return _unary("tg_relu", x, stream=stream)
+
+
+def leaky_relu_(x, alpha: float = 0.01, stream=None):
+    return _unary("tg_leaky_relu", x, alpha, stream=stream)
+
+
+def elu_(x, alpha: float = 1.0, stream=None):
+    return _unary("tg_elu", x, alpha, stream=stream)
+
+
+def sigmoid_(x, stream=None):
+    return _unary("tg_sigmoid", x, stream=stream)
+
+
+def tanh_(x, stream=None):
+    return _unary("tg_tanh", x, stream=stream)
+
+
+def gelu_(x, stream=None):
+    return _unary("tg_gelu", x, stream=stream)
+
+
+def softmax_(x, stream=None):
+    lib.check(lib.tg_softmax(x.shape[0], x.shape[1], dptr(x), stream_handle(stream)))
+    return x
+
+
+def log_softmax_(x, stream=None):
+    lib.check(lib.tg_log_softmax(x.shape[0], x.shape[1], dptr(x), stream_handle(stream)))
+    return x
+
+
+def add_bias_(x, bias, stream=None):
+    n = x.shape[1]
+    if bias.dim() != 2 or bias.shape[0] != 1 or bias.shape[1] != n:
+        shp = tuple(bias.shape) if bias.dim() == 2 else (1, bias.numel())
+        raise InvalidArgument(1, f"add_bias: bias must be shape (1×{n}) to match X columns, "
+                                 f"but got ({shp[0]}×{shp[1]}).")
+    lib.check(lib.tg_add_bias(x.shape[0], n, dptr(x), dptr(bias), stream_handle(stream)))
+    return x
+
+
+# ---------------------------------------------------------------------------
+# Layers
+# ---------------------------------------------------------------------------
+def sage_aggregate(plan: SpmmPlan, a: DeviceCSR, h, agg: int = AGG_MEAN, stream=None):
+    torch = _torch()
+    out = torch.empty((a.n_rows, h.shape[1]), dtype=torch.float32, device=h.device)
+    lib.check(lib.tg_sage_aggregate(plan.h, a.n_rows, h.shape[1], agg, dptr(a.row_ptr),
+                                    a.col_ind.data_ptr(), dptr(h), h.stride(0), dptr(out),
+                                    out.stride(0), stream_handle(stream)))
+    return out
+
+
+def sage_forward(plan: SpmmPlan, a: DeviceCSR, h, w_neigh, w_self, bias=None,
+                 act: int = ACT_RELU, post: int = POST_NONE, agg: int = AGG_MEAN,
+                 dataflow: int = SAGE_AUTO, stream=None):
+    """SAGELayer::forward (layers.cpp:538-752)."""
+    torch = _torch()
+    f_in, f_out = w_neigh.shape
+    out = torch.empty((a.n_rows, f_out), dtype=torch.float32, device=h.device)
+    lib.check(lib.tg_sage_forward(plan.h, a.n_rows, f_in, f_out, agg, dptr(a.row_ptr),
+                                  a.col_ind.data_ptr(), dptr(h), dptr(w_neigh), dptr(w_self),
+                                  dptr(bias), act, post, dataflow, dptr(out), None, 0,
+                                  stream_handle(stream)))
+    return out
+
+
+def gat_scores(wh, heads: int, f: int, att_l, att_r, stream=None):
+    torch = _torch()
+    n = wh.shape[0]
+    src = torch.empty((n, heads), dtype=torch.float32, device=wh.device)
+    dst = torch.empty_like(src)
+    lib.check(lib.tg_gat_scores(n, heads, f, dptr(wh), wh.stride(0), dptr(att_l), dptr(att_r),
+                                dptr(src), dptr(dst), stream_handle(stream)))
+    return src, dst
+
+
+def gat_aggregate(plan: SpmmPlan, a_sl: DeviceCSR, wh, heads: int, f: int, src, dst,
+                  slope: float = 0.2, bias=None, act: int = ACT_NONE, post: int = POST_NONE,
+                  concat: bool = True, stream=None):
+    """All heads of GATLayer::forward's fused edge pass (layers.cpp:1052-1112)."""
+    torch = _torch()
+    cols = heads * f if (concat or heads == 1) else f
+    out = torch.empty((a_sl.n_rows, cols), dtype=torch.float32, device=wh.device)
+    lib.check(lib.tg_gat_aggregate(plan.h, a_sl.n_rows, heads, f, dptr(a_sl.row_ptr),
+                                   a_sl.col_ind.data_ptr(), dptr(wh), wh.stride(0), dptr(src),
+                                   dptr(dst), slope, dptr(bias), act, post, int(concat),
+                                   dptr(out), out.stride(0), None, 0, stream_handle(stream)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Model
+# ---------------------------------------------------------------------------
+class Model:
+    """tinygnn::Model (model.hpp:89-164) on the device, over tg_model_*."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        lib.check(lib.tg_model_create(C.byref(h)))
+        self.h = h
+
+    def add_gcn_layer(self, in_f, out_f, bias=True, act=ACT_RELU, post=POST_NONE) -> int:
+        i = C.c_int64()
+        lib.check(lib.tg_model_add_gcn_layer(self.h, in_f, out_f, int(bias), act, post,
+                                             C.byref(i)))
+        return i.value
+
+    def add_sage_layer(self, in_f, out_f, agg=AGG_MEAN, bias=True, act=ACT_RELU,
+                       post=POST_NONE) -> int:
+        i = C.c_int64()
+        lib.check(lib.tg_model_add_sage_layer(self.h, in_f, out_f, agg, int(bias), act, post,
+                                              C.byref(i)))
+        return i.value
+
+    def add_gat_layer(self, in_f, out_f, num_heads=1, concat=True, neg_slope=0.2, bias=True,
+                      act=ACT_NONE, post=POST_NONE) -> int:
+        i = C.c_int64()
+        lib.check(lib.tg_model_add_gat_layer(self.h, in_f, out_f, num_heads, int(concat),
+                                             neg_slope, int(bias), act, post, C.byref(i)))
+        return i.value
+
+    def num_layers(self) -> int:
+        n = C.c_int64()
+        lib.check(lib.tg_model_num_layers(self.h, C.byref(n)))
+        return n.value
+
+    def output_cols(self) -> int:
+        n = C.c_int64()
+        lib.check(lib.tg_model_output_cols(self.h, C.byref(n)))
+        return n.value
+
+    def set_tensor(self, name: str, array) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(array, dtype=np.float32)
+        if a.ndim == 1:
+            a = a.reshape(1, -1)
+        lib.check(lib.tg_model_set_tensor(self.h, name.encode(), a.shape[0], a.shape[1],
+                                          a.ctypes.data_as(C.c_void_p)))
+
+    def load_weights(self, weights: dict | None = None) -> None:
+        for k, v in (weights or {}).items():
+            self.set_tensor(k, v)
+        lib.check(lib.tg_model_load_weights(self.h))
+
+    def set_sage_dataflow(self, dataflow: int) -> None:
+        lib.check(lib.tg_model_set_sage_dataflow(self.h, dataflow))
+
+    def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):
+        torch = _torch()
+        if out is None:
+            out = torch.empty((adj.n_rows, self.output_cols()), dtype=torch.float32,
+                              device=x.device)
+        lib.check(lib.tg_model_forward(self.h, adj.n_rows, adj.nnz, dptr(adj.row_ptr),
+                                       adj.col_ind.data_ptr(), adj.val.data_ptr(), x.shape[1],
+                                       dptr(x), dptr(out), mode, stream_handle(stream)))
+        return out
+
+    @staticmethod
+    def from_spec(spec, weights: dict | None = None) -> "Model":
+        """Builds a model from layer dicts (see tinygnn_amd.synth.spec_*)."""
+        m = Model()
+        for l in spec:
+            t = l["type"]
+            if t == "gcn":
+                m.add_gcn_layer(l["in"], l["out"], l.get("bias", True), l.get("act", ACT_RELU),
+                                l.get("post", POST_NONE))
+            elif t == "sage":
+                m.add_sage_layer(l["in"], l["out"], l.get("agg", AGG_MEAN), l.get("bias", True),
+                                 l.get("act", ACT_RELU), l.get("post", POST_NONE))
+            elif t == "gat":
+                m.add_gat_layer(l["in"], l["out"], l.get("heads", 1), l.get("concat", True),
+                                l.get("slope", 0.2), l.get("bias", True), l.get("act", ACT_NONE),
+                                l.get("post", POST_NONE))
+            else:
+                raise ValueError(t)
+        if weights is not None:
+            m.load_weights(weights)
+        return m
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            lib.tg_model_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -81,11 +81,11 @@ SIGNATURES = {
     "tg_add_bias": (i32, [i64, i64, vp, vp, vp]),
     "tg_edge_softmax": (i32, [i64, vp, vp, vp, vp]),
     "tg_sage_aggregate": (i32, [vp, i64, i64, i32, vp, vp, vp, i64, vp, i64, vp]),
-    "tg_sage_forward_workspace_size": (sz, [i64, i64, i64, i32, i32]),
+    "tg_sage_forward_workspace_size": (sz, [i64, i64, i64, i32, i32, i64]),
     "tg_sage_forward": (i32, [vp, i64, i64, i64, i32, vp, vp, vp, vp, vp, vp, i32, i32, i32,
                               vp, vp, sz, vp]),
     "tg_gat_scores": (i32, [i64, i64, i64, vp, i64, vp, vp, vp, vp, vp]),
-    "tg_gat_workspace_size": (sz, [i64, i64]),
+    "tg_gat_workspace_size": (sz, [vp, i64, i64, i64, i32]),
     "tg_gat_aggregate": (i32, [vp, i64, i64, i64, vp, vp, vp, i64, vp, vp, f32, vp, i32, i32,
                                i32, vp, i64, vp, sz, vp]),
     "tg_model_create": (i32, [C.POINTER(vp)]),

@@ -21,12 +21,14 @@ struct AggEpilogue {
     const float* self = nullptr;
     int64_t ld_self = 0;
     int mean = 0;
+    int max = 0;   // element-wise max instead of a sum (SAGE-Max); empty rows give 0
     int act = 0;
     int post = 0;
 };
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is
-// val[nz] (fma, in nonzero order) or, when val is null, 1 (plain add).
+// val[nz] (fma, in nonzero order) or, when val is null, 1 (plain add); with
+// epi.max the element-wise maximum of B[col, :] over the row instead.
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
                    const AggEpilogue& epi, hipStream_t s);

@@ -1,0 +1,495 @@
+// dense.hip -- dense transforms and epilogues for gfx950.
+//
+// Replaces tinygnn::matmul (reference src/ops.cpp:70-162) and the in-place
+// epilogues (ops.cpp:328-661): relu, leaky_relu, elu, sigmoid, tanh, gelu,
+// softmax, log_softmax, add_bias, plus edge_softmax (src/layers.cpp:768-822).
+//
+// Two GEMMs:
+//   * in order: one fma chain per output over k ascending from 0, through
+//     LDS tiles -- bit-identical to the reference; used for thin outputs
+//     (F_out 7/16/41) where the product is not a real contraction;
+//   * MFMA: v_mfma_f32_16x16x4f32, 128x128 workgroup tiles of four 64x64
+//     wavefront tiles, for the wide transforms (602->256, 4 heads x 64).
+// Both fuse the bias add and the activation into the store.
+#include "common.hpp"
+#include "dense.hpp"
+#include "device_utils.hpp"
+
+#include <string>
+
+namespace tg {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float epi_apply(float x, const float* __restrict__ bias, int64_t n,
+                                           int epi) {
+    if (bias) x = x + bias[n];
+    if (epi == TG_EPI_RELU) {
+        x = (0.0f < x) ? x : 0.0f;
+    } else if (epi == TG_EPI_ELU) {
+        if (x < 0.0f) x = 1.0f * (expf(x) - 1.0f);
+    }
+    return x;
+}
+
+// ---------------------------------------------------------------------------
+// In-order GEMM (bit-exact)
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int TM, int TN, bool DUAL>
+__global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
+    constexpr int BK = 16;
+    constexpr int TX = BN / TN;
+    constexpr int TY = BM / TM;
+    static_assert(TX * TY == 256, "256 threads");
+    constexpr int NP = DUAL ? 2 : 1;
+    __shared__ float As[NP][BK][BM];
+    __shared__ float Bs[NP][BK][BN];
+    const int tx = threadIdx.x % TX;
+    const int ty = threadIdx.x / TX;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * BM;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * BN;
+    const int64_t M = g.m, N = g.n, K = g.k1;
+
+    float acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
+
+    bool tail[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+        tail[j] = DUAL && g.tail_from >= 0 && (n0 + tx * TN + j) >= g.tail_from;
+
+    for (int64_t k0 = 0; k0 < K; k0 += BK) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float* A = p ? g.a2 : g.a1;
+            const float* B = p ? g.b2 : g.b1;
+            const int64_t lda = p ? g.lda2 : g.lda1;
+            const int64_t ldb = p ? g.ldb2 : g.ldb1;
+            for (int e = threadIdx.x; e < BM * BK; e += 256) {
+                const int mm = e / BK, kk = e % BK;
+                const int64_t gm = m0 + mm, gk = k0 + kk;
+                As[p][kk][mm] = (gm < M && gk < K) ? A[gm * lda + gk] : 0.0f;
+            }
+            for (int e = threadIdx.x; e < BN * BK; e += 256) {
+                const int kk = e / BN, nn = e % BN;
+                const int64_t gk = k0 + kk, gn = n0 + nn;
+                Bs[p][kk][nn] = (gk < K && gn < N) ? B[gk * ldb + gn] : 0.0f;
+            }
+        }
+        __syncthreads();
+        const int kmax = static_cast<int>(K - k0 < BK ? K - k0 : BK);
+        for (int kk = 0; kk < kmax; ++kk) {
+            float a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = As[0][kk][ty * TM + i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = Bs[0][kk][tx * TN + j];
+            if constexpr (DUAL) {
+                float a2[TM], b2[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) a2[i] = As[NP - 1][kk][ty * TM + i];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) b2[j] = Bs[NP - 1][kk][tx * TN + j];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        if (tail[j]) {
+                            acc[i][j] = acc[i][j] + __builtin_fmaf(a[i], b[j], a2[i] * b2[j]);
+                        } else {
+                            const float t = __builtin_fmaf(a[i], b[j], acc[i][j]);
+                            acc[i][j] = __builtin_fmaf(a2[i], b2[j], t);
+                        }
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int64_t gm = m0 + ty * TM + i;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int64_t gn = n0 + tx * TN + j;
+            if (gn < N) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM: 128x128 workgroup tile, 2x2 wavefronts of 64x64, BK = 16.
+// Lane (q = lane/16, r = lane%16) feeds k = 4q + s at MFMA step s (the same
+// permutation for A and B, so the products pair up), which lets each lane
+// read its four k values of a row as one 128-bit LDS load.
+// ---------------------------------------------------------------------------
+constexpr int kMBM = 128, kMBN = 128, kMBK = 16, kMLD = kMBK + 4;
+
+__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) float As[kMBM][kMLD];
+    __shared__ __attribute__((aligned(16))) float Bs[kMBN][kMLD];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int q = lane >> 4, r = lane & 15;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kMBM;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kMBN;
+    const int64_t M = g.m, N = g.n;
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nseg = g.a2 ? 2 : 1;
+    for (int seg = 0; seg < nseg; ++seg) {
+        const float* A = seg ? g.a2 : g.a1;
+        const float* B = seg ? g.b2 : g.b1;
+        const int64_t lda = seg ? g.lda2 : g.lda1;
+        const int64_t ldb = seg ? g.ldb2 : g.ldb1;
+        const int64_t K = seg ? g.k2 : g.k1;
+        for (int64_t k0 = 0; k0 < K; k0 += kMBK) {
+            {
+                const int mr = threadIdx.x >> 1, kc = (threadIdx.x & 1) * 8;
+                const int64_t gm = m0 + mr;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int64_t gk = k0 + kc + u;
+                    As[mr][kc + u] = (gm < M && gk < K) ? A[gm * lda + gk] : 0.0f;
+                }
+            }
+            {
+                const int kr = threadIdx.x >> 4, nc = (threadIdx.x & 15) * 8;
+                const int64_t gk = k0 + kr;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int64_t gn = n0 + nc + u;
+                    Bs[nc + u][kr] = (gk < K && gn < N) ? B[gk * ldb + gn] : 0.0f;
+                }
+            }
+            __syncthreads();
+            v4f a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4f*>(&As[wm + i * 16 + r][4 * q]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4f*>(&Bs[wn + j * 16 + r][4 * q]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s],
+                                                                         acc[i][j], 0, 0, 0);
+            __syncthreads();
+        }
+    }
+    // D layout of 16x16x4 f32: lane holds rows 4q..4q+3 of column r.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t gn = n0 + wn + j * 16 + r;
+            if (gn >= N) continue;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t gm = m0 + wm + i * 16 + 4 * q + rr;
+                if (gm < M) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j][rr], g.bias, gn, g.epi);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Elementwise and row epilogues
+// ---------------------------------------------------------------------------
+enum { OP_RELU = 0, OP_LEAKY = 1, OP_ELU = 2, OP_SIGMOID = 3, OP_TANH = 4, OP_GELU = 5 };
+
+template <int OP>
+__device__ __forceinline__ float unary(float x, float alpha) {
+    if constexpr (OP == OP_RELU) return (0.0f < x) ? x : 0.0f;
+    if constexpr (OP == OP_LEAKY) return x >= 0.0f ? x : alpha * x;
+    if constexpr (OP == OP_ELU) return x < 0.0f ? alpha * (expf(x) - 1.0f) : x;
+    if constexpr (OP == OP_SIGMOID) {
+        if (x >= 0.0f) return 1.0f / (1.0f + expf(-x));
+        const float ex = expf(x);
+        return ex / (1.0f + ex);
+    }
+    if constexpr (OP == OP_TANH) return tanhf(x);
+    if constexpr (OP == OP_GELU) {
+        // (0.5 x)(1 + tanh(c0 (x + c1 x^3))), the cube term fused as the
+        // reference build contracts it: fma((c1 x) x, x, x).
+        const float inner = 0.7978845608f * __builtin_fmaf((0.044715f * x) * x, x, x);
+        return (0.5f * x) * (1.0f + tanhf(inner));
+    }
+    return x;
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void unary_kernel(float* __restrict__ x, int64_t n, float alpha) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        x[i] = unary<OP>(x[i], alpha);
+}
+
+__global__ __launch_bounds__(256) void bias_act_kernel(float* __restrict__ x, int64_t rows,
+                                                       int64_t cols, int64_t ld,
+                                                       const float* __restrict__ bias, int act,
+                                                       int post) {
+    const int64_t n = rows * cols;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < n;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t i = t / cols, j = t % cols;
+        float v = x[i * ld + j];
+        if (bias) v = v + bias[j];
+        if (act == TG_ACT_RELU) v = (0.0f < v) ? v : 0.0f;
+        if (post == TG_POST_RELU) {
+            v = (0.0f < v) ? v : 0.0f;
+        } else if (post == TG_POST_ELU) {
+            if (v < 0.0f) v = 1.0f * (expf(v) - 1.0f);
+        }
+        x[i * ld + j] = v;
+    }
+}
+
+// One thread per row; the reference's sequential order (ops.cpp:520-606).
+template <bool LOG>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float* __restrict__ x, int64_t rows,
+                                                           int64_t cols) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows) return;
+    float* row = x + i * cols;
+    float mx = row[0];
+    for (int64_t j = 1; j < cols; ++j)
+        if (row[j] > mx) mx = row[j];
+    float s = 0.0f;
+    if constexpr (LOG) {
+        for (int64_t j = 0; j < cols; ++j) s += expf(row[j] - mx);
+        const float lse = mx + logf(s);
+        for (int64_t j = 0; j < cols; ++j) row[j] -= lse;
+    } else {
+        for (int64_t j = 0; j < cols; ++j) {
+            const float e = expf(row[j] - mx);
+            row[j] = e;
+            s += e;
+        }
+        const float inv = 1.0f / s;
+        for (int64_t j = 0; j < cols; ++j) row[j] *= inv;
+    }
+}
+
+// edge_softmax (layers.cpp:768-822): one thread per row, sequential.
+__global__ __launch_bounds__(256) void edge_softmax_kernel(const int32_t* __restrict__ rp,
+                                                           int64_t n,
+                                                           const float* __restrict__ v,
+                                                           float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int b = rp[i], e = rp[i + 1];
+    if (b == e) return;
+    float mx = v[b];
+    for (int nz = b + 1; nz < e; ++nz) mx = (mx < v[nz]) ? v[nz] : mx;
+    float s = 0.0f;
+    for (int nz = b; nz < e; ++nz) {
+        const float t = expf(v[nz] - mx);
+        out[nz] = t;
+        s += t;
+    }
+    if (s > 0.0f) {
+        const float inv = 1.0f / s;
+        for (int nz = b; nz < e; ++nz) out[nz] *= inv;
+    }
+}
+
+unsigned ew_grid(int64_t n) {
+    int64_t b = ceil_div(n, 256);
+    if (b < 1) b = 1;
+    if (b > 16384) b = 16384;
+    return static_cast<unsigned>(b);
+}
+
+template <int BM, int BN, int TM, int TN, bool DUAL>
+void launch_inorder(const GemmArgs& g, hipStream_t s) {
+    dim3 grid(static_cast<unsigned>(ceil_div(g.m, BM)), static_cast<unsigned>(ceil_div(g.n, BN)));
+    gemm_inorder_kernel<BM, BN, TM, TN, DUAL><<<grid, 256, 0, s>>>(g);
+    TG_LAUNCH_CHECK();
+}
+
+template <bool DUAL>
+void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
+    if (g.n > 32) return launch_inorder<64, 64, 4, 4, DUAL>(g, s);
+    if (g.n > 16) return launch_inorder<128, 32, 4, 4, DUAL>(g, s);
+    if (g.n > 8 || DUAL) return launch_inorder<256, 16, 4, 4, DUAL>(g, s);
+    return launch_inorder<256, 8, 4, 2, DUAL>(g, s);
+}
+
+void unary_launch(int op, float* x, int64_t n, float alpha, hipStream_t s) {
+    if (n <= 0) return;
+    require(x != nullptr, "activation: x is null");
+    switch (op) {
+        case OP_RELU: unary_kernel<OP_RELU><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        case OP_LEAKY: unary_kernel<OP_LEAKY><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        case OP_ELU: unary_kernel<OP_ELU><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        case OP_SIGMOID: unary_kernel<OP_SIGMOID><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        case OP_TANH: unary_kernel<OP_TANH><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        case OP_GELU: unary_kernel<OP_GELU><<<ew_grid(n), 256, 0, s>>>(x, n, alpha); break;
+        default: throw std::logic_error("unary op");
+    }
+    TG_LAUNCH_CHECK();
+}
+
+void softmax_launch(bool log, int64_t rows, int64_t cols, float* x, hipStream_t s) {
+    const char* fn = log ? "log_softmax_inplace" : "softmax_inplace";
+    require(rows >= 0 && cols >= 0, std::string(fn) + ": negative size");
+    if (cols == 0)
+        throw std::invalid_argument(std::string(fn) + ": tensor has 0 columns — " +
+                                    (log ? "log-softmax" : "softmax") +
+                                    " over an empty set is undefined.");
+    if (rows == 0) return;
+    require(x != nullptr, std::string(fn) + ": x is null");
+    const unsigned blocks = static_cast<unsigned>(ceil_div(rows, 256));
+    if (log)
+        softmax_rows_kernel<true><<<blocks, 256, 0, s>>>(x, rows, cols);
+    else
+        softmax_rows_kernel<false><<<blocks, 256, 0, s>>>(x, rows, cols);
+    TG_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+int resolve_gemm_algo(int algo, int64_t m, int64_t n, int64_t k) {
+    // MFMA only where the product is a real contraction (wide n, deep k and
+    // enough work to fill the chip); small products keep the bit-exact
+    // in-order kernel.
+    if (algo == TG_GEMM_AUTO)
+        return (n >= 64 && k >= 32 && m * n * k >= (int64_t(1) << 32)) ? TG_GEMM_MFMA
+                                                                        : TG_GEMM_INORDER;
+    return algo;
+}
+
+void gemm(const GemmArgs& g, int algo, hipStream_t s) {
+    require(g.m >= 0 && g.n >= 0 && g.k1 >= 0 && g.k2 >= 0, "matmul: negative dimension");
+    require(g.epi == TG_EPI_NONE || g.epi == TG_EPI_RELU || g.epi == TG_EPI_ELU,
+            "matmul: unknown epilogue");
+    require(algo == TG_GEMM_AUTO || algo == TG_GEMM_INORDER || algo == TG_GEMM_MFMA,
+            "matmul: unknown algorithm");
+    if (g.m == 0 || g.n == 0) return;
+    require(g.c != nullptr && g.ldc >= g.n, "matmul: bad output");
+    require(g.k1 == 0 || (g.a1 && g.b1 && g.lda1 >= g.k1 && g.ldb1 >= g.n),
+            "matmul: bad first operand pair");
+    const bool dual = g.a2 != nullptr;
+    if (dual)
+        require(g.b2 && g.lda2 >= g.k2 && g.ldb2 >= g.n, "matmul: bad second operand pair");
+    algo = resolve_gemm_algo(algo, g.m, g.n, g.k1 + g.k2);
+    if (algo == TG_GEMM_MFMA) {
+        dim3 grid(static_cast<unsigned>(ceil_div(g.m, kMBM)),
+                  static_cast<unsigned>(ceil_div(g.n, kMBN)));
+        gemm_mfma_kernel<<<grid, 256, 0, s>>>(g);
+        TG_LAUNCH_CHECK();
+        return;
+    }
+    if (dual) {
+        require(g.k1 == g.k2, "matmul: the in-order dual product needs equal k");
+        return dispatch_inorder<true>(g, s);
+    }
+    dispatch_inorder<false>(g, s);
+}
+
+void add_bias_act(float* x, int64_t rows, int64_t cols, int64_t ld, const float* bias, int act,
+                  int post, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return;
+    if (!bias && act == TG_ACT_NONE && post == TG_POST_NONE) return;
+    bias_act_kernel<<<ew_grid(rows * cols), 256, 0, s>>>(x, rows, cols, ld, bias, act, post);
+    TG_LAUNCH_CHECK();
+}
+
+void log_softmax_rows(float* x, int64_t rows, int64_t cols, hipStream_t s) {
+    softmax_launch(true, rows, cols, x, s);
+}
+
+}  // namespace tg
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+using tg::guard;
+using tg::require;
+
+extern "C" {
+
+int tg_matmul(int64_t m, int64_t k, int64_t n, const float* a, int64_t lda, const float* b,
+              int64_t ldb, float* c, int64_t ldc, const float* bias, int epilogue, int algo,
+              tg_stream_t stream) {
+    return guard([&] {
+        tg::GemmArgs g;
+        g.m = m;
+        g.n = n;
+        g.k1 = k;
+        g.a1 = a;
+        g.lda1 = lda;
+        g.b1 = b;
+        g.ldb1 = ldb;
+        g.c = c;
+        g.ldc = ldc;
+        g.bias = bias;
+        g.epi = epilogue;
+        tg::gemm(g, algo, static_cast<hipStream_t>(stream));
+    });
+}
+
+int tg_relu(int64_t n, float* x, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_RELU, x, n, 0.0f, static_cast<hipStream_t>(stream)); });
+}
+int tg_leaky_relu(int64_t n, float* x, float alpha, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_LEAKY, x, n, alpha, static_cast<hipStream_t>(stream)); });
+}
+int tg_elu(int64_t n, float* x, float alpha, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_ELU, x, n, alpha, static_cast<hipStream_t>(stream)); });
+}
+int tg_sigmoid(int64_t n, float* x, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_SIGMOID, x, n, 0.0f, static_cast<hipStream_t>(stream)); });
+}
+int tg_tanh(int64_t n, float* x, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_TANH, x, n, 0.0f, static_cast<hipStream_t>(stream)); });
+}
+int tg_gelu(int64_t n, float* x, tg_stream_t stream) {
+    return guard([&] { tg::unary_launch(tg::OP_GELU, x, n, 0.0f, static_cast<hipStream_t>(stream)); });
+}
+int tg_softmax(int64_t rows, int64_t cols, float* x, tg_stream_t stream) {
+    return guard([&] { tg::softmax_launch(false, rows, cols, x, static_cast<hipStream_t>(stream)); });
+}
+int tg_log_softmax(int64_t rows, int64_t cols, float* x, tg_stream_t stream) {
+    return guard([&] { tg::softmax_launch(true, rows, cols, x, static_cast<hipStream_t>(stream)); });
+}
+int tg_add_bias(int64_t rows, int64_t cols, float* x, const float* bias, tg_stream_t stream) {
+    return guard([&] {
+        require(rows >= 0 && cols >= 0, "add_bias: negative size");
+        require(rows * cols == 0 || (x && bias), "add_bias: null pointer");
+        tg::add_bias_act(x, rows, cols, cols, bias, TG_ACT_NONE, TG_POST_NONE,
+                         static_cast<hipStream_t>(stream));
+    });
+}
+
+int tg_edge_softmax(int64_t n_rows, const int32_t* row_ptr, const float* val, float* val_out,
+                    tg_stream_t stream) {
+    return guard([&] {
+        require(n_rows >= 0, "edge_softmax: negative size");
+        if (n_rows == 0) return;
+        require(row_ptr && val && val_out, "edge_softmax: null pointer");
+        tg::edge_softmax_kernel<<<static_cast<unsigned>(tg::ceil_div(n_rows, 256)), 256, 0,
+                                  static_cast<hipStream_t>(stream)>>>(row_ptr, n_rows, val,
+                                                                       val_out);
+        TG_LAUNCH_CHECK();
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,490 @@
+// gat.hip -- multi-head GAT on gfx950.
+//
+// Replaces GATLayer::forward (reference src/layers.cpp:945-1129) run once
+// per head, and Model's head concat / average (src/model.cpp:312-354,
+// :403-421), for all heads of a layer at once:
+//   * Wh = H * [W_0 | W_1 | ...] is one GEMM (the caller's);
+//   * gat_scores: src[i,h] = a_l(h).Wh_i(h), dst[i,h] = a_r(h).Wh_i(h) in
+//     the reference's operation order (8 interleaved fma partial sums, then
+//     the lane sum, then the tail; layers.cpp:991-1026);
+//   * gat_chunk_kernel, one pass per row chunk of the degree-binned plan:
+//     the lane group computes, per head, e_ij = LeakyReLU(src_i + dst_j),
+//     the row max and the sum of exp(e - max) with wavefront max/sum
+//     reductions, then walks the chunk again accumulating
+//     alpha_ij * Wh_j(h) with alpha = exp(e - max) * (1/sum) -- the
+//     reference's alpha -- into the lanes' feature registers.  The
+//     nnz x heads attention matrix is never stored.  Bias, the layer
+//     activation and the model's post activation are applied on store.
+//   * rows longer than one chunk: every chunk stores its unnormalised sum
+//     with its own (max, sum); gat_reduce_kernel merges them in chunk order
+//     (max of maxima, sums rescaled by exp(m_c - M)).
+#include "common.hpp"
+#include "device_utils.hpp"
+#include "spmm_plan.hpp"
+
+#include <string>
+
+namespace tg {
+namespace {
+
+template <int VEC>
+struct VecT;
+template <>
+struct VecT<1> { using T = float; };
+template <>
+struct VecT<2> { using T = float2; };
+template <>
+struct VecT<4> { using T = float4; };
+
+template <int VEC>
+__device__ __forceinline__ void ldv(const float* p, float (&x)[VEC]) {
+    typename VecT<VEC>::T t = *reinterpret_cast<const typename VecT<VEC>::T*>(p);
+    const float* q = reinterpret_cast<const float*>(&t);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) x[k] = q[k];
+}
+
+template <int VEC>
+__device__ __forceinline__ void stv(float* p, const float (&x)[VEC]) {
+    typename VecT<VEC>::T t;
+    float* q = reinterpret_cast<float*>(&t);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) q[k] = x[k];
+    *reinterpret_cast<typename VecT<VEC>::T*>(p) = t;
+}
+
+__device__ __forceinline__ float lrelu(float e, float slope) { return (e >= 0.0f) ? e : slope * e; }
+
+__device__ __forceinline__ float finish_val(float x, const float* bias, int64_t fo, int act,
+                                            int post) {
+    if (bias) x = x + bias[fo];
+    if (act == TG_ACT_RELU) x = (0.0f < x) ? x : 0.0f;
+    if (post == TG_POST_RELU) {
+        x = (0.0f < x) ? x : 0.0f;
+    } else if (post == TG_POST_ELU) {
+        if (x < 0.0f) x = 1.0f * (expf(x) - 1.0f);
+    }
+    return x;
+}
+
+__global__ __launch_bounds__(256) void gat_scores_kernel(int64_t n, int heads, int f,
+                                                         const float* __restrict__ wh,
+                                                         int64_t ldwh,
+                                                         const float* __restrict__ al,
+                                                         const float* __restrict__ ar,
+                                                         float* __restrict__ src,
+                                                         float* __restrict__ dst) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * heads) return;
+    const int64_t i = t / heads;
+    const int h = static_cast<int>(t % heads);
+    const float* w = wh + i * ldwh + static_cast<int64_t>(h) * f;
+    const float* a = al + static_cast<int64_t>(h) * f;
+    const float* b = ar + static_cast<int64_t>(h) * f;
+    const int f8 = (f / 8) * 8;
+    float ls[8], ld[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) ls[l] = ld[l] = 0.0f;
+    for (int q = 0; q < f8; q += 8) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float x = w[q + l];
+            ls[l] = __builtin_fmaf(a[q + l], x, ls[l]);
+            ld[l] = __builtin_fmaf(b[q + l], x, ld[l]);
+        }
+    }
+    float s = 0.0f, d = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        s = s + ls[l];
+        d = d + ld[l];
+    }
+    // Tail: groups of four as separate multiply and add, the rest fused
+    // (the operation sequence of the reference's compiled scalar tail).
+    const int t4 = f8 + ((f - f8) / 4) * 4;
+    for (int q = f8; q < t4; ++q) {
+        s = s + a[q] * w[q];
+        d = d + b[q] * w[q];
+    }
+    for (int q = t4; q < f; ++q) {
+        s = __builtin_fmaf(a[q], w[q], s);
+        d = __builtin_fmaf(b[q], w[q], d);
+    }
+    src[t] = s;
+    dst[t] = d;
+}
+
+struct GatArgs {
+    const int4* chunks;
+    int64_t n_chunks;
+    const int4* split;
+    int64_t n_split;
+    const int32_t* ci;
+    const float* wh;
+    int64_t ldwh;
+    const float* src;  // [n x heads]
+    const float* dst;  // [n x heads]
+    int heads;
+    int f;             // per-head width
+    int64_t ftot;      // heads * f
+    float slope;
+    float* out;
+    int64_t ldo;
+    float* partials;   // [n_partials x ftot]
+    float* pstats;     // [n_partials x heads x 2] (max, sum)
+    const float* bias;
+    int act;
+    int post;
+};
+
+template <int VEC, int LPR, int VPL>
+__global__ __launch_bounds__(256) void gat_chunk_kernel(GatArgs a) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int U = VPL == 1 ? 4 : 2;
+    constexpr int TILE = LPR * VPL * VEC;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (cid >= a.n_chunks) return;
+    const int4 ch = a.chunks[cid];
+    const int row = ch.x, b = ch.y, e = ch.z;
+    const bool split = ch.w >= 0;
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+    const int H = a.heads;
+    const float* srow = a.src + static_cast<int64_t>(row) * H;
+
+    int64_t fo[VPL];
+    bool ok[VPL];
+    int hv[VPL];
+    float mv[VPL], iv[VPL], si[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
+        ok[v] = fo[v] < a.ftot;
+        hv[v] = ok[v] ? static_cast<int>(fo[v] / a.f) : 0;
+        si[v] = srow[hv[v]];
+        mv[v] = 0.0f;
+        iv[v] = 0.0f;
+    }
+
+    // Per-head softmax statistics over the chunk: lanes split the edges,
+    // the group reduces.  Every lane ends with its own heads' (max, 1/sum).
+    for (int h = 0; h < H; ++h) {
+        const float s_i = srow[h];
+        float m = -INFINITY;
+        for (int nz = b + l; nz < e; nz += LPR) {
+            const float x = lrelu(s_i + a.dst[static_cast<int64_t>(a.ci[nz]) * H + h], a.slope);
+            m = (m < x) ? x : m;
+        }
+#pragma unroll
+        for (int d = LPR / 2; d > 0; d >>= 1) {
+            const float o = __shfl_xor(m, d, LPR);
+            m = (m < o) ? o : m;
+        }
+        float s = 0.0f;
+        for (int nz = b + l; nz < e; nz += LPR) {
+            const float x = lrelu(s_i + a.dst[static_cast<int64_t>(a.ci[nz]) * H + h], a.slope);
+            s += expf(x - m);
+        }
+#pragma unroll
+        for (int d = LPR / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, LPR);
+        // unsplit rows: alpha = exp(e - max) * (1/sum) (layers.cpp:1084-1087);
+        // split chunks keep exp(e - max_c) and report (max_c, sum_c).
+        const float inv = split ? 1.0f : ((s > 0.0f) ? 1.0f / s : 0.0f);
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            if (hv[v] == h) {
+                mv[v] = m;
+                iv[v] = inv;
+            }
+        if (split && l == 0 && blockIdx.y == 0) {
+            float* st = a.pstats + (static_cast<int64_t>(ch.w) * H + h) * 2;
+            st[0] = m;
+            st[1] = s;
+        }
+    }
+
+    float acc[VPL][VEC];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+
+    int nz = b;
+    for (; nz + U <= e; nz += U) {
+        int col[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) col[u] = a.ci[nz + u];
+        float w[U][VPL][VEC];
+        float dj[U][VPL];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float* wr = a.wh + static_cast<int64_t>(col[u]) * a.ldwh;
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+                dj[u][v] = a.dst[static_cast<int64_t>(col[u]) * H + hv[v]];
+                if (ok[v]) {
+                    ldv<VEC>(wr + fo[v], w[u][v]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) w[u][v][k] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < VPL; ++v) {
+                const float alpha = expf(lrelu(si[v] + dj[u][v], a.slope) - mv[v]) * iv[v];
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) acc[v][k] = __builtin_fmaf(alpha, w[u][v][k], acc[v][k]);
+            }
+    }
+    for (; nz < e; ++nz) {
+        const int col = a.ci[nz];
+        const float* wr = a.wh + static_cast<int64_t>(col) * a.ldwh;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+            if (!ok[v]) continue;
+            const float alpha =
+                expf(lrelu(si[v] + a.dst[static_cast<int64_t>(col) * H + hv[v]], a.slope) - mv[v]) *
+                iv[v];
+            float t[VEC];
+            ldv<VEC>(wr + fo[v], t);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) acc[v][k] = __builtin_fmaf(alpha, t[k], acc[v][k]);
+        }
+    }
+
+    if (split) {
+        float* prow = a.partials + static_cast<int64_t>(ch.w) * a.ftot;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+            if (ok[v]) stv<VEC>(prow + fo[v], acc[v]);
+        return;
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        if (!ok[v]) continue;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+            acc[v][k] = finish_val(acc[v][k], a.bias, fo[v] + k, a.act, a.post);
+        stv<VEC>(a.out + static_cast<int64_t>(row) * a.ldo + fo[v], acc[v]);
+    }
+}
+
+template <int VEC, int LPR, int VPL>
+__global__ __launch_bounds__(256) void gat_reduce_kernel(GatArgs a) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int TILE = LPR * VPL * VEC;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t sid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (sid >= a.n_split) return;
+    const int4 sp = a.split[sid];
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+    const int H = a.heads;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        const int64_t fo = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
+        if (fo >= a.ftot) continue;
+        const int h = static_cast<int>(fo / a.f);
+        float M = -INFINITY;
+        for (int c = 0; c < sp.z; ++c) {
+            const float m = a.pstats[(static_cast<int64_t>(sp.y + c) * H + h) * 2];
+            M = (M < m) ? m : M;
+        }
+        float S = 0.0f;
+        float acc[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+        for (int c = 0; c < sp.z; ++c) {
+            const float* st = a.pstats + (static_cast<int64_t>(sp.y + c) * H + h) * 2;
+            const float sc = expf(st[0] - M);
+            S = __builtin_fmaf(st[1], sc, S);
+            float t[VEC];
+            ldv<VEC>(a.partials + static_cast<int64_t>(sp.y + c) * a.ftot + fo, t);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) acc[k] = __builtin_fmaf(t[k], sc, acc[k]);
+        }
+        const float inv = (S > 0.0f) ? 1.0f / S : 0.0f;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] = finish_val(acc[k] * inv, a.bias, fo + k, a.act, a.post);
+        stv<VEC>(a.out + static_cast<int64_t>(sp.x) * a.ldo + fo, acc);
+    }
+}
+
+// Head average (concat = false): out = (sum over heads in order) * (1/heads),
+// then the post activation (model.cpp:335-354, :426-435).
+__global__ __launch_bounds__(256) void gat_average_kernel(const float* __restrict__ x,
+                                                          int64_t n, int heads, int f,
+                                                          float* __restrict__ out, int64_t ldo,
+                                                          int post) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n * f) return;
+    const int64_t i = t / f, j = t % f;
+    const float* xr = x + i * static_cast<int64_t>(heads) * f;
+    float s = 0.0f;
+    for (int h = 0; h < heads; ++h) s += xr[static_cast<int64_t>(h) * f + j];
+    s *= 1.0f / static_cast<float>(heads);
+    out[i * ldo + j] = finish_val(s, nullptr, 0, TG_ACT_NONE, post);
+}
+
+template <int VEC, int LPR, int VPL>
+void launch_gat(const tg_spmm_plan_s& p, const LaneLayout& L, GatArgs& a, hipStream_t s) {
+    constexpr int GPB = 256 / LPR;
+    if (p.n_chunks > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        gat_chunk_kernel<VEC, LPR, VPL><<<grid, 256, 0, s>>>(a);
+        TG_LAUNCH_CHECK();
+    }
+    if (p.n_split > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        gat_reduce_kernel<VEC, LPR, VPL><<<grid, 256, 0, s>>>(a);
+        TG_LAUNCH_CHECK();
+    }
+}
+
+template <int VEC>
+void dispatch_gat(const tg_spmm_plan_s& p, const LaneLayout& L, GatArgs& a, hipStream_t s) {
+#define TG_GAT_CASE(LPR_, VPL_) \
+    if (L.lpr == LPR_ && L.vpl == VPL_) return launch_gat<VEC, LPR_, VPL_>(p, L, a, s);
+    TG_GAT_CASE(4, 1)
+    TG_GAT_CASE(8, 1)
+    TG_GAT_CASE(16, 1)
+    TG_GAT_CASE(32, 1)
+    TG_GAT_CASE(64, 1)
+    TG_GAT_CASE(64, 2)
+    TG_GAT_CASE(64, 4)
+#undef TG_GAT_CASE
+    throw std::logic_error("gat: no kernel for this lane layout");
+}
+
+size_t gat_ws(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
+    Carver c(nullptr, 0);
+    c.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+    if (!concat && heads > 1) c.take<float>(n * heads * f);
+    return c.bytes();
+}
+
+}  // namespace
+
+void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
+                const float* al, const float* ar, float* src, float* dst, hipStream_t s) {
+    require(n >= 0 && heads >= 1 && f >= 1, "GATLayer: bad sizes");
+    require(ldwh >= heads * f, "GATLayer: Wh leading dimension too small");
+    require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
+    if (n == 0) return;
+    require(wh && al && ar && src && dst, "GATLayer: null pointer");
+    gat_scores_kernel<<<static_cast<unsigned>(ceil_div(n * heads, 256)), 256, 0, s>>>(
+        n, static_cast<int>(heads), static_cast<int>(f), wh, ldwh, al, ar, src, dst);
+    TG_LAUNCH_CHECK();
+}
+
+size_t gat_workspace(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
+    return gat_ws(p, n, heads, f, concat);
+}
+
+void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
+                   const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
+                   const float* dst, float slope, const float* bias, int act, int post,
+                   int concat, float* out, int64_t ldo, void* work, size_t work_bytes,
+                   hipStream_t s) {
+    require(n == p.m, "GATLayer::forward: plan rows differ from n");
+    require(heads >= 1 && f >= 1, "GATLayer: bad sizes");
+    require(act == TG_ACT_NONE || act == TG_ACT_RELU, "GATLayer: unknown activation");
+    require(post >= TG_POST_NONE && post <= TG_POST_ELU, "GATLayer: unknown post activation");
+    const int64_t ftot = heads * f;
+    require(ldwh >= ftot, "GATLayer: Wh leading dimension too small");
+    const bool avg = !concat && heads > 1;
+    require(ldo >= (avg ? f : ftot), "GATLayer: output leading dimension too small");
+    if (n == 0) return;
+    if (p.n_split > 0)
+        require(ftot <= p.max_f, "GATLayer: heads * f exceeds the plan's max_f");
+    DeviceBuffer own;
+    if (work == nullptr) {
+        own.resize(gat_ws(p, n, heads, f, concat));
+        work = own.get();
+        work_bytes = own.size();
+    }
+    Carver c(work, work_bytes);
+    float* pstats = c.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+    float* tmp = avg ? c.take<float>(n * ftot) : nullptr;
+
+    GatArgs a{};
+    a.chunks = p.chunks.as<int4>();
+    a.n_chunks = p.n_chunks;
+    a.split = p.split.as<int4>();
+    a.n_split = p.n_split;
+    a.ci = ci;
+    a.wh = wh;
+    a.ldwh = ldwh;
+    a.src = src;
+    a.dst = dst;
+    a.heads = static_cast<int>(heads);
+    a.f = static_cast<int>(f);
+    a.ftot = ftot;
+    a.slope = slope;
+    a.out = avg ? tmp : out;
+    a.ldo = avg ? ftot : ldo;
+    a.partials = p.partials.as<float>();
+    a.pstats = pstats;
+    a.bias = bias;
+    a.act = act;
+    a.post = avg ? TG_POST_NONE : post;
+    // Vectors never straddle heads: the access width divides f.
+    const int vec = pick_vec(ftot, {f, ldwh, a.ldo}, {wh, a.out});
+    const LaneLayout L = choose_layout(ftot, vec);
+    if (vec == 4)
+        dispatch_gat<4>(p, L, a, s);
+    else if (vec == 2)
+        dispatch_gat<2>(p, L, a, s);
+    else
+        dispatch_gat<1>(p, L, a, s);
+    if (avg) {
+        gat_average_kernel<<<static_cast<unsigned>(ceil_div(n * f, 256)), 256, 0, s>>>(
+            tmp, n, static_cast<int>(heads), static_cast<int>(f), out, ldo, post);
+        TG_LAUNCH_CHECK();
+    }
+    if (own.get()) TG_HIP(hipStreamSynchronize(s));
+}
+
+}  // namespace tg
+
+using tg::guard;
+using tg::require;
+
+extern "C" {
+
+int tg_gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
+                  const float* att_l, const float* att_r, float* src, float* dst,
+                  tg_stream_t stream) {
+    return guard([&] {
+        tg::gat_scores(n, heads, f, wh, ldwh, att_l, att_r, src, dst,
+                       static_cast<hipStream_t>(stream));
+    });
+}
+
+size_t tg_gat_workspace_size(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
+                             int concat) {
+    if (plan == nullptr || heads < 1 || f < 1 || n < 0) return 0;
+    return tg::gat_workspace(*plan, n, heads, f, concat);
+}
+
+int tg_gat_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
+                     const int32_t* row_ptr, const int32_t* col_ind, const float* wh,
+                     int64_t ldwh, const float* src, const float* dst, float slope,
+                     const float* bias, int act, int post, int concat, float* out, int64_t ldo,
+                     void* workspace, size_t workspace_bytes, tg_stream_t stream) {
+    return guard([&] {
+        require(plan != nullptr, "GATLayer::forward: plan is null");
+        require(row_ptr == plan->row_ptr, "GATLayer::forward: row_ptr differs from the plan's");
+        tg::gat_aggregate(*plan, n, heads, f, col_ind, wh, ldwh, src, dst, slope, bias, act, post,
+                          concat, out, ldo, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,49 @@
+// layers.hpp -- library-internal entry points of the graph, SAGE and GAT
+// modules, used by the C-ABI wrappers and by the Model.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "spmm_plan.hpp"
+
+namespace tg {
+
+// graph.hip
+void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
+                      int32_t* row_ptr, int32_t* col_ind, float* val, void* workspace,
+                      size_t ws_bytes, hipStream_t s);
+size_t edge_list_to_csr_ws(int64_t n_nodes);
+void csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz, const int32_t* row_ptr,
+                  const int32_t* col_ind, hipStream_t s);
+void add_self_loops(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
+                    const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
+                    void* ws, size_t ws_bytes, hipStream_t s);
+void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
+              const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
+              float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s);
+size_t self_loops_workspace(int64_t n);
+
+// sage.hip
+void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* ci,
+                    const float* h, int64_t ldh, float* out, int64_t ldo, hipStream_t s);
+size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
+                       int64_t nnz);
+void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
+                  const int32_t* ci, const float* h, const float* wn, const float* ws,
+                  const float* bias, int act, int post, int dataflow, float* out, void* work,
+                  size_t work_bytes, hipStream_t s);
+
+// gat.hip
+void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
+                const float* al, const float* ar, float* src, float* dst, hipStream_t s);
+size_t gat_workspace(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat);
+void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
+                   const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
+                   const float* dst, float slope, const float* bias, int act, int post,
+                   int concat, float* out, int64_t ldo, void* work, size_t work_bytes,
+                   hipStream_t s);
+
+}  // namespace tg

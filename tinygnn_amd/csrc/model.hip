@@ -1,0 +1,479 @@
+// model.hip -- the sequential GNN execution graph on the device.
+//
+// Replaces tinygnn::Model (reference include/tinygnn/model.hpp:89-164,
+// src/model.cpp:191-439): a registry of GCN / SAGE / GAT layers with the
+// reference's constructor defaults and weight names, load_weights from a
+// set of named tensors, and forward().
+//
+// forward() follows model.cpp:359-439: gcn_norm if any GCN layer,
+// add_self_loops if any GAT layer, layers in order, multi-head GAT concat or
+// average, then the post activation.  Differences of mapping, not of
+// result:
+//   * all heads of a GAT layer run as one GEMM + one fused edge kernel;
+//   * GCN's bias/activation and the post activation are applied in the
+//     aggregation's store;
+//   * GCN and GAT share A + I's structure (gcn_norm's output has the
+//     structure of add_self_loops' output; GAT reads structure only), so when
+//     both are present the self-loop pass runs once;
+//   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
+//     while the adjacency pointers and sizes are unchanged;
+//     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
+#include "aggregate.hpp"
+#include "common.hpp"
+#include "dense.hpp"
+#include "layers.hpp"
+#include "spmm_plan.hpp"
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace {
+
+using tg::DeviceBuffer;
+using tg::require;
+
+struct HostTensor {
+    int64_t rows = 0, cols = 0;
+    std::vector<float> data;
+};
+
+enum class LType { GCN, SAGE, GAT };
+
+struct Layer {
+    LType type;
+    int64_t in = 0, out = 0, heads = 1;
+    bool concat = true;
+    float slope = 0.2f;
+    bool bias = true;
+    int act = TG_ACT_RELU;
+    int post = TG_POST_NONE;
+    int agg = TG_AGG_MEAN;
+    DeviceBuffer w;       // GCN [in x out]; GAT [in x heads*out] (head-major columns)
+    DeviceBuffer wn, ws;  // SAGE [in x out]
+    DeviceBuffer b;       // [heads*out]
+    DeviceBuffer al, ar;  // GAT [heads*out]
+
+    int64_t out_cols() const { return type == LType::GAT && concat ? heads * out : out; }
+    int64_t wide() const { return type == LType::GAT ? heads * out : out; }
+};
+
+void upload(DeviceBuffer& d, const std::vector<float>& h) {
+    d.resize(h.size() * sizeof(float));
+    if (!h.empty())
+        TG_HIP(hipMemcpy(d.get(), h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
+}
+
+std::string shape(int64_t r, int64_t c) {
+    return "(" + std::to_string(r) + "\xC3\x97" + std::to_string(c) + ")";
+}
+
+}  // namespace
+
+struct tg_model_s {
+    std::vector<Layer> layers;
+    std::map<std::string, HostTensor> staged;
+    int sage_dataflow = TG_SAGE_AUTO;
+
+    // adjacency-derived state
+    bool have_cache = false;
+    const int32_t* key_rp = nullptr;
+    const int32_t* key_ci = nullptr;
+    const float* key_v = nullptr;
+    int64_t key_n = -1, key_nnz = -1;
+    DeviceBuffer sl_rp, sl_ci, sl_v;  // A + I (normalised values when GCN is present)
+    std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
+
+    // per-forward buffers
+    DeviceBuffer act[2], tmp, scores, work;
+
+    bool need_norm() const {
+        for (auto& l : layers) if (l.type == LType::GCN) return true;
+        return false;
+    }
+    bool need_sl() const {
+        for (auto& l : layers) if (l.type == LType::GAT) return true;
+        return false;
+    }
+    bool need_raw() const {
+        for (auto& l : layers) if (l.type == LType::SAGE) return true;
+        return false;
+    }
+    int64_t max_wide() const {
+        int64_t m = 1;
+        for (auto& l : layers) m = std::max({m, l.wide(), l.in, l.out_cols()});
+        return m;
+    }
+};
+
+namespace tg {
+namespace {
+
+int64_t add_layer(tg_model_s& m, Layer&& l) {
+    const char* name = l.type == LType::GCN ? "GCNLayer" : l.type == LType::SAGE ? "SAGELayer"
+                                                                                 : "GATLayer";
+    if (l.in <= 0) throw std::invalid_argument(std::string(name) + ": in_features must be > 0.");
+    if (l.out <= 0) throw std::invalid_argument(std::string(name) + ": out_features must be > 0.");
+    require(l.heads >= 1, "Model::add_gat_layer: num_heads must be >= 1");
+    require(l.act == TG_ACT_NONE || l.act == TG_ACT_RELU, std::string(name) + ": unknown activation");
+    require(l.post >= TG_POST_NONE && l.post <= TG_POST_ELU, "Model: unknown post activation");
+    require(l.agg == TG_AGG_MEAN || l.agg == TG_AGG_MAX, "SAGELayer: unknown aggregator");
+    // zero-initialised weights, as the reference's layer constructors
+    const int64_t wide = l.type == LType::GAT ? l.heads * l.out : l.out;
+    std::vector<float> zw(static_cast<size_t>(l.in * wide), 0.0f), zb(static_cast<size_t>(wide), 0.0f);
+    if (l.type == LType::SAGE) {
+        upload(l.wn, zw);
+        upload(l.ws, zw);
+    } else {
+        upload(l.w, zw);
+    }
+    upload(l.b, zb);
+    if (l.type == LType::GAT) {
+        upload(l.al, zb);
+        upload(l.ar, zb);
+    }
+    m.layers.push_back(std::move(l));
+    return static_cast<int64_t>(m.layers.size()) - 1;
+}
+
+const HostTensor& get(const tg_model_s& m, const std::string& name) {
+    auto it = m.staged.find(name);
+    if (it == m.staged.end())
+        throw std::runtime_error("Model::load_weights: missing tensor '" + name + "'");
+    return it->second;
+}
+
+void check_shape(const HostTensor& t, int64_t r, int64_t c, const std::string& what) {
+    if (t.rows != r || t.cols != c)
+        throw std::invalid_argument(what + ": expected shape " + shape(r, c) + ", got " +
+                                    shape(t.rows, t.cols) + ".");
+}
+
+void load_weights(tg_model_s& m) {
+    for (size_t li = 0; li < m.layers.size(); ++li) {
+        Layer& l = m.layers[li];
+        const std::string p = "layer" + std::to_string(li);
+        if (l.type == LType::GCN) {
+            const HostTensor& w = get(m, p + ".weight");
+            check_shape(w, l.in, l.out, "GCNLayer::set_weight");
+            upload(l.w, w.data);
+            if (l.bias) {
+                const HostTensor& b = get(m, p + ".bias");
+                check_shape(b, 1, l.out, "GCNLayer::set_bias");
+                upload(l.b, b.data);
+            }
+        } else if (l.type == LType::SAGE) {
+            const HostTensor& wn = get(m, p + ".weight_neigh");
+            check_shape(wn, l.in, l.out, "SAGELayer::set_weight_neigh");
+            const HostTensor& ws = get(m, p + ".weight_self");
+            check_shape(ws, l.in, l.out, "SAGELayer::set_weight_self");
+            upload(l.wn, wn.data);
+            upload(l.ws, ws.data);
+            if (l.bias) {
+                const HostTensor& b = get(m, p + ".bias");
+                check_shape(b, 1, l.out, "SAGELayer::set_bias");
+                upload(l.b, b.data);
+            }
+        } else {
+            const int64_t H = l.heads, F = l.out, wide = H * F;
+            std::vector<float> w(static_cast<size_t>(l.in * wide)), al(wide), ar(wide),
+                b(wide, 0.0f);
+            for (int64_t h = 0; h < H; ++h) {
+                const std::string hp = p + ".head" + std::to_string(h);
+                const HostTensor& wh = get(m, hp + ".weight");
+                check_shape(wh, l.in, F, "GATLayer::set_weight");
+                const HostTensor& a_l = get(m, hp + ".attn_left");
+                check_shape(a_l, 1, F, "GATLayer::set_attn_left");
+                const HostTensor& a_r = get(m, hp + ".attn_right");
+                check_shape(a_r, 1, F, "GATLayer::set_attn_right");
+                for (int64_t r = 0; r < l.in; ++r)
+                    for (int64_t c = 0; c < F; ++c) w[r * wide + h * F + c] = wh.data[r * F + c];
+                for (int64_t c = 0; c < F; ++c) {
+                    al[h * F + c] = a_l.data[c];
+                    ar[h * F + c] = a_r.data[c];
+                }
+                if (l.bias) {
+                    const HostTensor& bb = get(m, hp + ".bias");
+                    check_shape(bb, 1, F, "GATLayer::set_bias");
+                    for (int64_t c = 0; c < F; ++c) b[h * F + c] = bb.data[c];
+                }
+            }
+            upload(l.w, w);
+            upload(l.al, al);
+            upload(l.ar, ar);
+            upload(l.b, b);
+        }
+    }
+}
+
+void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
+                       const int32_t* ci, const float* v, int mode, hipStream_t s) {
+    const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
+                      m.key_n == n && m.key_nnz == nnz;
+    if (mode == TG_FORWARD_CACHED && same) return;
+    m.have_cache = false;
+    const int64_t maxf = m.max_wide();
+    if (m.need_raw()) {
+        m.plan_raw = std::make_unique<tg_spmm_plan_s>();
+        build_plan(*m.plan_raw, n, nnz, rp, maxf, 0, s);
+    } else {
+        m.plan_raw.reset();
+    }
+    if (m.need_norm() || m.need_sl()) {
+        require(nnz + n < (int64_t(1) << 31), "Model::forward: nnz + n must be < 2^31");
+        m.sl_rp.reserve((n + 1) * sizeof(int32_t));
+        m.sl_ci.reserve((nnz + n) * sizeof(int32_t));
+        m.sl_v.reserve((nnz + n) * sizeof(float));
+        m.work.reserve(self_loops_workspace(n));
+        if (m.need_norm())
+            gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                     m.sl_v.as<float>(), nullptr, nullptr, m.work.get(), m.work.size(), s);
+        else
+            add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                           m.sl_v.as<float>(), m.work.get(), m.work.size(), s);
+        m.plan_sl = std::make_unique<tg_spmm_plan_s>();
+        build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, 0, s);
+    } else {
+        m.plan_sl.reset();
+    }
+    m.have_cache = true;
+    m.key_rp = rp;
+    m.key_ci = ci;
+    m.key_v = v;
+    m.key_n = n;
+    m.key_nnz = nnz;
+}
+
+void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int32_t* ci,
+             const float* v, int64_t f_in, const float* x, float* out, int mode, hipStream_t s) {
+    if (m.layers.empty()) throw std::runtime_error("Model::forward: no layers configured.");
+    require(mode == TG_FORWARD_REFERENCE || mode == TG_FORWARD_CACHED,
+            "Model::forward: unknown mode");
+    require(n >= 0 && nnz >= 0 && f_in >= 0, "Model::forward: negative size");
+    require(n < (int64_t(1) << 31) && nnz < (int64_t(1) << 31),
+            "Model::forward: sizes must be < 2^31 (int32 CSR)");
+    // the first layer's own shape check (layers.cpp:302-306, :551-555, :964-968)
+    {
+        const Layer& l0 = m.layers[0];
+        const char* name = l0.type == LType::GCN ? "GCNLayer" : l0.type == LType::SAGE
+                                                                 ? "SAGELayer" : "GATLayer";
+        if (f_in != l0.in)
+            throw std::invalid_argument(std::string(name) + "::forward: H has " +
+                                        std::to_string(f_in) +
+                                        " columns but layer expects in_features=" +
+                                        std::to_string(l0.in) + ".");
+    }
+    for (size_t li = 1; li < m.layers.size(); ++li)
+        if (m.layers[li].in != m.layers[li - 1].out_cols())
+            throw std::invalid_argument("Model::forward: layer " + std::to_string(li) +
+                                        " expects in_features=" +
+                                        std::to_string(m.layers[li].in) + " but layer " +
+                                        std::to_string(li - 1) + " produces " +
+                                        std::to_string(m.layers[li - 1].out_cols()) + ".");
+    if (n == 0) return;
+    require(rp && x && out, "Model::forward: null pointer");
+    require(nnz == 0 || (ci && v), "Model::forward: null pointer");
+
+    prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
+
+    // buffers
+    const int64_t wmax = m.max_wide();
+    int64_t heads_max = 1;
+    size_t ws = 0;
+    for (auto& l : m.layers) {
+        heads_max = std::max(heads_max, l.heads);
+        if (l.type == LType::SAGE)
+            ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, m.sage_dataflow, nnz));
+        if (l.type == LType::GAT)
+            ws = std::max(ws, gat_workspace(*m.plan_sl, n, l.heads, l.out, l.concat));
+    }
+    m.act[0].reserve(n * wmax * sizeof(float));
+    m.act[1].reserve(n * wmax * sizeof(float));
+    m.tmp.reserve(n * wmax * sizeof(float));
+    m.scores.reserve(2 * n * heads_max * sizeof(float) + 256);
+    m.work.reserve(ws);
+
+    const float* h = x;
+    for (size_t li = 0; li < m.layers.size(); ++li) {
+        const Layer& l = m.layers[li];
+        const bool last = li + 1 == m.layers.size();
+        float* y = last ? out : m.act[li % 2].as<float>();
+        if (l.type == LType::GCN) {
+            // H*W, then A_norm * (H*W) + b -> act -> post  (layers.cpp:319-336)
+            float* hw = m.tmp.as<float>();
+            GemmArgs g;
+            g.m = n;
+            g.n = l.out;
+            g.a1 = h;
+            g.lda1 = l.in;
+            g.b1 = l.w.as<float>();
+            g.ldb1 = l.out;
+            g.k1 = l.in;
+            g.c = hw;
+            g.ldc = l.out;
+            gemm(g, TG_GEMM_AUTO, s);
+            AggEpilogue epi;
+            epi.bias = l.bias ? l.b.as<float>() : nullptr;
+            epi.act = l.act;
+            epi.post = l.post;
+            run_aggregate(*m.plan_sl, l.out, m.sl_ci.as<int32_t>(), m.sl_v.as<float>(), hw, l.out,
+                          y, l.out, epi, s);
+        } else if (l.type == LType::SAGE) {
+            sage_forward(*m.plan_raw, n, l.in, l.out, l.agg, ci, h, l.wn.as<float>(),
+                         l.ws.as<float>(), l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
+                         m.sage_dataflow, y, m.work.get(), m.work.size(), s);
+        } else {
+            const int64_t wide = l.heads * l.out;
+            float* wh = m.tmp.as<float>();
+            GemmArgs g;
+            g.m = n;
+            g.n = wide;
+            g.a1 = h;
+            g.lda1 = l.in;
+            g.b1 = l.w.as<float>();
+            g.ldb1 = wide;
+            g.k1 = l.in;
+            g.c = wh;
+            g.ldc = wide;
+            gemm(g, TG_GEMM_AUTO, s);
+            float* src = m.scores.as<float>();
+            float* dst = src + n * l.heads;
+            gat_scores(n, l.heads, l.out, wh, wide, l.al.as<float>(), l.ar.as<float>(), src, dst,
+                       s);
+            gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, wide, src,
+                          dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
+                          l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s);
+        }
+        h = y;
+    }
+}
+
+}  // namespace
+}  // namespace tg
+
+using tg::guard;
+using tg::require;
+
+extern "C" {
+
+int tg_model_create(tg_model_t* model_out) {
+    return guard([&] {
+        require(model_out != nullptr, "tg_model_create: model_out is null");
+        *model_out = new tg_model_s();
+    });
+}
+
+int tg_model_destroy(tg_model_t model) {
+    return guard([&] { delete model; });
+}
+
+int tg_model_add_gcn_layer(tg_model_t model, int64_t in_f, int64_t out_f, int bias, int act,
+                           int post, int64_t* index_out) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        Layer l;
+        l.type = LType::GCN;
+        l.in = in_f;
+        l.out = out_f;
+        l.bias = bias != 0;
+        l.act = act;
+        l.post = post;
+        const int64_t i = tg::add_layer(*model, std::move(l));
+        if (index_out) *index_out = i;
+    });
+}
+
+int tg_model_add_sage_layer(tg_model_t model, int64_t in_f, int64_t out_f, int agg, int bias,
+                            int act, int post, int64_t* index_out) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        Layer l;
+        l.type = LType::SAGE;
+        l.in = in_f;
+        l.out = out_f;
+        l.agg = agg;
+        l.bias = bias != 0;
+        l.act = act;
+        l.post = post;
+        const int64_t i = tg::add_layer(*model, std::move(l));
+        if (index_out) *index_out = i;
+    });
+}
+
+int tg_model_add_gat_layer(tg_model_t model, int64_t in_f, int64_t out_f, int64_t heads,
+                           int concat, float neg_slope, int bias, int act, int post,
+                           int64_t* index_out) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        Layer l;
+        l.type = LType::GAT;
+        l.in = in_f;
+        l.out = out_f;
+        l.heads = heads;
+        l.concat = concat != 0;
+        l.slope = neg_slope;
+        l.bias = bias != 0;
+        l.act = act;
+        l.post = post;
+        const int64_t i = tg::add_layer(*model, std::move(l));
+        if (index_out) *index_out = i;
+    });
+}
+
+int tg_model_num_layers(tg_model_t model, int64_t* n_out) {
+    return guard([&] {
+        require(model != nullptr && n_out != nullptr, "null argument");
+        *n_out = static_cast<int64_t>(model->layers.size());
+    });
+}
+
+int tg_model_output_cols(tg_model_t model, int64_t* cols_out) {
+    return guard([&] {
+        require(model != nullptr && cols_out != nullptr, "null argument");
+        if (model->layers.empty()) throw std::runtime_error("Model::forward: no layers configured.");
+        *cols_out = model->layers.back().out_cols();
+    });
+}
+
+int tg_model_set_tensor(tg_model_t model, const char* name, int64_t rows, int64_t cols,
+                        const float* host_data) {
+    return guard([&] {
+        require(model != nullptr && name != nullptr, "null argument");
+        require(rows >= 0 && cols >= 0, "tg_model_set_tensor: negative shape");
+        require(rows * cols == 0 || host_data != nullptr, "tg_model_set_tensor: data is null");
+        HostTensor t;
+        t.rows = rows;
+        t.cols = cols;
+        t.data.assign(host_data, host_data + rows * cols);
+        model->staged[name] = std::move(t);
+    });
+}
+
+int tg_model_load_weights(tg_model_t model) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        tg::load_weights(*model);
+    });
+}
+
+int tg_model_set_sage_dataflow(tg_model_t model, int dataflow) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        require(dataflow >= TG_SAGE_AUTO && dataflow <= TG_SAGE_TRANSFORM_FIRST,
+                "unknown SAGE dataflow");
+        model->sage_dataflow = dataflow;
+    });
+}
+
+int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz, const int32_t* row_ptr,
+                     const int32_t* col_ind, const float* val, int64_t f_in, const float* x,
+                     float* out, int mode, tg_stream_t stream) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        tg::forward(*model, n, nnz, row_ptr, col_ind, val, f_in, x, out, mode,
+                    static_cast<hipStream_t>(stream));
+    });
+}
+
+}  // extern "C"

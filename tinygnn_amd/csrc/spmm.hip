@@ -279,12 +279,24 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
     store_vec<VEC>(c + static_cast<int64_t>(row) * ldc + fo, x);
 }
 
+enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2 };
+
+// One step of a row's reduction: fma with the edge value (SpMM, ops.cpp:
+// 266-287), a plain add (SAGE mean, layers.cpp:604-620), or the element-wise
+// max written as std::max(acc, x) = (acc < x) ? x : acc (layers.cpp:398-417).
+template <int MODE>
+__device__ __forceinline__ float combine(float acc, float x, float w) {
+    if constexpr (MODE == kAggWeighted) return __builtin_fmaf(w, x, acc);
+    if constexpr (MODE == kAggSum) return acc + x;
+    return (acc < x) ? x : acc;
+}
+
 template <int VPL>
 struct Unroll {
     static constexpr int value = VPL == 1 ? 8 : (VPL == 2 ? 4 : 2);
 };
 
-template <int VEC, int LPR, int VPL, bool HAS_VAL>
+template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256) void agg_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
     const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
@@ -311,7 +323,7 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+        for (int k = 0; k < VEC; ++k) acc[v][k] = MODE == kAggMax ? -INFINITY : 0.0f;
 
     int nz = ch.y;
     const int e = ch.z;
@@ -321,7 +333,7 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             col[u] = ci[nz + u];
-            if constexpr (HAS_VAL) w[u] = av[nz + u];
+            if constexpr (MODE == kAggWeighted) w[u] = av[nz + u];
         }
         float bv[U][VPL][VEC];
 #pragma unroll
@@ -342,17 +354,12 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
 #pragma unroll
             for (int v = 0; v < VPL; ++v)
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) {
-                    if constexpr (HAS_VAL)
-                        acc[v][k] = __builtin_fmaf(w[u], bv[u][v][k], acc[v][k]);
-                    else
-                        acc[v][k] = acc[v][k] + bv[u][v][k];
-                }
+                for (int k = 0; k < VEC; ++k) acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
     }
     for (; nz < e; ++nz) {
         const int col = ci[nz];
         float w = 1.0f;
-        if constexpr (HAS_VAL) w = av[nz];
+        if constexpr (MODE == kAggWeighted) w = av[nz];
         const float* brow = B + static_cast<int64_t>(col) * ldb;
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
@@ -360,17 +367,19 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
                 float t[VEC];
                 load_vec<VEC>(brow + fo[v], t);
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) {
-                    if constexpr (HAS_VAL)
-                        acc[v][k] = __builtin_fmaf(w, t[k], acc[v][k]);
-                    else
-                        acc[v][k] = acc[v][k] + t[k];
-                }
+                for (int k = 0; k < VEC; ++k) acc[v][k] = combine<MODE>(acc[v][k], t[k], w);
             }
         }
     }
 
     if (ch.w < 0) {
+        if (MODE == kAggMax && ch.z == ch.y) {
+            // an empty row aggregates to 0 (layers.cpp:377-380)
+#pragma unroll
+            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+        }
 #pragma unroll
         for (int v = 0; v < VPL; ++v)
             if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], C, ldc, epi);
@@ -382,8 +391,8 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     }
 }
 
-// Finishes split rows: partials of a row are added in chunk order.
-template <int VEC, int LPR, int VPL>
+// Finishes split rows: partials of a row are combined in chunk order.
+template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict__ split,
                                                          int64_t n_split,
                                                          const float* __restrict__ partials,
@@ -408,13 +417,14 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
             float t[VEC];
             load_vec<VEC>(partials + static_cast<int64_t>(sp.y + c) * ldp + fo, t);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) acc[k] = acc[k] + t[k];
+            for (int k = 0; k < VEC; ++k)
+                acc[k] = MODE == kAggMax ? ((acc[k] < t[k]) ? t[k] : acc[k]) : acc[k] + t[k];
         }
         finish_store<VEC>(acc, sp.x, sp.w, fo, C, ldc, epi);
     }
 }
 
-template <int VEC, int LPR, int VPL, bool HAS_VAL>
+template <int VEC, int LPR, int VPL, int MODE>
 void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                 const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
                 const AggEpilogue& epi, hipStream_t s) {
@@ -424,26 +434,26 @@ void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const i
     if (p.n_chunks > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
-        agg_chunk_kernel<VEC, LPR, VPL, HAS_VAL><<<grid, 256, 0, s>>>(
+        agg_chunk_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
             p.chunks.as<int4>(), p.n_chunks, ci, av, B, ldb, C, ldc, partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
     if (p.n_split > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
                   static_cast<unsigned>(L.n_tiles));
-        agg_reduce_kernel<VEC, LPR, VPL><<<grid, 256, 0, s>>>(p.split.as<int4>(), p.n_split,
+        agg_reduce_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(p.split.as<int4>(), p.n_split,
                                                              partials, ldp, C, ldc, f, epi);
         TG_LAUNCH_CHECK();
     }
 }
 
-template <int VEC, bool HAS_VAL>
+template <int VEC, int MODE>
 void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                   const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
                   const AggEpilogue& epi, hipStream_t s) {
 #define TG_AGG_CASE(LPR_, VPL_)                                                          \
     if (L.lpr == LPR_ && L.vpl == VPL_)                                                  \
-        return launch_agg<VEC, LPR_, VPL_, HAS_VAL>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+        return launch_agg<VEC, LPR_, VPL_, MODE>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
     TG_AGG_CASE(4, 1)
     TG_AGG_CASE(8, 1)
     TG_AGG_CASE(16, 1)
@@ -470,14 +480,19 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
     const int vec = pick_vec(f, {ldb, ldc, epi.self ? epi.ld_self : 0},
                              {B, C, epi.self, epi.bias});
     const LaneLayout L = choose_layout(f, vec);
-    if (av) {
-        if (vec == 4) return dispatch_lpr<4, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
-        if (vec == 2) return dispatch_lpr<2, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
-        return dispatch_lpr<1, true>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+#define TG_AGG_MODE(M_)                                                                \
+    if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);    \
+    if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);    \
+    return dispatch_lpr<1, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    if (epi.max) {
+        require(!epi.mean, "aggregate: max and mean are exclusive");
+        TG_AGG_MODE(kAggMax)
     }
-    if (vec == 4) return dispatch_lpr<4, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
-    if (vec == 2) return dispatch_lpr<2, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
-    return dispatch_lpr<1, false>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    if (av) {
+        TG_AGG_MODE(kAggWeighted)
+    }
+    TG_AGG_MODE(kAggSum)
+#undef TG_AGG_MODE
 }
 
 }  // namespace tg
