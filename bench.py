@@ -15,7 +15,15 @@ Default run (N=1):
   * the rest of the sweep (F = 32, 512) as ``sweep``;
   * ``cpu_baseline``: the reference's spmm compiled from its sources
     (oracle/_ref) or, where that library is absent, the oracle restatement,
-    timed on the host cores over a bounded row sample of the same matrix.
+    timed on the host cores over a bounded row sample of the same matrix;
+  * ``forward``: the config-E forwards (232,965 nodes, 114,615,892 edges,
+    602-d features): 2-layer GCN, SAGE-mean and GAT (4 x 64 heads), median
+    ms with cached preprocessing and with the reference's semantics
+    (gcn_norm / add_self_loops inside every forward), the reference's
+    Model::forward timed once on the host cores, and the parity of the
+    log-softmax logits against it (|err| <= 1e-5 + 1e-4|ref|, argmax).
+Graphs are generated on the GPU from seeded power-law degrees and built into
+CSR by the library's own edge_list_to_csr (its time is reported).
 
 ``--gpus N`` with N > 1 exits: this build measures one GPU.
 """
@@ -34,6 +42,23 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+DEFAULT_SEED = 2101
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "spmm_configD_pmc.md")
+
+
+def measured_traffic(f: int, seed: int):
+    """HBM bytes per SpMM launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (copy-kernel calibrated), for the default workload
+    only; None when no profile covers this configuration."""
+    import re
+
+    if seed != DEFAULT_SEED or not os.path.exists(PMC_SUMMARY):
+        return None
+    m = re.search(r'"spmm_configD_traffic_bytes":\s*(\{[^}]*\})', open(PMC_SUMMARY).read())
+    if not m:
+        return None
+    v = json.loads(m.group(1)).get(str(f))
+    return int(v) if v is not None else None
 
 
 def log(msg: str) -> None:
@@ -43,17 +68,6 @@ def log(msg: str) -> None:
 def spmm_bytes(m: int, nnz: int, f: int) -> int:
     """Algorithmic HBM bytes of one SpMM pass (reference ops.cpp:186-191)."""
     return 4 * (m + 1) + 8 * nnz + 4 * f * nnz + 4 * f * m
-
-
-def csr_from_edges_host(src: np.ndarray, dst: np.ndarray, n: int):
-    """edge_list_to_csr semantics (row = src, sorted destinations, duplicates
-    kept) computed with numpy; used only to stage the benchmark input."""
-    key = (src.astype(np.int64) << 32) | dst.astype(np.int64)
-    key.sort()
-    ci = (key & 0xFFFFFFFF).astype(np.int32)
-    rp = np.zeros(n + 1, np.int64)
-    np.cumsum(np.bincount(src, minlength=n), out=rp[1:])
-    return rp.astype(np.int32), ci
 
 
 class StreamTimer:
@@ -78,24 +92,47 @@ class StreamTimer:
         return [a.elapsed_time(b) for a, b in self.pairs]
 
 
+def build_graph_gpu(torch, tg, n, n_edges, seed, dev):
+    """Seeded power-law edge list (degrees on the host, destinations and a
+    random edge order drawn on the GPU), then the device CSR build
+    (edge_list_to_csr).  Returns the device CSR and the build time in ms."""
+    from tinygnn_amd import synth
+
+    deg = synth.powerlaw_degrees(n, n_edges, alpha=2.1, dmax=20000, seed=seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    src = torch.repeat_interleave(torch.arange(n, dtype=torch.int32, device=dev),
+                                  torch.from_numpy(deg.astype(np.int64)).to(dev))
+    dst = torch.randint(0, n - 1, (n_edges,), generator=g, device=dev, dtype=torch.int32)
+    dst += (dst >= src).to(torch.int32)  # no self-loops in the raw graph
+    perm = torch.randperm(n_edges, generator=g, device=dev)
+    src, dst = src[perm].contiguous(), dst[perm].contiguous()
+    del perm
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    a = tg.edge_list_to_csr(src, dst, n)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3
+    del src, dst
+    return a, ms
+
+
 def run_spmm_d(args, torch, tg):
     from tinygnn_amd import synth
 
     t0 = time.time()
-    src, dst = synth.powerlaw_edges(synth.D_NODES, synth.D_EDGES, alpha=2.1, dmax=20000,
-                                    seed=args.seed, shuffle=False)
-    m = synth.D_NODES
-    rp, ci = csr_from_edges_host(src, dst, m)
-    del src, dst
-    nnz = int(rp[-1])
-    rng = np.random.default_rng(args.seed + 2)
-    val = (1.0 - rng.random(nnz, dtype=np.float32)).astype(np.float32)  # (0, 1]
-    deg = np.diff(rp)
-    log(f"config D: m={m} nnz={nnz} max_deg={int(deg.max())} built in {time.time()-t0:.1f}s")
-
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
-    a = tg.DeviceCSR.from_numpy(m, m, rp, ci, val, device=dev)
+    m = synth.D_NODES
+    a, csr_ms = build_graph_gpu(torch, tg, m, synth.D_EDGES, args.seed, dev)
+    nnz = a.nnz
+    gv = torch.Generator(device=dev)
+    gv.manual_seed(args.seed + 2)
+    a.val = 1.0 - torch.rand(nnz, generator=gv, device=dev)  # (0, 1]
+    rp, ci, val = a.to_numpy()
+    deg = np.diff(rp)
+    log(f"config D: m={m} nnz={nnz} max_deg={int(deg.max())} built in {time.time()-t0:.1f}s "
+        f"(device CSR build {csr_ms:.1f} ms)")
     fs = sorted(set(args.f_sweep) | {args.f})
     fmax = max(fs)
     gen = torch.Generator(device=dev)
@@ -150,7 +187,93 @@ def run_spmm_d(args, torch, tg):
         cpu = cpu_baseline_spmm(rp, ci, val, b_full[:, :args.f].contiguous().cpu().numpy(),
                                 args)
     return dict(m=m, nnz=nnz, max_deg=int(deg.max()), plan=info, results=results,
-                head=head, cpu=cpu)
+                head=head, cpu=cpu, csr_build_ms=csr_ms)
+
+
+# Roofline times of the declared dataflows at config E (8 TB/s, 157.3 TF/s):
+# GCN and GAT aggregate at F_out, SAGE runs transform-first.
+FORWARD_ROOFLINE_MS = {"gcn": 17.81, "sage": 18.18, "gat": 17.70}
+
+
+def run_forward_e(args, torch, tg):
+    """2-layer GCN / SAGE-mean / GAT forwards at config E, with the
+    reference's Model::forward timed on the host cores and full-size
+    parity of the logits."""
+    from tinygnn_amd import synth
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    n = synth.E_NODES
+    t0 = time.time()
+    adj, csr_ms = build_graph_gpu(torch, tg, n, synth.E_EDGES, args.seed + 10, dev)
+    rng = np.random.default_rng(args.seed + 11)
+    x_h = rng.standard_normal((n, synth.E_FEATURES), dtype=np.float32)
+    x = torch.from_numpy(x_h).to(dev)
+    log(f"config E: n={n} nnz={adj.nnz} built in {time.time()-t0:.1f}s "
+        f"(device CSR build {csr_ms:.1f} ms)")
+    specs = {"gcn": synth.spec_gcn(synth.E_FEATURES, 256, synth.E_CLASSES),
+             "sage": synth.spec_sage(synth.E_FEATURES, 256, synth.E_CLASSES),
+             "gat": synth.spec_gat(synth.E_FEATURES, 64, 4, synth.E_CLASSES)}
+    ref = ref_tensors = None
+    if not args.no_cpu:
+        import oracle
+        if oracle.has_reference():
+            ref = oracle.reference()
+            rp, ci, val = adj.to_numpy()
+            t1 = time.time()
+            ref_tensors = (ref.csr(oracle.CSR(n, n, rp, ci, val)), ref.dense(x_h))
+            log(f"reference tensors built in {time.time()-t1:.1f}s")
+            del rp, ci, val
+    out = {}
+    for name, spec in specs.items():
+        w = synth.model_weights(spec, seed=args.seed + 20)
+        model = tg.Model.from_spec(spec, w)
+        y = torch.empty((n, model.output_cols()), device=dev)
+        for _ in range(args.fwd_warmup):
+            model.forward(adj, x, mode=tg.FORWARD_CACHED, out=y)
+        torch.cuda.synchronize()
+        timer = StreamTimer(torch, stream)
+        for _ in range(args.fwd_steps):
+            e0 = timer.start()
+            model.forward(adj, x, mode=tg.FORWARD_CACHED, out=y)
+            timer.stop(e0)
+        torch.cuda.synchronize()
+        cached = float(np.median(timer.ms()))
+        timer = StreamTimer(torch, stream)
+        for _ in range(3):
+            torch.cuda.synchronize()
+            e0 = timer.start()
+            model.forward(adj, x, mode=tg.FORWARD_REFERENCE, out=y)
+            timer.stop(e0)
+        torch.cuda.synchronize()
+        refsem = float(np.median(timer.ms()))
+        logits = tg.log_softmax_(y.clone()).cpu().numpy()
+        r = dict(gpu_ms=round(cached, 3), gpu_ms_reference_semantics=round(refsem, 3),
+                 roofline_ms=FORWARD_ROOFLINE_MS[name],
+                 roofline_frac=round(FORWARD_ROOFLINE_MS[name] / cached, 4))
+        log(f"{name}: cached {cached:.2f} ms, reference semantics {refsem:.2f} ms")
+        if ref is not None:
+            rm = ref.model(spec, w)
+            t1 = time.perf_counter()
+            want = rm.forward_handles(ref_tensors[0], ref_tensors[1], n)
+            cpu_ms = (time.perf_counter() - t1) * 1e3
+            want = ref.activation("log_softmax", want)
+            err = np.abs(logits.astype(np.float64) - want)
+            tol = 1e-5 + 1e-4 * np.abs(want.astype(np.float64))
+            top2 = np.sort(want, axis=1)[:, -2:]
+            ties = int(((top2[:, 1] - top2[:, 0]) <= float(err.max())).sum())
+            r.update(cpu_ms=round(cpu_ms, 1), cpu_threads=ref.num_threads(),
+                     speedup=round(cpu_ms / cached, 1),
+                     parity=dict(max_abs_err=float(err.max()),
+                                 within_tol=bool((err <= tol).all()),
+                                 n_out_of_tol=int((err > tol).sum()),
+                                 argmax_mismatch=int((logits.argmax(1) != want.argmax(1)).sum()),
+                                 near_ties=ties))
+            log(f"{name}: cpu {cpu_ms:.0f} ms ({ref.num_threads()} thr), parity {r['parity']}")
+            del rm, want
+        out[name] = r
+        del model, y
+    return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)
 
 
 def cpu_baseline_spmm(rp, ci, val, b, args):
@@ -200,10 +323,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--f", type=int, default=128, help="headline feature width")
     ap.add_argument("--f-sweep", type=int, nargs="*", default=[32, 128, 512])
-    ap.add_argument("--seed", type=int, default=2101)
+    ap.add_argument("--seed", type=int, default=DEFAULT_SEED)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-sample-nnz", type=int, default=10_000_000)
+    ap.add_argument("--no-forward", action="store_true", help="skip the config-E forwards")
+    ap.add_argument("--fwd-steps", type=int, default=10)
+    ap.add_argument("--fwd-warmup", type=int, default=2)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 1 GiB copy kernel (out = x * 1), the reference "
+                         "dispatch for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -220,6 +349,15 @@ def main():
     torch.cuda.set_device(0)
 
     r = run_spmm_d(args, torch, tg)
+    torch.cuda.empty_cache()
+    if args.calib_copy:
+        xc = torch.ones(1 << 28, device="cuda:0")  # 1 GiB read, 1 GiB written
+        yc = torch.empty_like(xc)
+        for _ in range(3):
+            torch.mul(xc, 1.0, out=yc)
+        torch.cuda.synchronize()
+        del xc, yc
+    fwd = None if args.no_forward else run_forward_e(args, torch, tg)
     head = r["head"]
     line = {
         "metric": "CSR SpMM GB/s & % HBM peak; forward ms at 233K nodes / 114.6M edges",
@@ -241,7 +379,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(args.f, args.seed),
+                     "traffic_source": "profiles/spmm_configD_pmc.md (FETCH_SIZE x2 + "
+                                       "WRITE_SIZE x1, copy-kernel calibrated)",
                      "kernel": "spmm pass (agg_chunk_kernel + agg_reduce_kernel)",
                      "kernel_ms_avg": round(head["kernel_ms_avg"], 4),
                      "bytes_per_launch": head["bytes"]},
@@ -250,6 +390,8 @@ def main():
                    "pct_hbm_peak": round(100 * v["kernel_gbs"] / HBM_PEAK_GBS, 2)}
                   for v in r["results"].values()],
         "cpu_baseline": r["cpu"],
+        "csr_build_ms": round(r["csr_build_ms"], 2),
+        "forward": fwd,
     }
     print(json.dumps(line), flush=True)
 
