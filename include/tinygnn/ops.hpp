@@ -1,0 +1,30 @@
+// tinygnn/ops.hpp -- compute kernels of TinyGNN's API (reference
+// include/tinygnn/ops.hpp:76-286), running on the MI355X through the C-ABI
+// in tinygnn_amd.h.  Same names, arguments, results and exceptions.
+#pragma once
+
+#include <cstddef>
+
+#include "tinygnn/tensor.hpp"
+
+namespace tinygnn {
+
+/// C = A * B, both Dense (ops.cpp:70-162).  Small products are bit-identical
+/// to the reference; wide ones (n >= 64, k >= 32, m*n*k >= 2^32) run on fp32
+/// MFMA (within 1e-4 relative).
+Tensor matmul(const Tensor& A, const Tensor& B);
+
+/// C = A * B, A SparseCSR, B Dense (ops.cpp:198-297).
+Tensor spmm(const Tensor& A, const Tensor& B);
+
+void relu_inplace(Tensor& X);
+void leaky_relu_inplace(Tensor& X, float alpha = 0.01f);
+void elu_inplace(Tensor& X, float alpha = 1.0f);
+void sigmoid_inplace(Tensor& X);
+void tanh_inplace(Tensor& X);
+void gelu_inplace(Tensor& X);
+void softmax_inplace(Tensor& X);
+void log_softmax_inplace(Tensor& X);
+void add_bias(Tensor& X, const Tensor& bias);
+
+}  // namespace tinygnn

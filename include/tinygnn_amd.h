@@ -262,6 +262,8 @@ int tg_model_num_layers(tg_model_t model, int64_t* n_out);
 int tg_model_output_cols(tg_model_t model, int64_t* cols_out);
 int tg_model_set_tensor(tg_model_t model, const char* name, int64_t rows,
                         int64_t cols, const float* host_data);
+/* Forgets every staged tensor (a new WeightFile replaces the old one). */
+int tg_model_clear_tensors(tg_model_t model);
 int tg_model_load_weights(tg_model_t model);
 /* SAGE dataflow used by the model's SAGE-mean layers (TG_SAGE_*). */
 int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);

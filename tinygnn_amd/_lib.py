@@ -96,6 +96,7 @@ SIGNATURES = {
     "tg_model_num_layers": (i32, [vp, pi64]),
     "tg_model_output_cols": (i32, [vp, pi64]),
     "tg_model_set_tensor": (i32, [vp, C.c_char_p, i64, i64, vp]),
+    "tg_model_clear_tensors": (i32, [vp]),
     "tg_model_load_weights": (i32, [vp]),
     "tg_model_set_sage_dataflow": (i32, [vp, i32]),
     "tg_model_forward": (i32, [vp, i64, i64, vp, vp, vp, i64, vp, vp, i32, vp]),

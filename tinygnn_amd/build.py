@@ -1,10 +1,13 @@
-"""Builds libtinygnn_amd.so (gfx950) in-tree with hipcc.
+"""Builds the libraries in-tree with hipcc.
 
-Every ``csrc/*.hip`` and ``csrc/*.cpp`` file is compiled to an object under
-``tinygnn_amd/_build/obj`` (in parallel) and linked into
-``tinygnn_amd/_build/libtinygnn_amd.so``.  Device code is compiled for gfx950
-only, with packed-fp32 instructions disabled and floating-point contraction
-off, so that every fused multiply-add in the kernels is an explicit one.
+* ``tinygnn_amd/_build/libtinygnn_amd.so`` -- the C-ABI (include/tinygnn_amd.h):
+  every ``csrc/*.hip`` file compiled to an object under ``_build/obj`` (in
+  parallel).  Device code is compiled for gfx950 only, with packed-fp32
+  instructions disabled and floating-point contraction off, so that every
+  fused multiply-add in the kernels is an explicit one.
+* ``tinygnn_amd/_build/libtinygnn.so`` -- TinyGNN's C++ API
+  (include/tinygnn/*.hpp) over the C-ABI, from ``cpp/*.cpp`` (host code).
+* ``tinygnn_amd/_build/test_cpp_api`` -- the C++ API test (tests/cpp).
 
 Usage: ``python -m tinygnn_amd.build [-j N] [--quiet]``.
 """
@@ -23,6 +26,9 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OBJ = os.path.join(BUILD, "obj")
 LIB = os.path.join(BUILD, "libtinygnn_amd.so")
+CPP = os.path.join(HERE, "cpp")
+API_LIB = os.path.join(BUILD, "libtinygnn.so")
+CPP_TEST = os.path.join(BUILD, "test_cpp_api")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -58,8 +64,36 @@ def _compile(src: str, quiet: bool) -> str:
     return obj
 
 
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def _build_cpp_api() -> None:
+    """The C++ API (include/tinygnn/*.hpp) as libtinygnn.so over the C-ABI
+    library, and the C++ API test binary; host code only."""
+    host = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall", f"-I{os.path.join(ROOT, 'include')}"]
+    api_src = sorted(glob.glob(os.path.join(CPP, "*.cpp")))
+    api_obj = []
+    for s in api_src:
+        o = os.path.join(OBJ, "api_" + os.path.basename(s) + ".o")
+        _run(host + ["-c", s, "-o", o])
+        api_obj.append(o)
+    tmp = API_LIB + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", "-o", tmp] + api_obj +
+         [f"-L{BUILD}", "-ltinygnn_amd", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, API_LIB)
+    test_src = os.path.join(ROOT, "tests", "cpp", "test_api.cpp")
+    tmp = CPP_TEST + ".tmp"
+    _run(host + [test_src, "-o", tmp, f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd",
+                 "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, CPP_TEST)
+
+
 def build(jobs: int | None = None, quiet: bool = True) -> str:
-    """Compiles every source and links the shared library; returns its path."""
+    """Compiles every source and links the shared libraries; returns the
+    C-ABI library's path."""
     os.makedirs(OBJ, exist_ok=True)
     srcs = _sources()
     jobs = jobs or min(8, os.cpu_count() or 4)
@@ -71,6 +105,7 @@ def build(jobs: int | None = None, quiet: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    _build_cpp_api()
     return LIB
 
 

@@ -450,6 +450,13 @@ int tg_model_set_tensor(tg_model_t model, const char* name, int64_t rows, int64_
     });
 }
 
+int tg_model_clear_tensors(tg_model_t model) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        model->staged.clear();
+    });
+}
+
 int tg_model_load_weights(tg_model_t model) {
     return guard([&] {
         require(model != nullptr, "model is null");
