@@ -84,6 +84,26 @@ def test_sage_transform_first(gpu, restate, f_in, f_out):
     assert_close(got, want, what="sage transform-first")
 
 
+def test_sage_concat_mfma_dual(gpu, restate):
+    """Concat dataflow large enough for the MFMA GEMM (m*n*k >= 2^32): the
+    dual product [AGG | H] x [Wn ; Ws] runs as two K segments of one MFMA
+    kernel; within tolerance of the reference."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(21)
+    n, f_in, f_out = 40000, 256, 210
+    a = random_csr(rng, n, n, avg_deg=3, max_deg=50, empty_frac=0.05)
+    h = rng.standard_normal((n, f_in)).astype(np.float32)
+    s = np.float32(1.0 / np.sqrt(f_in))
+    wn = (rng.standard_normal((f_in, f_out)) * s).astype(np.float32)
+    ws = (rng.standard_normal((f_in, f_out)) * s).astype(np.float32)
+    b = rng.standard_normal((1, f_out)).astype(np.float32)
+    want = restate.sage_layer(a, h, wn, ws, b, act=1, agg=0)
+    da = _dev(a)
+    got = tg.sage_forward(_plan(da, f_in), da, _t(gpu, h), _t(gpu, wn), _t(gpu, ws), _t(gpu, b),
+                          act=1, agg=0, dataflow=tg.SAGE_CONCAT).cpu().numpy()
+    assert_close(got, want, what="sage concat (MFMA dual)")
+
+
 @pytest.mark.parametrize("f", [1, 2, 3, 7, 8, 9, 16, 17, 41, 64, 100])
 def test_gat_scores_bitexact(gpu, restate, f):
     import tinygnn_amd as tg

@@ -68,6 +68,31 @@ def _exact_spmm(a, b):
     return exact, absum
 
 
+@pytest.mark.parametrize("f,pad", [(41, 3), (41, 7), (7, 1), (3, 1), (130, 2), (257, 3)])
+@pytest.mark.parametrize("chunk", [4096, 16])
+def test_spmm_padded_rows(gpu, restate, f, pad, chunk):
+    """B with a padded leading dimension (ld = f + pad, a multiple of 4):
+    128-bit gathers read into the row padding (filled with NaN here, which
+    must never reach the output), stores stay within the f columns of a
+    row-major output whose rows are not 16-byte aligned."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(f * 10 + pad + chunk)
+    a = random_csr(rng, 500, 300, avg_deg=10, max_deg=400, empty_frac=0.1)
+    b = rng.standard_normal((300, f)).astype(np.float32)
+    bp = np.full((300, f + pad), np.nan, np.float32)
+    bp[:, :f] = b
+    da = tg.DeviceCSR.from_numpy(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, a.val)
+    dbp = gpu.from_numpy(bp).cuda()
+    p = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, f, chunk)
+    got = tg.spmm(da, dbp[:, :f], plan=p).cpu().numpy()
+    want = restate.spmm(a, b)
+    deg = np.diff(a.row_ptr)
+    single = deg <= chunk
+    assert np.isfinite(got).all()
+    np.testing.assert_array_equal(bits(got[single]), bits(want[single]))
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
 def test_spmm_one_shot_and_empty(gpu, restate):
     rng = np.random.default_rng(3)
     a = random_csr(rng, 300, 200, avg_deg=5, empty_frac=0.3)

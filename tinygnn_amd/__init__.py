@@ -36,17 +36,17 @@ def stream_handle(stream=None) -> int:
 
 
 def dptr(t, dtype=None) -> int:
-    """Device pointer of a contiguous CUDA/HIP torch tensor (0 for None)."""
+    """Device pointer of a CUDA/HIP torch tensor (0 for None): contiguous, or
+    a row-major 2-D view with unit column stride (its row stride is passed as
+    the leading dimension)."""
     if t is None:
         return 0
-    torch = _torch()
     if not t.is_cuda:
         raise ValueError("tinygnn_amd expects device (cuda) tensors")
     if dtype is not None and t.dtype != dtype:
         raise ValueError(f"expected {dtype}, got {t.dtype}")
-    if not t.is_contiguous():
-        raise ValueError("tinygnn_amd expects contiguous tensors")
-    del torch
+    if not (t.is_contiguous() or (t.dim() == 2 and t.stride(1) == 1)):
+        raise ValueError("tinygnn_amd expects contiguous tensors or row-major 2-D views")
     return int(t.data_ptr())
 
 

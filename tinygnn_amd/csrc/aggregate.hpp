@@ -24,6 +24,7 @@ struct AggEpilogue {
     int max = 0;   // element-wise max instead of a sum (SAGE-Max); empty rows give 0
     int act = 0;
     int post = 0;
+    int vec_io = 1;  // set by run_aggregate: stores and epilogue loads are full vectors
 };
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is

@@ -127,16 +127,50 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMM: 128x128 workgroup tile, 2x2 wavefronts of 64x64, BK = 16.
-// Lane (q = lane/16, r = lane%16) feeds k = 4q + s at MFMA step s (the same
-// permutation for A and B, so the products pair up), which lets each lane
-// read its four k values of a row as one 128-bit LDS load.
+// MFMA GEMM: 128x128 workgroup tile, 2x2 wavefronts of 64x64 (4x4 tiles of
+// v_mfma_f32_16x16x4f32), BK = 16, two LDS buffers with register prefetch:
+// the next K tile is loaded from global memory while the current one feeds
+// the MFMAs, so there is one barrier per tile.
+// Lane (q = lane/16, r = lane%16) feeds k = 4q + s at MFMA step s for both
+// operands (the products pair up; only the order of the k sum changes).
+// A is staged as [m][k] so a lane's four k values of a row are one 128-bit
+// LDS read; B stays [k][n] with a 132-float pitch, so the 64 lanes' reads of
+// B[4q+s][n0+r] fall in 64 distinct banks.
 // ---------------------------------------------------------------------------
-constexpr int kMBM = 128, kMBN = 128, kMBK = 16, kMLD = kMBK + 4;
+constexpr int kMBM = 128, kMBN = 128, kMBK = 16;
+constexpr int kMLDA = kMBK + 4;   // A tile pitch (floats): 16-byte aligned rows
+constexpr int kMLDB = kMBN + 4;   // B tile pitch
 
+// Loads 8 consecutive floats p[0..7] of which the first `valid` exist
+// (valid <= 0: none), with V-wide accesses when all 8 exist.
+template <int V>
+__device__ __forceinline__ void load8(const float* __restrict__ p, int64_t valid,
+                                      float (&x)[8]) {
+    if (valid >= 8 && V > 1) {
+#pragma unroll
+        for (int u = 0; u < 8; u += V) {
+            if constexpr (V == 4) {
+                const float4 t = *reinterpret_cast<const float4*>(p + u);
+                x[u] = t.x;
+                x[u + 1] = t.y;
+                x[u + 2] = t.z;
+                x[u + 3] = t.w;
+            } else {
+                const float2 t = *reinterpret_cast<const float2*>(p + u);
+                x[u] = t.x;
+                x[u + 1] = t.y;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = (u < valid) ? p[u] : 0.0f;
+}
+
+template <int VA, int VB>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
-    __shared__ __attribute__((aligned(16))) float As[kMBM][kMLD];
-    __shared__ __attribute__((aligned(16))) float Bs[kMBN][kMLD];
+    __shared__ __attribute__((aligned(16))) float As[2][kMBM][kMLDA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kMBK][kMLDB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -144,6 +178,36 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kMBM;
     const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kMBN;
     const int64_t M = g.m, N = g.n;
+    const int64_t t1 = (g.k1 + kMBK - 1) / kMBK;
+    const int64_t nt = t1 + (g.a2 ? (g.k2 + kMBK - 1) / kMBK : 0);
+
+    // this thread's share of a tile: A row ar (8 k values from ak), B row bk
+    // (8 n values from bn)
+    const int ar = threadIdx.x >> 1, ak = (threadIdx.x & 1) * 8;
+    const int bk = threadIdx.x >> 4, bn = (threadIdx.x & 15) * 8;
+    float ra[8], rb[8];
+
+    auto fetch = [&](int64_t kt) {
+        const bool seg2 = kt >= t1;
+        const float* A = seg2 ? g.a2 : g.a1;
+        const float* B = seg2 ? g.b2 : g.b1;
+        const int64_t lda = seg2 ? g.lda2 : g.lda1;
+        const int64_t ldb = seg2 ? g.ldb2 : g.ldb1;
+        const int64_t K = seg2 ? g.k2 : g.k1;
+        const int64_t k0 = (seg2 ? kt - t1 : kt) * kMBK;
+        const int64_t gm = m0 + ar;
+        const int64_t ka = k0 + ak;
+        load8<VA>(A + (gm < M ? gm : 0) * lda + ka, gm < M ? K - ka : 0, ra);
+        const int64_t kb = k0 + bk;
+        const int64_t nb = n0 + bn;
+        load8<VB>(B + (kb < K ? kb : 0) * ldb + nb, kb < K ? N - nb : 0, rb);
+    };
+    auto stage = [&](int buf) {
+        *reinterpret_cast<float4*>(&As[buf][ar][ak]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
+        *reinterpret_cast<float4*>(&As[buf][ar][ak + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
+        *reinterpret_cast<float4*>(&Bs[buf][bk][bn]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
+        *reinterpret_cast<float4*>(&Bs[buf][bk][bn + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
+    };
 
     v4f acc[4][4];
 #pragma unroll
@@ -151,48 +215,32 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nseg = g.a2 ? 2 : 1;
-    for (int seg = 0; seg < nseg; ++seg) {
-        const float* A = seg ? g.a2 : g.a1;
-        const float* B = seg ? g.b2 : g.b1;
-        const int64_t lda = seg ? g.lda2 : g.lda1;
-        const int64_t ldb = seg ? g.ldb2 : g.ldb1;
-        const int64_t K = seg ? g.k2 : g.k1;
-        for (int64_t k0 = 0; k0 < K; k0 += kMBK) {
-            {
-                const int mr = threadIdx.x >> 1, kc = (threadIdx.x & 1) * 8;
-                const int64_t gm = m0 + mr;
+    if (nt > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        const int cb = static_cast<int>(kt & 1);
+        if (kt + 1 < nt) fetch(kt + 1);
+        v4f a[4];
+        float b[4][4];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int64_t gk = k0 + kc + u;
-                    As[mr][kc + u] = (gm < M && gk < K) ? A[gm * lda + gk] : 0.0f;
-                }
-            }
-            {
-                const int kr = threadIdx.x >> 4, nc = (threadIdx.x & 15) * 8;
-                const int64_t gk = k0 + kr;
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4f*>(&As[cb][wm + i * 16 + r][4 * q]);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int64_t gn = n0 + nc + u;
-                    Bs[nc + u][kr] = (gk < K && gn < N) ? B[gk * ldb + gn] : 0.0f;
-                }
-            }
-            __syncthreads();
-            v4f a[4], b[4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4f*>(&As[wm + i * 16 + r][4 * q]);
+            for (int s = 0; s < 4; ++s) b[j][s] = Bs[cb][4 * q + s][wn + j * 16 + r];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4f*>(&Bs[wn + j * 16 + r][4 * q]);
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s],
-                                                                         acc[i][j], 0, 0, 0);
-            __syncthreads();
-        }
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j],
+                                                                     0, 0, 0);
+        if (kt + 1 < nt) stage(cb ^ 1);
+        __syncthreads();
     }
     // D layout of 16x16x4 f32: lane holds rows 4q..4q+3 of column r.
 #pragma unroll
@@ -393,9 +441,25 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
     if (algo == TG_GEMM_MFMA) {
         dim3 grid(static_cast<unsigned>(ceil_div(g.m, kMBM)),
                   static_cast<unsigned>(ceil_div(g.n, kMBN)));
-        gemm_mfma_kernel<<<grid, 256, 0, s>>>(g);
-        TG_LAUNCH_CHECK();
-        return;
+        auto width = [](std::initializer_list<int64_t> lds, std::initializer_list<const void*> ps) {
+            for (int v : {4, 2}) {
+                bool ok = true;
+                for (int64_t ld : lds) ok = ok && ld % v == 0;
+                for (const void* p : ps)
+                    ok = ok && reinterpret_cast<uintptr_t>(p) % (sizeof(float) * v) == 0;
+                if (ok) return v;
+            }
+            return 1;
+        };
+        const int va = dual ? width({g.lda1, g.lda2}, {g.a1, g.a2}) : width({g.lda1}, {g.a1});
+        const int vb = dual ? width({g.ldb1, g.ldb2}, {g.b1, g.b2}) : width({g.ldb1}, {g.b1});
+#define TG_MFMA_CASE(A_, B_) \
+        if (va == A_ && vb == B_) { gemm_mfma_kernel<A_, B_><<<grid, 256, 0, s>>>(g); TG_LAUNCH_CHECK(); return; }
+        TG_MFMA_CASE(4, 4) TG_MFMA_CASE(4, 2) TG_MFMA_CASE(4, 1)
+        TG_MFMA_CASE(2, 4) TG_MFMA_CASE(2, 2) TG_MFMA_CASE(2, 1)
+        TG_MFMA_CASE(1, 4) TG_MFMA_CASE(1, 2) TG_MFMA_CASE(1, 1)
+#undef TG_MFMA_CASE
+        throw std::logic_error("matmul: no MFMA kernel for this access width");
     }
     if (dual) {
         require(g.k1 == g.k2, "matmul: the in-order dual product needs equal k");

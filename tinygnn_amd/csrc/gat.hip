@@ -8,12 +8,13 @@
 //     the reference's operation order (8 interleaved fma partial sums, then
 //     the lane sum, then the tail; layers.cpp:991-1026);
 //   * gat_chunk_kernel, one pass per row chunk of the degree-binned plan:
-//     the lane group computes, per head, e_ij = LeakyReLU(src_i + dst_j),
-//     the row max and the sum of exp(e - max) with wavefront max/sum
-//     reductions, then walks the chunk again accumulating
-//     alpha_ij * Wh_j(h) with alpha = exp(e - max) * (1/sum) -- the
-//     reference's alpha -- into the lanes' feature registers.  The
-//     nnz x heads attention matrix is never stored.  Bias, the layer
+//     each lane scores e_ij = LeakyReLU(src_i + dst_j) for the head of its
+//     feature vector and keeps an online softmax -- running max, running
+//     sum of exp(e - max), and the accumulated exp(e - max) * Wh_j(h),
+//     rescaled when the max grows -- so the row is read once; the store
+//     multiplies by 1/sum, giving the reference's
+//     out_i = sum_j exp(e_ij - max) (1/sum) Wh_j (layers.cpp:1076-1109).
+//     The nnz x heads attention matrix is never stored.  Bias, the layer
 //     activation and the model's post activation are applied on store.
 //   * rows longer than one chunk: every chunk stores its unnormalised sum
 //     with its own (max, sum); gat_reduce_kernel merges them in chunk order
@@ -130,17 +131,36 @@ struct GatArgs {
     float slope;
     float* out;
     int64_t ldo;
-    float* partials;   // [n_partials x ftot]
+    float* partials;   // [n_partials x ldp]
+    int64_t ldp;       // ftot rounded up to the access width
     float* pstats;     // [n_partials x heads x 2] (max, sum)
     const float* bias;
     int act;
     int post;
+    int vec_io;        // stores and bias loads are full, aligned vectors
 };
+
+// Applies the epilogue and stores one lane vector of row `row`.
+template <int VEC>
+__device__ __forceinline__ void gat_store(const GatArgs& a, int64_t row, int64_t fo,
+                                          float (&x)[VEC], float scale) {
+    if (a.vec_io) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) x[k] = finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post);
+        stv<VEC>(a.out + row * a.ldo + fo, x);
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        if (fo + k >= a.ftot) break;
+        a.out[row * a.ldo + fo + k] = finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post);
+    }
+}
 
 template <int VEC, int LPR, int VPL>
 __global__ __launch_bounds__(256) void gat_chunk_kernel(GatArgs a) {
     constexpr int GPB = 256 / LPR;
-    constexpr int U = VPL == 1 ? 4 : 2;
+    constexpr int U = VPL <= 2 ? 8 : 4;  // gathers in flight per lane
     constexpr int TILE = LPR * VPL * VEC;
     const int g = threadIdx.x / LPR;
     const int l = threadIdx.x % LPR;
@@ -156,120 +176,113 @@ __global__ __launch_bounds__(256) void gat_chunk_kernel(GatArgs a) {
     int64_t fo[VPL];
     bool ok[VPL];
     int hv[VPL];
-    float mv[VPL], iv[VPL], si[VPL];
+    float si[VPL];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
         fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
         ok[v] = fo[v] < a.ftot;
         hv[v] = ok[v] ? static_cast<int>(fo[v] / a.f) : 0;
         si[v] = srow[hv[v]];
-        mv[v] = 0.0f;
-        iv[v] = 0.0f;
     }
 
-    // Per-head softmax statistics over the chunk: lanes split the edges,
-    // the group reduces.  Every lane ends with its own heads' (max, 1/sum).
-    for (int h = 0; h < H; ++h) {
-        const float s_i = srow[h];
-        float m = -INFINITY;
-        for (int nz = b + l; nz < e; nz += LPR) {
-            const float x = lrelu(s_i + a.dst[static_cast<int64_t>(a.ci[nz]) * H + h], a.slope);
-            m = (m < x) ? x : m;
-        }
+    // One pass with an online softmax per lane vector (its head): running
+    // max m, running sum s of exp(e - m), and acc = sum exp(e - m) Wh_j; a
+    // larger max rescales s and acc by exp(m_old - m_new) (exactly 1 when
+    // the max is unchanged, 0 from the initial -inf).  Lanes of one head see
+    // the same scores, so their (m, s) agree.
+    float m[VPL], s[VPL], acc[VPL][VEC];
 #pragma unroll
-        for (int d = LPR / 2; d > 0; d >>= 1) {
-            const float o = __shfl_xor(m, d, LPR);
-            m = (m < o) ? o : m;
-        }
-        float s = 0.0f;
-        for (int nz = b + l; nz < e; nz += LPR) {
-            const float x = lrelu(s_i + a.dst[static_cast<int64_t>(a.ci[nz]) * H + h], a.slope);
-            s += expf(x - m);
-        }
-#pragma unroll
-        for (int d = LPR / 2; d > 0; d >>= 1) s += __shfl_xor(s, d, LPR);
-        // unsplit rows: alpha = exp(e - max) * (1/sum) (layers.cpp:1084-1087);
-        // split chunks keep exp(e - max_c) and report (max_c, sum_c).
-        const float inv = split ? 1.0f : ((s > 0.0f) ? 1.0f / s : 0.0f);
-#pragma unroll
-        for (int v = 0; v < VPL; ++v)
-            if (hv[v] == h) {
-                mv[v] = m;
-                iv[v] = inv;
-            }
-        if (split && l == 0 && blockIdx.y == 0) {
-            float* st = a.pstats + (static_cast<int64_t>(ch.w) * H + h) * 2;
-            st[0] = m;
-            st[1] = s;
-        }
-    }
-
-    float acc[VPL][VEC];
-#pragma unroll
-    for (int v = 0; v < VPL; ++v)
+    for (int v = 0; v < VPL; ++v) {
+        m[v] = -INFINITY;
+        s[v] = 0.0f;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+    }
 
-    int nz = b;
-    for (; nz + U <= e; nz += U) {
-        int col[U];
+    // Batches of BE entries: each lane loads CPL consecutive column indices
+    // with one coalesced access, the group broadcasts them with shuffles,
+    // and U gathers are in flight per step (slots past the chunk's end read
+    // row 0 and are not accumulated).
+    constexpr int CPL = U > LPR ? U / LPR : 1;
+    constexpr int BE = LPR * CPL;
+    for (int base = b; base < e; base += BE) {
+        int cl[CPL];
 #pragma unroll
-        for (int u = 0; u < U; ++u) col[u] = a.ci[nz + u];
-        float w[U][VPL][VEC];
-        float dj[U][VPL];
+        for (int j = 0; j < CPL; ++j) {
+            const int idx = base + l * CPL + j;
+            cl[j] = idx < e ? a.ci[idx] : 0;
+        }
+        const int cnt = e - base < BE ? e - base : BE;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float* wr = a.wh + static_cast<int64_t>(col[u]) * a.ldwh;
+        for (int s0 = 0; s0 < BE; s0 += U) {
+          if (s0 < cnt) {  // uniform across the group: no early exit in the unrolled body
+            const int nv = cnt - s0 < U ? cnt - s0 : U;  // valid slots of this step
+            int col[U];
 #pragma unroll
-            for (int v = 0; v < VPL; ++v) {
-                dj[u][v] = a.dst[static_cast<int64_t>(col[u]) * H + hv[v]];
-                if (ok[v]) {
-                    ldv<VEC>(wr + fo[v], w[u][v]);
-                } else {
+            for (int u = 0; u < U; ++u) col[u] = __shfl(cl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+            float w[U][VPL][VEC];
+            float ev[U][VPL];
 #pragma unroll
-                    for (int k = 0; k < VEC; ++k) w[u][v][k] = 0.0f;
+            for (int u = 0; u < U; ++u) {
+                const float* wr = a.wh + static_cast<int64_t>(col[u]) * a.ldwh;
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) {
+                    ev[u][v] = a.dst[static_cast<int64_t>(col[u]) * H + hv[v]];
+                    // lanes past ftot load the row's first vector, never stored
+                    ldv<VEC>(wr + (ok[v] ? fo[v] : 0), w[u][v]);
                 }
             }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int v = 0; v < VPL; ++v) {
-                const float alpha = expf(lrelu(si[v] + dj[u][v], a.slope) - mv[v]) * iv[v];
+                float mn = m[v];
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) acc[v][k] = __builtin_fmaf(alpha, w[u][v][k], acc[v][k]);
+                for (int u = 0; u < U; ++u) {
+                    ev[u][v] = lrelu(si[v] + ev[u][v], a.slope);
+                    if (u < nv) mn = (mn < ev[u][v]) ? ev[u][v] : mn;
+                }
+                const float sc = expf(m[v] - mn);
+                m[v] = mn;
+                s[v] *= sc;
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) acc[v][k] *= sc;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const bool valid = u < nv;  // a select, not a branch
+                    const float p = expf(ev[u][v] - mn);
+                    s[v] = valid ? s[v] + p : s[v];
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) {
+                        const float nx = __builtin_fmaf(p, w[u][v][k], acc[v][k]);
+                        acc[v][k] = valid ? nx : acc[v][k];
+                    }
+                }
             }
-    }
-    for (; nz < e; ++nz) {
-        const int col = a.ci[nz];
-        const float* wr = a.wh + static_cast<int64_t>(col) * a.ldwh;
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-            if (!ok[v]) continue;
-            const float alpha =
-                expf(lrelu(si[v] + a.dst[static_cast<int64_t>(col) * H + hv[v]], a.slope) - mv[v]) *
-                iv[v];
-            float t[VEC];
-            ldv<VEC>(wr + fo[v], t);
-#pragma unroll
-            for (int k = 0; k < VEC; ++k) acc[v][k] = __builtin_fmaf(alpha, t[k], acc[v][k]);
+          }
         }
     }
 
     if (split) {
-        float* prow = a.partials + static_cast<int64_t>(ch.w) * a.ftot;
+        // the chunk's (max, sum) per head, written by the lane that owns the
+        // head's first feature
+        float* prow = a.partials + static_cast<int64_t>(ch.w) * a.ldp;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v)
-            if (ok[v]) stv<VEC>(prow + fo[v], acc[v]);
+        for (int v = 0; v < VPL; ++v) {
+            if (!ok[v]) continue;
+            stv<VEC>(prow + fo[v], acc[v]);
+            if (fo[v] % a.f == 0) {
+                float* st = a.pstats + (static_cast<int64_t>(ch.w) * H + hv[v]) * 2;
+                st[0] = m[v];
+                st[1] = s[v];
+            }
+        }
         return;
     }
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
         if (!ok[v]) continue;
-#pragma unroll
-        for (int k = 0; k < VEC; ++k)
-            acc[v][k] = finish_val(acc[v][k], a.bias, fo[v] + k, a.act, a.post);
-        stv<VEC>(a.out + static_cast<int64_t>(row) * a.ldo + fo[v], acc[v]);
+        // empty rows: s = 0 gives 0 before the bias (layers.cpp:1059)
+        const float inv = (s[v] > 0.0f) ? 1.0f / s[v] : 0.0f;
+        gat_store<VEC>(a, row, fo[v], acc[v], inv);
     }
 }
 
@@ -303,14 +316,12 @@ __global__ __launch_bounds__(256) void gat_reduce_kernel(GatArgs a) {
             const float sc = expf(st[0] - M);
             S = __builtin_fmaf(st[1], sc, S);
             float t[VEC];
-            ldv<VEC>(a.partials + static_cast<int64_t>(sp.y + c) * a.ftot + fo, t);
+            ldv<VEC>(a.partials + static_cast<int64_t>(sp.y + c) * a.ldp + fo, t);
 #pragma unroll
             for (int k = 0; k < VEC; ++k) acc[k] = __builtin_fmaf(t[k], sc, acc[k]);
         }
         const float inv = (S > 0.0f) ? 1.0f / S : 0.0f;
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) acc[k] = finish_val(acc[k] * inv, a.bias, fo + k, a.act, a.post);
-        stv<VEC>(a.out + static_cast<int64_t>(sp.x) * a.ldo + fo, acc);
+        gat_store<VEC>(a, sp.x, fo, acc, inv);
     }
 }
 
@@ -434,8 +445,13 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
     a.bias = bias;
     a.act = act;
     a.post = avg ? TG_POST_NONE : post;
-    // Vectors never straddle heads: the access width divides f.
-    const int vec = pick_vec(ftot, {f, ldwh, a.ldo}, {wh, a.out});
+    // Loads: the widest access the rows of Wh allow, never straddling two
+    // heads (the width divides f, or there is one head); stores and bias
+    // loads are vectors only when aligned as well.
+    int vec = pick_load_vec(ftot, ldwh, wh);
+    while (vec > 1 && heads > 1 && f % vec != 0) vec /= 2;
+    a.ldp = round_up(ftot, vec);
+    a.vec_io = pick_vec(ftot, {a.ldo}, {a.out, bias}) >= vec;
     const LaneLayout L = choose_layout(ftot, vec);
     if (vec == 4)
         dispatch_gat<4>(p, L, a, s);

@@ -61,17 +61,29 @@ __global__ __launch_bounds__(256) void edge_count_kernel(const int32_t* __restri
 
 // Sorts rows into length classes: 0 = 2..64, 1 = 65..1024, 2 = 1025..16384,
 // 3 = longer.  counts[c] ends as the class size.
+// Positions are reserved per workgroup (LDS counts, one global atomic per
+// class and workgroup), so the global counters see n/256 atomics, not n.
 __global__ __launch_bounds__(256) void classify_rows_kernel(const int32_t* __restrict__ deg,
                                                             int64_t n,
                                                             int32_t* __restrict__ lists,
                                                             int32_t* __restrict__ counts) {
+    __shared__ int lcount[4], lbase[4];
+    if (threadIdx.x < 4) lcount[threadIdx.x] = 0;
+    __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (r >= n) return;
-    const int d = deg[r];
-    if (d < 2) return;
-    const int c = d <= kSortWaveMax ? 0 : d <= kSortBlockMax ? 1 : d <= kSortBigMax ? 2 : 3;
-    const int pos = atomicAdd(&counts[c], 1);
-    lists[static_cast<int64_t>(c) * n + pos] = static_cast<int32_t>(r);
+    int c = -1, lpos = 0;
+    if (r < n) {
+        const int d = deg[r];
+        if (d >= 2) {
+            c = d <= kSortWaveMax ? 0 : d <= kSortBlockMax ? 1 : d <= kSortBigMax ? 2 : 3;
+            lpos = atomicAdd(&lcount[c], 1);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 && lcount[threadIdx.x] > 0)
+        lbase[threadIdx.x] = atomicAdd(&counts[threadIdx.x], lcount[threadIdx.x]);
+    __syncthreads();
+    if (c >= 0) lists[static_cast<int64_t>(c) * n + lbase[c] + lpos] = static_cast<int32_t>(r);
 }
 
 __global__ __launch_bounds__(256) void edge_scatter_kernel(const int32_t* __restrict__ src,

@@ -290,7 +290,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     }
     m.act[0].reserve(n * wmax * sizeof(float));
     m.act[1].reserve(n * wmax * sizeof(float));
-    m.tmp.reserve(n * wmax * sizeof(float));
+    m.tmp.reserve(n * gather_pitch(wmax) * sizeof(float));
     m.scores.reserve(2 * n * heads_max * sizeof(float) + 256);
     m.work.reserve(ws);
 
@@ -300,8 +300,10 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
         const bool last = li + 1 == m.layers.size();
         float* y = last ? out : m.act[li % 2].as<float>();
         if (l.type == LType::GCN) {
-            // H*W, then A_norm * (H*W) + b -> act -> post  (layers.cpp:319-336)
+            // H*W, then A_norm * (H*W) + b -> act -> post  (layers.cpp:319-336);
+            // H*W's rows are padded (gather_pitch) for 128-bit, line-aligned gathers
             float* hw = m.tmp.as<float>();
+            const int64_t ldhw = gather_pitch(l.out);
             GemmArgs g;
             g.m = n;
             g.n = l.out;
@@ -311,13 +313,13 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             g.ldb1 = l.out;
             g.k1 = l.in;
             g.c = hw;
-            g.ldc = l.out;
+            g.ldc = ldhw;
             gemm(g, TG_GEMM_AUTO, s);
             AggEpilogue epi;
             epi.bias = l.bias ? l.b.as<float>() : nullptr;
             epi.act = l.act;
             epi.post = l.post;
-            run_aggregate(*m.plan_sl, l.out, m.sl_ci.as<int32_t>(), m.sl_v.as<float>(), hw, l.out,
+            run_aggregate(*m.plan_sl, l.out, m.sl_ci.as<int32_t>(), m.sl_v.as<float>(), hw, ldhw,
                           y, l.out, epi, s);
         } else if (l.type == LType::SAGE) {
             sage_forward(*m.plan_raw, n, l.in, l.out, l.agg, ci, h, l.wn.as<float>(),
@@ -325,6 +327,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
                          m.sage_dataflow, y, m.work.get(), m.work.size(), s);
         } else {
             const int64_t wide = l.heads * l.out;
+            const int64_t ldwh = gather_pitch(wide);  // line-aligned rows for the gathers
             float* wh = m.tmp.as<float>();
             GemmArgs g;
             g.m = n;
@@ -335,13 +338,13 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             g.ldb1 = wide;
             g.k1 = l.in;
             g.c = wh;
-            g.ldc = wide;
+            g.ldc = ldwh;
             gemm(g, TG_GEMM_AUTO, s);
             float* src = m.scores.as<float>();
             float* dst = src + n * l.heads;
-            gat_scores(n, l.heads, l.out, wh, wide, l.al.as<float>(), l.ar.as<float>(), src, dst,
+            gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
                        s);
-            gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, wide, src,
+            gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh, src,
                           dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
                           l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s);
         }

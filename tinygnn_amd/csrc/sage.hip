@@ -31,8 +31,9 @@ int resolve_dataflow(int dataflow, int agg, int64_t f_in, int64_t f_out, int64_t
 size_t sage_ws(int64_t n, int64_t f_in, int64_t f_out, int dataflow) {
     Carver c(nullptr, 0);
     if (dataflow == TG_SAGE_TRANSFORM_FIRST) {
-        c.take<float>(n * 2 * f_out);
-        c.take<float>(f_in * 2 * f_out);
+        const int64_t fp = gather_pitch(f_out);
+        c.take<float>(n * 2 * fp);
+        c.take<float>(f_in * 2 * fp);
     } else {
         c.take<float>(n * f_in);
     }
@@ -101,33 +102,37 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         gemm(g, TG_GEMM_AUTO, s);
         add_bias_act(out, n, f_out, f_out, nullptr, TG_ACT_NONE, post, s);
     } else {
-        float* t = c.take<float>(n * 2 * f_out);
-        float* wcat = c.take<float>(f_in * 2 * f_out);
-        // [Ws | Wn]: self half first, neighbour half second
-        TG_HIP(hipMemcpy2DAsync(wcat, 2 * f_out * sizeof(float), ws, f_out * sizeof(float),
+        // [Ws | 0 | Wn | 0]: each half padded to fp = gather_pitch(f_out)
+        // columns, so the neighbour half's rows start line-aligned and are
+        // gathered with 128-bit loads; the zero columns make the GEMM write
+        // zeros into the padding.
+        const int64_t fp = gather_pitch(f_out);
+        float* t = c.take<float>(n * 2 * fp);
+        float* wcat = c.take<float>(f_in * 2 * fp);
+        if (fp != f_out) fill_zero_2d(wcat, f_in, 2 * fp, 2 * fp, s);
+        TG_HIP(hipMemcpy2DAsync(wcat, 2 * fp * sizeof(float), ws, f_out * sizeof(float),
                                 f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
-        TG_HIP(hipMemcpy2DAsync(wcat + f_out, 2 * f_out * sizeof(float), wn,
-                                f_out * sizeof(float), f_out * sizeof(float), f_in,
-                                hipMemcpyDeviceToDevice, s));
+        TG_HIP(hipMemcpy2DAsync(wcat + fp, 2 * fp * sizeof(float), wn, f_out * sizeof(float),
+                                f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
         GemmArgs g;
         g.m = n;
-        g.n = 2 * f_out;
+        g.n = 2 * fp;
         g.a1 = h;
         g.lda1 = f_in;
         g.b1 = wcat;
-        g.ldb1 = 2 * f_out;
+        g.ldb1 = 2 * fp;
         g.k1 = f_in;
         g.c = t;
-        g.ldc = 2 * f_out;
+        g.ldc = 2 * fp;
         gemm(g, TG_GEMM_AUTO, s);
         AggEpilogue epi;
         epi.mean = 1;
         epi.self = t;
-        epi.ld_self = 2 * f_out;
+        epi.ld_self = 2 * fp;
         epi.bias = bias;
         epi.act = act;
         epi.post = post;
-        run_aggregate(p, f_out, ci, nullptr, t + f_out, 2 * f_out, out, f_out, epi, s);
+        run_aggregate(p, f_out, ci, nullptr, t + fp, 2 * fp, out, f_out, epi, s);
     }
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
 }

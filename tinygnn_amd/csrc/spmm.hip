@@ -78,29 +78,56 @@ __global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
     }
 }
 
+// Chunk positions are reserved per workgroup: each row takes local slots in
+// an LDS histogram (its full chunks as one range, its remainder as one
+// slot), then one global atomic per nonempty bin and workgroup claims the
+// ranges.
 __global__ __launch_bounds__(256) void plan_scatter_kernel(
     const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
     const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
     int32_t* __restrict__ bin_cursor, int4* __restrict__ chunks, int4* __restrict__ split) {
+    __shared__ int hist[kPlanBins], gbase[kPlanBins];
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    int b = 0, e = 0, deg = 0, full = 0, rem = 0;
+    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0;
+    if (r < m) {
+        b = row_ptr[r];
+        e = row_ptr[r + 1];
+        deg = e - b;
+        if (deg <= chunk) {
+            bin_r = chunk_bin(deg);
+            pos_r = atomicAdd(&hist[bin_r], 1);
+            rem = -1;  // one direct chunk
+        } else {
+            full = deg / chunk;
+            rem = deg - full * chunk;
+            bin_f = chunk_bin(chunk);
+            pos_f = atomicAdd(&hist[bin_f], full);
+            if (rem) {
+                bin_r = chunk_bin(rem);
+                pos_r = atomicAdd(&hist[bin_r], 1);
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+        if (hist[i] > 0) gbase[i] = atomicAdd(&bin_cursor[i], hist[i]);
+    __syncthreads();
     if (r >= m) return;
-    const int b = row_ptr[r], e = row_ptr[r + 1];
-    const int deg = e - b;
     const int row = static_cast<int>(r);
-    if (deg <= chunk) {
-        const int pos = atomicAdd(&bin_cursor[chunk_bin(deg)], 1);
-        chunks[pos] = make_int4(row, b, e, -1);
+    if (rem < 0) {
+        chunks[gbase[bin_r] + pos_r] = make_int4(row, b, e, -1);
         return;
     }
-    const int nch = (deg + chunk - 1) / chunk;
     const int slot0 = slot_base[r];
-    for (int c = 0; c < nch; ++c) {
+    for (int c = 0; c < full; ++c) {
         const int cb = b + c * chunk;
-        const int ce = min(e, cb + chunk);
-        const int pos = atomicAdd(&bin_cursor[chunk_bin(ce - cb)], 1);
-        chunks[pos] = make_int4(row, cb, ce, slot0 + c);
+        chunks[gbase[bin_f] + pos_f + c] = make_int4(row, cb, cb + chunk, slot0 + c);
     }
-    split[split_pos[r]] = make_int4(row, slot0, nch, deg);
+    if (rem) chunks[gbase[bin_r] + pos_r] = make_int4(row, b + full * chunk, e, slot0 + full);
+    split[split_pos[r]] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
 }
 
 }  // namespace
@@ -164,9 +191,10 @@ void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* 
 
     p.chunks.resize(static_cast<size_t>(p.n_chunks) * sizeof(int4));
     p.split.resize(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
+    // partial rows are padded to a multiple of 4 floats (128-bit access)
     if (p.n_partials > 0 && max_f > 0)
-        p.partials.resize(static_cast<size_t>(p.n_partials) * static_cast<size_t>(max_f) *
-                          sizeof(float));
+        p.partials.resize(static_cast<size_t>(p.n_partials) *
+                          static_cast<size_t>(round_up(max_f, 4)) * sizeof(float));
     plan_scatter_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), slot_base,
                                              split_pos, bin_cursor, p.chunks.as<int4>(),
                                              p.split.as<int4>());
@@ -204,6 +232,15 @@ int pick_vec(int64_t f, std::initializer_list<int64_t> lds,
         for (const void* p : ptrs)
             ok = ok && (reinterpret_cast<uintptr_t>(p) % (sizeof(float) * v)) == 0;
         if (ok) return v;
+    }
+    return 1;
+}
+
+int pick_load_vec(int64_t f, int64_t ldb, const void* b) {
+    for (int v : {4, 2}) {
+        if (ldb % v == 0 && round_up(f, v) <= ldb &&
+            reinterpret_cast<uintptr_t>(b) % (sizeof(float) * v) == 0)
+            return v;
     }
     return 1;
 }
@@ -253,12 +290,25 @@ __device__ __forceinline__ float apply_act(float x, int act, int post) {
 
 template <int VEC>
 __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, int64_t fo,
-                                             float* __restrict__ c, int64_t ldc,
+                                             int64_t f, float* __restrict__ c, int64_t ldc,
                                              const AggEpilogue& epi) {
     if (epi.mean && deg > 0) {
         const float inv = 1.0f / static_cast<float>(deg);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) x[k] *= inv;
+    }
+    if (!epi.vec_io) {
+        // element by element, within the f valid columns (the output or the
+        // epilogue operands are not aligned to the access width)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            if (fo + k >= f) break;
+            float v = x[k];
+            if (epi.self) v += epi.self[static_cast<int64_t>(row) * epi.ld_self + fo + k];
+            if (epi.bias) v += epi.bias[fo + k];
+            c[static_cast<int64_t>(row) * ldc + fo + k] = apply_act(v, epi.act, epi.post);
+        }
+        return;
     }
     if (epi.self) {
         float t[VEC];
@@ -291,10 +341,17 @@ __device__ __forceinline__ float combine(float acc, float x, float w) {
     return (acc < x) ? x : acc;
 }
 
+// Gathers in flight per lane (row vectors of B loaded before they are used).
 template <int VPL>
 struct Unroll {
-    static constexpr int value = VPL == 1 ? 8 : (VPL == 2 ? 4 : 2);
+    static constexpr int value = VPL <= 2 ? 8 : 4;
 };
+
+// Shuffle of an edge entry held by lane `src` of the caller's lane group.
+__device__ __forceinline__ int shfl_i(int v, int src, int width) { return __shfl(v, src, width); }
+__device__ __forceinline__ float shfl_f(float v, int src, int width) {
+    return __shfl(v, src, width);
+}
 
 template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256) void agg_chunk_kernel(
@@ -312,12 +369,13 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     const int4 ch = chunks[cid];
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
 
-    int64_t fo[VPL];
+    int64_t fo[VPL], fl[VPL];
     bool ok[VPL];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
         fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
         ok[v] = fo[v] < f;
+        fl[v] = ok[v] ? fo[v] : 0;  // lanes past f load the row's first vector, never stored
     }
     float acc[VPL][VEC];
 #pragma unroll
@@ -325,49 +383,58 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc[v][k] = MODE == kAggMax ? -INFINITY : 0.0f;
 
-    int nz = ch.y;
+    // The chunk's entries are walked in batches of BE = max(LPR, U): each
+    // lane of the group loads CPL consecutive (col, val) pairs of the batch
+    // with one coalesced access, and the group broadcasts them with
+    // shuffles, so the per-edge cost is the row gather alone.  Edges stay in
+    // nonzero order (entry t of a batch is lane t / CPL, slot t % CPL).
+    constexpr int CPL = U > LPR ? U / LPR : 1;
+    constexpr int BE = LPR * CPL;
     const int e = ch.z;
-    for (; nz + U <= e; nz += U) {
-        int col[U];
-        float w[U];
+    for (int base = ch.y; base < e; base += BE) {
+        int cl[CPL];
+        float wl[CPL];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            col[u] = ci[nz + u];
-            if constexpr (MODE == kAggWeighted) w[u] = av[nz + u];
+        for (int j = 0; j < CPL; ++j) {
+            const int idx = base + l * CPL + j;
+            cl[j] = idx < e ? ci[idx] : 0;
+            wl[j] = 1.0f;
+            if constexpr (MODE == kAggWeighted) wl[j] = idx < e ? av[idx] : 0.0f;
         }
-        float bv[U][VPL][VEC];
+        // U gathers in flight per step; in the chunk's last, partial batch
+        // the slots past its end gather row 0 (in bounds: cl is 0 there) and
+        // are not accumulated.
+        const int cnt = e - base < BE ? e - base : BE;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float* brow = B + static_cast<int64_t>(col[u]) * ldb;
+        for (int s0 = 0; s0 < BE; s0 += U) {
+            if (s0 < cnt) {  // uniform across the group: no early exit in the unrolled body
+                int col[U];
+                float w[U];
 #pragma unroll
-            for (int v = 0; v < VPL; ++v) {
-                if (ok[v]) {
-                    load_vec<VEC>(brow + fo[v], bv[u][v]);
-                } else {
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) bv[u][v][k] = 0.0f;
+                for (int u = 0; u < U; ++u) {
+                    col[u] = shfl_i(cl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+                    w[u] = 1.0f;
+                    if constexpr (MODE == kAggWeighted)
+                        w[u] = shfl_f(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
                 }
-            }
-        }
+                float bv[U][VPL][VEC];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+                for (int u = 0; u < U; ++u) {
+                    const float* brow = B + static_cast<int64_t>(col[u]) * ldb;
 #pragma unroll
-            for (int v = 0; v < VPL; ++v)
+                    for (int v = 0; v < VPL; ++v) load_vec<VEC>(brow + fl[v], bv[u][v]);
+                }
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
-    }
-    for (; nz < e; ++nz) {
-        const int col = ci[nz];
-        float w = 1.0f;
-        if constexpr (MODE == kAggWeighted) w = av[nz];
-        const float* brow = B + static_cast<int64_t>(col) * ldb;
+                for (int u = 0; u < U; ++u) {
+                    const bool valid = s0 + u < cnt;  // a select, not a branch
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-            if (ok[v]) {
-                float t[VEC];
-                load_vec<VEC>(brow + fo[v], t);
+                    for (int v = 0; v < VPL; ++v)
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) acc[v][k] = combine<MODE>(acc[v][k], t[k], w);
+                        for (int k = 0; k < VEC; ++k) {
+                            const float nx = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
+                            acc[v][k] = valid ? nx : acc[v][k];
+                        }
+                }
             }
         }
     }
@@ -382,7 +449,7 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
         }
 #pragma unroll
         for (int v = 0; v < VPL; ++v)
-            if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], C, ldc, epi);
+            if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], f, C, ldc, epi);
     } else {
         float* prow = partials + static_cast<int64_t>(ch.w) * ldp;
 #pragma unroll
@@ -420,7 +487,7 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
             for (int k = 0; k < VEC; ++k)
                 acc[k] = MODE == kAggMax ? ((acc[k] < t[k]) ? t[k] : acc[k]) : acc[k] + t[k];
         }
-        finish_store<VEC>(acc, sp.x, sp.w, fo, C, ldc, epi);
+        finish_store<VEC>(acc, sp.x, sp.w, fo, f, C, ldc, epi);
     }
 }
 
@@ -430,7 +497,7 @@ void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const i
                 const AggEpilogue& epi, hipStream_t s) {
     constexpr int GPB = 256 / LPR;
     float* partials = p.partials.as<float>();
-    const int64_t ldp = f;
+    const int64_t ldp = round_up(f, VEC);  // padded partial rows
     if (p.n_chunks > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
@@ -477,13 +544,17 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
         require(f <= p.max_f,
                 "aggregate: feature width " + std::to_string(f) +
                     " exceeds the plan's max_f " + std::to_string(p.max_f));
-    const int vec = pick_vec(f, {ldb, ldc, epi.self ? epi.ld_self : 0},
-                             {B, C, epi.self, epi.bias});
+    // Loads use the widest access the rows of B allow (a padded leading
+    // dimension lets the last vector of a row run into the padding); stores
+    // and the epilogue operands are vectors only when they are aligned too.
+    const int vec = pick_load_vec(f, ldb, B);
+    AggEpilogue e = epi;
+    e.vec_io = pick_vec(f, {ldc, epi.self ? epi.ld_self : vec}, {C, epi.self, epi.bias}) >= vec;
     const LaneLayout L = choose_layout(f, vec);
 #define TG_AGG_MODE(M_)                                                                \
-    if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);    \
-    if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);    \
-    return dispatch_lpr<1, M_>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
+    if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
+    if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
+    return dispatch_lpr<1, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);
     if (epi.max) {
         require(!epi.mean, "aggregate: max and mean are exclusive");
         TG_AGG_MODE(kAggMax)

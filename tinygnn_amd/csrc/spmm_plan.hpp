@@ -57,4 +57,21 @@ LaneLayout choose_layout(int64_t f, int vec);
 int pick_vec(int64_t f, std::initializer_list<int64_t> lds,
              std::initializer_list<const void*> ptrs);
 
+// Largest width for loading rows of f valid floats from a matrix of leading
+// dimension ldb: the last vector of a row may run into the row's padding
+// (round_up(f, v) <= ldb), whose values are loaded and never stored.
+int pick_load_vec(int64_t f, int64_t ldb, const void* b);
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Row pitch (floats) for a dense matrix whose rows are gathered: widths of
+// 4, 8, 16 or 32 floats after 4-float padding tile a 128-byte cache line
+// exactly; wider rows are padded to whole lines, so a gathered row always
+// touches ceil(f / 32) lines and never one more.
+inline int64_t gather_pitch(int64_t f) {
+    const int64_t p = round_up(f, 4);
+    if (p == 4 || p == 8 || p == 16 || p == 32) return p;
+    return round_up(f, 32);
+}
+
 }  // namespace tg
