@@ -190,6 +190,19 @@ def run_spmm_d(args, torch, tg):
                 head=head, cpu=cpu, csr_build_ms=csr_ms)
 
 
+def logit_parity(got, want):
+    """|err| <= 1e-5 + 1e-4|want| elementwise, argmax agreement, and the
+    number of nodes whose reference top-2 gap is within the largest error
+    (near-ties, where any non-bit-exact path may flip the argmax)."""
+    err = np.abs(got.astype(np.float64) - want)
+    tol = 1e-5 + 1e-4 * np.abs(want.astype(np.float64))
+    top2 = np.sort(want, axis=1)[:, -2:]
+    ties = int(((top2[:, 1] - top2[:, 0]) <= float(err.max())).sum())
+    return dict(max_abs_err=float(err.max()), within_tol=bool((err <= tol).all()),
+                n_out_of_tol=int((err > tol).sum()),
+                argmax_mismatch=int((got.argmax(1) != want.argmax(1)).sum()), near_ties=ties)
+
+
 # Roofline times of the declared dataflows at config E (8 TB/s, 157.3 TF/s):
 # GCN and GAT aggregate at F_out, SAGE runs transform-first.
 FORWARD_ROOFLINE_MS = {"gcn": 17.81, "sage": 18.18, "gat": 17.70}
@@ -247,30 +260,44 @@ def run_forward_e(args, torch, tg):
             timer.stop(e0)
         torch.cuda.synchronize()
         refsem = float(np.median(timer.ms()))
+        raw = y.cpu().numpy()
         logits = tg.log_softmax_(y.clone()).cpu().numpy()
+        # the same model in exact precision (the reference's operation order)
+        model.set_precision(tg.PRECISION_EXACT)
+        model.forward(adj, x, mode=tg.FORWARD_CACHED, out=y)
+        torch.cuda.synchronize()
+        timer = StreamTimer(torch, stream)
+        for _ in range(3):
+            e0 = timer.start()
+            model.forward(adj, x, mode=tg.FORWARD_CACHED, out=y)
+            timer.stop(e0)
+        torch.cuda.synchronize()
+        exact_ms = float(np.median(timer.ms()))
+        raw_x = y.cpu().numpy()
+        logits_x = tg.log_softmax_(y.clone()).cpu().numpy()
+        model.set_precision(tg.PRECISION_FAST)
         r = dict(gpu_ms=round(cached, 3), gpu_ms_reference_semantics=round(refsem, 3),
+                 gpu_ms_exact=round(exact_ms, 3),
                  roofline_ms=FORWARD_ROOFLINE_MS[name],
                  roofline_frac=round(FORWARD_ROOFLINE_MS[name] / cached, 4))
-        log(f"{name}: cached {cached:.2f} ms, reference semantics {refsem:.2f} ms")
+        log(f"{name}: cached {cached:.2f} ms, reference semantics {refsem:.2f} ms, "
+            f"exact {exact_ms:.2f} ms")
         if ref is not None:
             rm = ref.model(spec, w)
             t1 = time.perf_counter()
-            want = rm.forward_handles(ref_tensors[0], ref_tensors[1], n)
+            want_raw = rm.forward_handles(ref_tensors[0], ref_tensors[1], n)
             cpu_ms = (time.perf_counter() - t1) * 1e3
-            want = ref.activation("log_softmax", want)
-            err = np.abs(logits.astype(np.float64) - want)
-            tol = 1e-5 + 1e-4 * np.abs(want.astype(np.float64))
-            top2 = np.sort(want, axis=1)[:, -2:]
-            ties = int(((top2[:, 1] - top2[:, 0]) <= float(err.max())).sum())
+            want = ref.activation("log_softmax", want_raw)
             r.update(cpu_ms=round(cpu_ms, 1), cpu_threads=ref.num_threads(),
                      speedup=round(cpu_ms / cached, 1),
-                     parity=dict(max_abs_err=float(err.max()),
-                                 within_tol=bool((err <= tol).all()),
-                                 n_out_of_tol=int((err > tol).sum()),
-                                 argmax_mismatch=int((logits.argmax(1) != want.argmax(1)).sum()),
-                                 near_ties=ties))
-            log(f"{name}: cpu {cpu_ms:.0f} ms ({ref.num_threads()} thr), parity {r['parity']}")
-            del rm, want
+                     parity=logit_parity(logits, want),
+                     parity_exact=dict(
+                         logit_parity(logits_x, want),
+                         forward_bit_identical_frac=float(
+                             (raw_x.view(np.int32) == want_raw.view(np.int32)).mean())))
+            log(f"{name}: cpu {cpu_ms:.0f} ms ({ref.num_threads()} thr), parity {r['parity']}, "
+                f"exact {r['parity_exact']}")
+            del rm, want, want_raw
         out[name] = r
         del model, y
     return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)

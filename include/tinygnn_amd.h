@@ -267,6 +267,19 @@ int tg_model_clear_tensors(tg_model_t model);
 int tg_model_load_weights(tg_model_t model);
 /* SAGE dataflow used by the model's SAGE-mean layers (TG_SAGE_*). */
 int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);
+/* Precision of the model's forward:
+ *   TG_PRECISION_FAST (default): fp32 MFMA for the wide transforms, rows of
+ *     more than one plan chunk summed from per-chunk partials, SAGE
+ *     transform-first on large graphs, GAT with a one-pass online softmax;
+ *     within 1e-4 relative / 1e-5 absolute of the reference.
+ *   TG_PRECISION_EXACT: the reference's operation order everywhere -- in-order
+ *     GEMMs, every row one fma chain (no row splitting), SAGE concat, GAT's
+ *     max / sequential sum / alpha = t*(1/sum) per row with exp and ELU
+ *     evaluated in double and rounded.  GCN and SAGE outputs are
+ *     bit-identical to the reference; GAT differs only where the reference's
+ *     libm expf is not correctly rounded. */
+enum { TG_PRECISION_FAST = 0, TG_PRECISION_EXACT = 1 };
+int tg_model_set_precision(tg_model_t model, int precision);
 int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
                      const int32_t* row_ptr, const int32_t* col_ind, const float* val,
                      int64_t f_in, const float* x, float* out, int mode,

@@ -117,6 +117,43 @@ def test_sage_dataflows_agree(gpu, restate):
         assert_close(m.forward(da, _t(gpu, x)).cpu().numpy(), want, what=f"dataflow {df}")
 
 
+@pytest.mark.parametrize("model", ["gcn", "sage", "gat"])
+def test_exact_precision(gpu, restate, model):
+    """PRECISION_EXACT on a graph whose long rows (up to 3,000 nonzeros) the
+    fast mode splits, with wide transforms: GCN and SAGE outputs equal the
+    reference's bytes; GAT differs only through exp (device exp rounded from
+    double vs the host libm's expf)."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(77)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=25, max_deg=3000, empty_frac=0.02)
+    x = rng.standard_normal((n, 70)).astype(np.float32)
+    spec = {"gcn": synth.spec_gcn(70, 96, 41), "sage": synth.spec_sage(70, 96, 41),
+            "gat": synth.spec_gat(70, 24, 4, 41)}[model]
+    w = synth.model_weights(spec, seed=4)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    m = tg.Model.from_spec(spec, w)
+    m.set_precision(tg.PRECISION_EXACT)
+    got = m.forward(da, _t(gpu, x)).cpu().numpy()
+    if model == "gat":
+        assert_close(got, want, rtol=2e-6, atol=2e-7, what="gat exact")
+    else:
+        np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+    # Switching back rebuilds the plans: the output equals a fresh fast-mode
+    # model's bytes (every kernel is deterministic).  The fast mode is not
+    # held to 1e-4 here: on the 1,600-nonzero hub rows of this graph the
+    # reference's own fp32 result is 1.6e-3 (relative) from a float64
+    # forward, so a different summation order may legitimately differ by that.
+    m.set_precision(tg.PRECISION_FAST)
+    fresh = tg.Model.from_spec(spec, w).forward(da, _t(gpu, x)).cpu().numpy()
+    np.testing.assert_array_equal(m.forward(da, _t(gpu, x)).cpu().numpy().view(np.int32),
+                                  fresh.view(np.int32))
+
+
 def test_model_errors(gpu):
     import tinygnn_amd as tg
     da = tg.DeviceCSR.from_numpy(2, 2, np.array([0, 1, 2], np.int32), np.array([1, 0], np.int32),

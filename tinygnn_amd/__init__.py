@@ -22,6 +22,7 @@ GEMM_AUTO, GEMM_INORDER, GEMM_MFMA = 0, 1, 2
 EPI_NONE, EPI_RELU, EPI_ELU = 0, 1, 2
 SAGE_AUTO, SAGE_CONCAT, SAGE_TRANSFORM_FIRST = 0, 1, 2
 FORWARD_REFERENCE, FORWARD_CACHED = 0, 1
+PRECISION_FAST, PRECISION_EXACT = 0, 1
 
 
 def _torch():
@@ -383,6 +384,11 @@ class Model:
 
     def set_sage_dataflow(self, dataflow: int) -> None:
         lib.check(lib.tg_model_set_sage_dataflow(self.h, dataflow))
+
+    def set_precision(self, precision: int) -> None:
+        """PRECISION_FAST (default) or PRECISION_EXACT (the reference's
+        operation order: bit-identical GCN / SAGE outputs)."""
+        lib.check(lib.tg_model_set_precision(self.h, precision))
 
     def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):
         torch = _torch()

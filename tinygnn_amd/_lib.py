@@ -99,6 +99,7 @@ SIGNATURES = {
     "tg_model_clear_tensors": (i32, [vp]),
     "tg_model_load_weights": (i32, [vp]),
     "tg_model_set_sage_dataflow": (i32, [vp, i32]),
+    "tg_model_set_precision": (i32, [vp, i32]),
     "tg_model_forward": (i32, [vp, i64, i64, vp, vp, vp, i64, vp, vp, i32, vp]),
 }
 

@@ -127,6 +127,133 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Wide in-order GEMM (bit-exact, n > 32): 128x128 workgroup tile, an 8x8
+// register micro-tile per thread, BK = 8, two LDS buffers with register
+// prefetch.  Each output is still one fma chain over k ascending from 0 (the
+// k loop is outermost, and no padded k is ever accumulated), so the result
+// equals the reference's (i,k,j) loop bit for bit; DUAL interleaves the two
+// products per k exactly as the in-order kernel above.
+// ---------------------------------------------------------------------------
+constexpr int kWBM = 128, kWBN = 128, kWBK = 8;
+
+template <int VA, bool DUAL>
+__global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
+    constexpr int NP = DUAL ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) float As[2][NP][kWBK][kWBM];
+    __shared__ __attribute__((aligned(16))) float Bs[2][NP][kWBK][kWBN];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kWBM;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kWBN;
+    const int64_t M = g.m, N = g.n, K = g.k1;
+    const int64_t nt = (K + kWBK - 1) / kWBK;
+    // loads: A row ar, 4 k from ak; B row bk, 4 n from bn
+    const int ar = threadIdx.x >> 1, ak = (threadIdx.x & 1) * 4;
+    const int bk = threadIdx.x >> 5, bn = (threadIdx.x & 31) * 4;
+    float ra[NP][4], rb[NP][4];
+
+    auto fetch = [&](int64_t kt) {
+        const int64_t k0 = kt * kWBK;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float* A = p ? g.a2 : g.a1;
+            const float* B = p ? g.b2 : g.b1;
+            const int64_t lda = p ? g.lda2 : g.lda1;
+            const int64_t ldb = p ? g.ldb2 : g.ldb1;
+            const int64_t gm = m0 + ar, ka = k0 + ak;
+            const float* pa = A + (gm < M ? gm : 0) * lda + ka;
+            const int64_t va = gm < M ? K - ka : 0;
+            if (VA == 4 && va >= 4) {
+                const float4 t = *reinterpret_cast<const float4*>(pa);
+                ra[p][0] = t.x; ra[p][1] = t.y; ra[p][2] = t.z; ra[p][3] = t.w;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) ra[p][u] = u < va ? pa[u] : 0.0f;
+            }
+            const int64_t kb = k0 + bk, nb = n0 + bn;
+            const float* pb = B + (kb < K ? kb : 0) * ldb + nb;
+            const int64_t vb = kb < K ? N - nb : 0;
+            if (vb >= 4 && (ldb % 4) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0) {
+                const float4 t = *reinterpret_cast<const float4*>(pb);
+                rb[p][0] = t.x; rb[p][1] = t.y; rb[p][2] = t.z; rb[p][3] = t.w;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) rb[p][u] = u < vb ? pb[u] : 0.0f;
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) As[buf][p][ak + u][ar] = ra[p][u];
+            *reinterpret_cast<float4*>(&Bs[buf][p][bk][bn]) =
+                make_float4(rb[p][0], rb[p][1], rb[p][2], rb[p][3]);
+        }
+    };
+
+    float acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+    bool tail[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tail[j] = DUAL && g.tail_from >= 0 && (n0 + tx * 8 + j) >= g.tail_from;
+
+    if (nt > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        const int cb = static_cast<int>(kt & 1);
+        if (kt + 1 < nt) fetch(kt + 1);
+        const int kmax = static_cast<int>(K - kt * kWBK < kWBK ? K - kt * kWBK : kWBK);
+        for (int kk = 0; kk < kmax; ++kk) {
+            float a[NP][8], b[NP][8];
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const float4 a0 = *reinterpret_cast<const float4*>(&As[cb][p][kk][ty * 8]);
+                const float4 a1 = *reinterpret_cast<const float4*>(&As[cb][p][kk][ty * 8 + 4]);
+                const float4 b0 = *reinterpret_cast<const float4*>(&Bs[cb][p][kk][tx * 8]);
+                const float4 b1 = *reinterpret_cast<const float4*>(&Bs[cb][p][kk][tx * 8 + 4]);
+                a[p][0] = a0.x; a[p][1] = a0.y; a[p][2] = a0.z; a[p][3] = a0.w;
+                a[p][4] = a1.x; a[p][5] = a1.y; a[p][6] = a1.z; a[p][7] = a1.w;
+                b[p][0] = b0.x; b[p][1] = b0.y; b[p][2] = b0.z; b[p][3] = b0.w;
+                b[p][4] = b1.x; b[p][5] = b1.y; b[p][6] = b1.z; b[p][7] = b1.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if constexpr (DUAL) {
+                        if (tail[j]) {
+                            acc[i][j] = acc[i][j] + __builtin_fmaf(a[0][i], b[0][j], a[1][i] * b[1][j]);
+                        } else {
+                            const float t = __builtin_fmaf(a[0][i], b[0][j], acc[i][j]);
+                            acc[i][j] = __builtin_fmaf(a[1][i], b[1][j], t);
+                        }
+                    } else {
+                        acc[i][j] = __builtin_fmaf(a[0][i], b[0][j], acc[i][j]);
+                    }
+                }
+        }
+        if (kt + 1 < nt) stage(cb ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t gm = m0 + ty * 8 + i;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t gn = n0 + tx * 8 + j;
+            if (gn < N) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA GEMM: 128x128 workgroup tile, 2x2 wavefronts of 64x64 (4x4 tiles of
 // v_mfma_f32_16x16x4f32), BK = 16, two LDS buffers with register prefetch:
 // the next K tile is loaded from global memory while the current one feeds
@@ -374,7 +501,21 @@ void launch_inorder(const GemmArgs& g, hipStream_t s) {
 
 template <bool DUAL>
 void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
-    if (g.n > 32) return launch_inorder<64, 64, 4, 4, DUAL>(g, s);
+    if (g.n > 32) {
+        // the 8x8 register-blocked kernel; 128-bit A loads when rows allow
+        auto aligned = [](const float* p, int64_t ld) {
+            return p == nullptr || (ld % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0);
+        };
+        const bool va4 = aligned(g.a1, g.lda1) && (!DUAL || aligned(g.a2, g.lda2));
+        dim3 grid(static_cast<unsigned>(ceil_div(g.m, kWBM)),
+                  static_cast<unsigned>(ceil_div(g.n, kWBN)));
+        if (va4)
+            gemm_inorder_wide_kernel<4, DUAL><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_inorder_wide_kernel<1, DUAL><<<grid, 256, 0, s>>>(g);
+        TG_LAUNCH_CHECK();
+        return;
+    }
     if (g.n > 16) return launch_inorder<128, 32, 4, 4, DUAL>(g, s);
     if (g.n > 8 || DUAL) return launch_inorder<256, 16, 4, 4, DUAL>(g, s);
     return launch_inorder<256, 8, 4, 2, DUAL>(g, s);

@@ -56,14 +56,20 @@ __device__ __forceinline__ void stv(float* p, const float (&x)[VEC]) {
 
 __device__ __forceinline__ float lrelu(float e, float slope) { return (e >= 0.0f) ? e : slope * e; }
 
+// exp evaluated in double and rounded once: the correctly rounded float
+// exp except when the double result falls within an ulp of a float
+// midpoint; the host libm's expf is within 0.502 ulp, so the two agree but
+// for rare last-ulp cases.
+__device__ __forceinline__ float exp_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+
 __device__ __forceinline__ float finish_val(float x, const float* bias, int64_t fo, int act,
-                                            int post) {
+                                            int post, bool exact = false) {
     if (bias) x = x + bias[fo];
     if (act == TG_ACT_RELU) x = (0.0f < x) ? x : 0.0f;
     if (post == TG_POST_RELU) {
         x = (0.0f < x) ? x : 0.0f;
     } else if (post == TG_POST_ELU) {
-        if (x < 0.0f) x = 1.0f * (expf(x) - 1.0f);
+        if (x < 0.0f) x = 1.0f * ((exact ? exp_rn(x) : expf(x)) - 1.0f);
     }
     return x;
 }
@@ -138,6 +144,7 @@ struct GatArgs {
     int act;
     int post;
     int vec_io;        // stores and bias loads are full, aligned vectors
+    int exact;         // the reference's operation order (rows never split)
 };
 
 // Applies the epilogue and stores one lane vector of row `row`.
@@ -146,15 +153,111 @@ __device__ __forceinline__ void gat_store(const GatArgs& a, int64_t row, int64_t
                                           float (&x)[VEC], float scale) {
     if (a.vec_io) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) x[k] = finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post);
+        for (int k = 0; k < VEC; ++k)
+            x[k] = finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post, a.exact);
         stv<VEC>(a.out + row * a.ldo + fo, x);
         return;
     }
 #pragma unroll
     for (int k = 0; k < VEC; ++k) {
         if (fo + k >= a.ftot) break;
-        a.out[row * a.ldo + fo + k] = finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post);
+        a.out[row * a.ldo + fo + k] =
+            finish_val(x[k] * scale, a.bias, fo + k, a.act, a.post, a.exact);
     }
+}
+
+// Exact variant (the plan never splits rows): per row and head, the
+// reference's sequence (layers.cpp:1056-1109) -- e = LeakyReLU(s_i + d_j);
+// the row max; t = exp(e - max) summed in nonzero order; alpha = t * (1/sum)
+// (0 when the sum is 0); out = fma(alpha, Wh_j, out) in nonzero order.  Each
+// lane walks the whole row for its own head, so every sum is sequential.
+template <int VEC, int LPR, int VPL>
+__global__ __launch_bounds__(256) void gat_exact_kernel(GatArgs a) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int TILE = LPR * VPL * VEC;
+    constexpr int U = 8;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (cid >= a.n_chunks) return;
+    const int4 ch = a.chunks[cid];
+    const int row = ch.x, b = ch.y, e = ch.z;
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+    const int H = a.heads;
+    const float* srow = a.src + static_cast<int64_t>(row) * H;
+    int64_t fo[VPL], fl[VPL];
+    bool ok[VPL];
+    int hv[VPL];
+    float si[VPL], m[VPL], sum[VPL], inv[VPL], acc[VPL][VEC];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+        fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
+        ok[v] = fo[v] < a.ftot;
+        fl[v] = ok[v] ? fo[v] : 0;
+        hv[v] = ok[v] ? static_cast<int>(fo[v] / a.f) : 0;
+        si[v] = srow[hv[v]];
+        m[v] = -INFINITY;
+        sum[v] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[v][k] = 0.0f;
+    }
+    // passes 1 and 2: the max, then the sequential sum of exp(e - max)
+    for (int pass = 0; pass < 2; ++pass) {
+        for (int base = b; base < e; base += LPR) {
+            const int idx = base + l;
+            const int cl = idx < e ? a.ci[idx] : 0;
+            const int cnt = e - base < LPR ? e - base : LPR;
+            for (int t = 0; t < cnt; ++t) {
+                const int col = __shfl(cl, t, LPR);
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) {
+                    const float x = lrelu(si[v] + a.dst[static_cast<int64_t>(col) * H + hv[v]], a.slope);
+                    if (pass == 0)
+                        m[v] = (m[v] < x) ? x : m[v];
+                    else
+                        sum[v] += exp_rn(x - m[v]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) inv[v] = (sum[v] > 0.0f) ? 1.0f / sum[v] : 0.0f;
+    // pass 3: alpha-weighted rows in nonzero order, U gathers in flight
+    for (int base = b; base < e; base += LPR) {
+        const int idx = base + l;
+        const int cl = idx < e ? a.ci[idx] : 0;
+        const int cnt = e - base < LPR ? e - base : LPR;
+        for (int s0 = 0; s0 < cnt; s0 += U) {
+            int col[U];
+            float w[U][VPL][VEC], al[U][VPL];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int t = s0 + u < LPR ? s0 + u : LPR - 1;
+                col[u] = __shfl(cl, t, LPR);
+                const float* wr = a.wh + static_cast<int64_t>(col[u]) * a.ldwh;
+#pragma unroll
+                for (int v = 0; v < VPL; ++v) {
+                    const float x = lrelu(si[v] + a.dst[static_cast<int64_t>(col[u]) * H + hv[v]], a.slope);
+                    al[u][v] = exp_rn(x - m[v]) * inv[v];
+                    ldv<VEC>(wr + fl[v], w[u][v]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const bool valid = s0 + u < cnt;
+#pragma unroll
+                for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                    for (int k = 0; k < VEC; ++k) {
+                        const float nx = __builtin_fmaf(al[u][v], w[u][v][k], acc[v][k]);
+                        acc[v][k] = valid ? nx : acc[v][k];
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+        if (ok[v]) gat_store<VEC>(a, row, fo[v], acc[v], 1.0f);
 }
 
 template <int VEC, int LPR, int VPL>
@@ -330,7 +433,7 @@ __global__ __launch_bounds__(256) void gat_reduce_kernel(GatArgs a) {
 __global__ __launch_bounds__(256) void gat_average_kernel(const float* __restrict__ x,
                                                           int64_t n, int heads, int f,
                                                           float* __restrict__ out, int64_t ldo,
-                                                          int post) {
+                                                          int post, int exact) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (t >= n * f) return;
     const int64_t i = t / f, j = t % f;
@@ -338,12 +441,22 @@ __global__ __launch_bounds__(256) void gat_average_kernel(const float* __restric
     float s = 0.0f;
     for (int h = 0; h < heads; ++h) s += xr[static_cast<int64_t>(h) * f + j];
     s *= 1.0f / static_cast<float>(heads);
-    out[i * ldo + j] = finish_val(s, nullptr, 0, TG_ACT_NONE, post);
+    out[i * ldo + j] = finish_val(s, nullptr, 0, TG_ACT_NONE, post, exact != 0);
 }
 
 template <int VEC, int LPR, int VPL>
 void launch_gat(const tg_spmm_plan_s& p, const LaneLayout& L, GatArgs& a, hipStream_t s) {
     constexpr int GPB = 256 / LPR;
+    if (a.exact) {
+        require(p.n_split == 0, "GATLayer: the exact edge pass needs a plan without split rows");
+        if (p.n_chunks > 0) {
+            dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
+                      static_cast<unsigned>(L.n_tiles));
+            gat_exact_kernel<VEC, LPR, VPL><<<grid, 256, 0, s>>>(a);
+            TG_LAUNCH_CHECK();
+        }
+        return;
+    }
     if (p.n_chunks > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
@@ -402,7 +515,7 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
                    const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
                    const float* dst, float slope, const float* bias, int act, int post,
                    int concat, float* out, int64_t ldo, void* work, size_t work_bytes,
-                   hipStream_t s) {
+                   hipStream_t s, bool exact) {
     require(n == p.m, "GATLayer::forward: plan rows differ from n");
     require(heads >= 1 && f >= 1, "GATLayer: bad sizes");
     require(act == TG_ACT_NONE || act == TG_ACT_RELU, "GATLayer: unknown activation");
@@ -445,6 +558,7 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
     a.bias = bias;
     a.act = act;
     a.post = avg ? TG_POST_NONE : post;
+    a.exact = exact ? 1 : 0;
     // Loads: the widest access the rows of Wh allow, never straddling two
     // heads (the width divides f, or there is one head); stores and bias
     // loads are vectors only when aligned as well.
@@ -461,7 +575,7 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
         dispatch_gat<1>(p, L, a, s);
     if (avg) {
         gat_average_kernel<<<static_cast<unsigned>(ceil_div(n * f, 256)), 256, 0, s>>>(
-            tmp, n, static_cast<int>(heads), static_cast<int>(f), out, ldo, post);
+            tmp, n, static_cast<int>(heads), static_cast<int>(f), out, ldo, post, exact ? 1 : 0);
         TG_LAUNCH_CHECK();
     }
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
@@ -499,7 +613,7 @@ int tg_gat_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
         require(row_ptr == plan->row_ptr, "GATLayer::forward: row_ptr differs from the plan's");
         tg::gat_aggregate(*plan, n, heads, f, col_ind, wh, ldwh, src, dst, slope, bias, act, post,
                           concat, out, ldo, workspace, workspace_bytes,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream), false);
     });
 }
 

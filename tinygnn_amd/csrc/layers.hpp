@@ -34,7 +34,7 @@ size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int data
 void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
-                  size_t work_bytes, hipStream_t s);
+                  size_t work_bytes, hipStream_t s, int gemm_algo = TG_GEMM_AUTO);
 
 // gat.hip
 void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
@@ -44,6 +44,6 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
                    const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
                    const float* dst, float slope, const float* bias, int act, int post,
                    int concat, float* out, int64_t ldo, void* work, size_t work_bytes,
-                   hipStream_t s);
+                   hipStream_t s, bool exact = false);
 
 }  // namespace tg

@@ -75,6 +75,8 @@ struct tg_model_s {
     std::vector<Layer> layers;
     std::map<std::string, HostTensor> staged;
     int sage_dataflow = TG_SAGE_AUTO;
+    int precision = TG_PRECISION_FAST;
+    int built_precision = -1;  // precision the cached plans were built for
 
     // adjacency-derived state
     bool have_cache = false;
@@ -210,13 +212,15 @@ void load_weights(tg_model_s& m) {
 void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
-                      m.key_n == n && m.key_nnz == nnz;
+                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision;
     if (mode == TG_FORWARD_CACHED && same) return;
     m.have_cache = false;
     const int64_t maxf = m.max_wide();
+    // exact: no row is split, so every row is one fma chain in nonzero order
+    const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
     if (m.need_raw()) {
         m.plan_raw = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*m.plan_raw, n, nnz, rp, maxf, 0, s);
+        build_plan(*m.plan_raw, n, nnz, rp, maxf, chunk, s);
     } else {
         m.plan_raw.reset();
     }
@@ -233,11 +237,12 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
             add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                            m.sl_v.as<float>(), m.work.get(), m.work.size(), s);
         m.plan_sl = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, 0, s);
+        build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, chunk, s);
     } else {
         m.plan_sl.reset();
     }
     m.have_cache = true;
+    m.built_precision = m.precision;
     m.key_rp = rp;
     m.key_ci = ci;
     m.key_v = v;
@@ -277,6 +282,11 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
 
     prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
 
+    // precision: the exact mode keeps the reference's operation order
+    const bool exact = m.precision == TG_PRECISION_EXACT;
+    const int algo = exact ? TG_GEMM_INORDER : TG_GEMM_AUTO;
+    const int dataflow = exact ? TG_SAGE_CONCAT : m.sage_dataflow;
+
     // buffers
     const int64_t wmax = m.max_wide();
     int64_t heads_max = 1;
@@ -284,7 +294,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     for (auto& l : m.layers) {
         heads_max = std::max(heads_max, l.heads);
         if (l.type == LType::SAGE)
-            ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, m.sage_dataflow, nnz));
+            ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, dataflow, nnz));
         if (l.type == LType::GAT)
             ws = std::max(ws, gat_workspace(*m.plan_sl, n, l.heads, l.out, l.concat));
     }
@@ -314,7 +324,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             g.k1 = l.in;
             g.c = hw;
             g.ldc = ldhw;
-            gemm(g, TG_GEMM_AUTO, s);
+            gemm(g, algo, s);
             AggEpilogue epi;
             epi.bias = l.bias ? l.b.as<float>() : nullptr;
             epi.act = l.act;
@@ -324,7 +334,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
         } else if (l.type == LType::SAGE) {
             sage_forward(*m.plan_raw, n, l.in, l.out, l.agg, ci, h, l.wn.as<float>(),
                          l.ws.as<float>(), l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
-                         m.sage_dataflow, y, m.work.get(), m.work.size(), s);
+                         dataflow, y, m.work.get(), m.work.size(), s, algo);
         } else {
             const int64_t wide = l.heads * l.out;
             const int64_t ldwh = gather_pitch(wide);  // line-aligned rows for the gathers
@@ -339,14 +349,14 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             g.k1 = l.in;
             g.c = wh;
             g.ldc = ldwh;
-            gemm(g, TG_GEMM_AUTO, s);
+            gemm(g, algo, s);
             float* src = m.scores.as<float>();
             float* dst = src + n * l.heads;
             gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
                        s);
             gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh, src,
                           dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
-                          l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s);
+                          l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s, exact);
         }
         h = y;
     }
@@ -450,6 +460,15 @@ int tg_model_set_tensor(tg_model_t model, const char* name, int64_t rows, int64_
         t.cols = cols;
         t.data.assign(host_data, host_data + rows * cols);
         model->staged[name] = std::move(t);
+    });
+}
+
+int tg_model_set_precision(tg_model_t model, int precision) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        require(precision == TG_PRECISION_FAST || precision == TG_PRECISION_EXACT,
+                "unknown precision");
+        model->precision = precision;
     });
 }
 

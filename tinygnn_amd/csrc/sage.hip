@@ -59,7 +59,7 @@ size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int data
 void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
-                  size_t work_bytes, hipStream_t s) {
+                  size_t work_bytes, hipStream_t s, int gemm_algo) {
     require(n == p.m, "SAGELayer::forward: plan rows differ from n");
     require(f_in >= 0 && f_out >= 0, "SAGELayer::forward: negative size");
     require(act == TG_ACT_NONE || act == TG_ACT_RELU, "SAGELayer: unknown activation");
@@ -99,7 +99,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         g.bias = bias;
         g.epi = act == TG_ACT_RELU ? TG_EPI_RELU : TG_EPI_NONE;
         g.tail_from = (f_out / 8) * 8;  // the reference's scalar tail columns
-        gemm(g, TG_GEMM_AUTO, s);
+        gemm(g, gemm_algo, s);
         add_bias_act(out, n, f_out, f_out, nullptr, TG_ACT_NONE, post, s);
     } else {
         // [Ws | 0 | Wn | 0]: each half padded to fp = gather_pitch(f_out)
@@ -124,7 +124,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         g.k1 = f_in;
         g.c = t;
         g.ldc = 2 * fp;
-        gemm(g, TG_GEMM_AUTO, s);
+        gemm(g, gemm_algo, s);
         AggEpilogue epi;
         epi.mean = 1;
         epi.self = t;
@@ -171,7 +171,7 @@ int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
         require(row_ptr == plan->row_ptr, "SAGELayer::forward: row_ptr differs from the plan's");
         tg::sage_forward(*plan, n, f_in, f_out, agg, col_ind, h, w_neigh, w_self, bias, act, post,
                          dataflow, out, workspace, workspace_bytes,
-                         static_cast<hipStream_t>(stream));
+                         static_cast<hipStream_t>(stream), TG_GEMM_AUTO);
     });
 }
 
