@@ -285,6 +285,91 @@ int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
                      int64_t f_in, const float* x, float* out, int mode,
                      tg_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * CSV ingestion -- replaces GraphLoader::parse_edges / parse_features and
+ * the reading half of GraphLoader::load (src/graph_loader.cpp:61-206,
+ * 286-326).  The text is indexed into lines once on the device (lines split
+ * at '\n', trimmed of " \t\r\n", empty ones dropped: read_lines, :38-53;
+ * line 0 is a header when a letter or '_' precedes its first ',', ' ' or
+ * '\t': is_header, :24-33), then parsed as an edge list or a feature table.
+ * Fields convert with std::stoi / std::stof semantics (glibc strtol /
+ * strtof, bit for bit, ERANGE included).  Errors are std::runtime_error
+ * (TG_ERR_RUNTIME) with the reference's messages, for the first failing line
+ * in file order; line numbers count the non-empty lines from 1.
+ *   tg_csv_open           reads a file into device memory and indexes it
+ *                         ("GraphLoader: cannot open file '<path>'").
+ *   tg_csv_index          indexes text already in device memory; the text
+ *                         must outlive the handle.  name is used in messages.
+ *   tg_csv_parse_edges    <- parse_edges (:61-107): one (src, dst) per data
+ *                         line into device int32 src[], dst[] of
+ *                         n_lines - has_header entries; max_id_out (host,
+ *                         optional) receives the largest endpoint, -1 if none.
+ *   tg_csv_feature_shape  <- parse_features' dimensions (:118-183): rows =
+ *                         largest node_id + 1, cols = the first data line's
+ *                         feature count.  Reports only "file is empty" /
+ *                         "no data rows"; field errors come from the parse.
+ *   tg_csv_parse_features <- parse_features (:112-206): out (device,
+ *                         n_rows >= rows, leading dimension ld >= cols) gets
+ *                         in row r the features of the last line whose
+ *                         node_id is r, zeros where no line has that node_id,
+ *                         and zeros in rows [rows, n_rows) (the zero padding
+ *                         of GraphLoader::load, :311-320).
+ * All of them synchronise the stream (data-dependent sizes and errors).
+ * ------------------------------------------------------------------------ */
+typedef struct tg_csv_s* tg_csv_t;
+int tg_csv_open(const char* path, tg_csv_t* csv_out, tg_stream_t stream);
+int tg_csv_index(const char* text, int64_t n_bytes, const char* name, tg_csv_t* csv_out,
+                 tg_stream_t stream);
+int tg_csv_destroy(tg_csv_t csv);
+int tg_csv_info(tg_csv_t csv, int64_t* n_lines, int* has_header);
+int tg_csv_parse_edges(tg_csv_t csv, int32_t* src, int32_t* dst, int64_t* max_id_out,
+                       tg_stream_t stream);
+int tg_csv_feature_shape(tg_csv_t csv, int64_t* rows, int64_t* cols, tg_stream_t stream);
+int tg_csv_parse_features(tg_csv_t csv, float* out, int64_t n_rows, int64_t ld,
+                          tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * TGNN weight file, version 1 -- replaces load_weight_file
+ * (src/model.cpp:134-185; format include/tinygnn/model.hpp:22-33).  Read on
+ * the host; entries keep the file's order (a repeated name: the last one is
+ * what the reference's map keeps).  Errors are std::runtime_error with the
+ * reference's messages ("load_weight_file: cannot open <path>", "... invalid
+ * magic in <path>", "... unsupported version <v> in <path>", "...: unexpected
+ * end of file or read error.").  tg_weights_tensor's pointers are host
+ * memory owned by the handle.  Model::load_weights(path) is tg_weights_open,
+ * tg_model_set_tensor per entry, tg_model_load_weights.
+ * ------------------------------------------------------------------------ */
+typedef struct tg_weights_s* tg_weights_t;
+int tg_weights_open(const char* path, tg_weights_t* out);
+int tg_weights_info(tg_weights_t w, int64_t* n_tensors, float* test_accuracy);
+int tg_weights_tensor(tg_weights_t w, int64_t i, const char** name, int64_t* name_len,
+                      int64_t* rows, int64_t* cols, const float** data);
+int tg_weights_destroy(tg_weights_t w);
+
+/* ------------------------------------------------------------------------
+ * Cora binary export -- replaces load_cora_binary (src/model.cpp:49-129).
+ * tg_cora_open reads the file on the host (errors as the reference:
+ * "load_cora_binary: cannot open <path>", "load_cora_binary: unexpected end
+ * of file or read error.").  tg_cora_upload copies the features to the
+ * device ([num_nodes x num_features]) and builds the adjacency there
+ * (row_ptr[num_nodes + 1], col_ind / val[num_edges]): rows = sources,
+ * destinations sorted, duplicates kept, values 1.0f, then the checks of
+ * Tensor::sparse_csr (an out-of-range destination raises
+ * "Tensor::sparse_csr: col_ind[k] = ..." at its sorted position, as in the
+ * reference).  A source outside [0, num_nodes), undefined behaviour in the
+ * reference, raises std::invalid_argument.  tg_cora_host's arrays are host
+ * memory owned by the handle.
+ * ------------------------------------------------------------------------ */
+typedef struct tg_cora_s* tg_cora_t;
+int tg_cora_open(const char* path, tg_cora_t* out);
+int tg_cora_info(tg_cora_t c, int64_t* num_nodes, int64_t* num_features,
+                 int64_t* num_classes, int64_t* num_edges);
+int tg_cora_host(tg_cora_t c, const int32_t** labels, const uint8_t** train_mask,
+                 const uint8_t** val_mask, const uint8_t** test_mask);
+int tg_cora_upload(tg_cora_t c, float* features, int32_t* row_ptr, int32_t* col_ind,
+                   float* val, tg_stream_t stream);
+int tg_cora_destroy(tg_cora_t c);
+
 #ifdef __cplusplus
 }
 #endif

@@ -107,11 +107,40 @@ class _Restate:
             "or_gat_scores": (None, [_i64, _i64, _p, _p, _p, _p, _p]),
             "or_gat_forward": (None, [_i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
                                       _p, _f32, _i32, _i32, _p]),
+            "or_parse_edges": (_i32, [_p, _i64, C.c_char_p, _p, _p, _i64, C.POINTER(_i64)]),
+            "or_parse_features": (_i32, [_p, _i64, C.c_char_p, _p, _i64, C.POINTER(_i64),
+                                         C.POINTER(_i64)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+
+    # -- CSV ingestion (graph_loader.cpp:61-206), over bytes ------------------
+    def parse_edges(self, text: bytes, name: str = ""):
+        """(src, dst) int32 arrays; raises OracleError('runtime_error', msg)."""
+        t = np.frombuffer(bytes(text), np.uint8).copy()
+        cap = int(text.count(b"\n")) + 1
+        src = np.zeros(cap, np.int32)
+        dst = np.zeros(cap, np.int32)
+        cnt = _i64()
+        rc = self.L.or_parse_edges(_ptr(t), len(text), name.encode(), _ptr(src), _ptr(dst), cap,
+                                   C.byref(cnt))
+        if rc:
+            raise OracleError("runtime_error", self.L.or_last_error().decode("latin-1"))
+        return src[:cnt.value].copy(), dst[:cnt.value].copy()
+
+    def parse_features(self, text: bytes, name: str = "") -> np.ndarray:
+        t = np.frombuffer(bytes(text), np.uint8).copy()
+        rows, cols = _i64(), _i64()
+        rc = self.L.or_parse_features(_ptr(t), len(text), name.encode(), None, 0, C.byref(rows),
+                                      C.byref(cols))
+        if rc:
+            raise OracleError("runtime_error", self.L.or_last_error().decode("latin-1"))
+        out = np.zeros((rows.value, cols.value), np.float32)
+        self.L.or_parse_features(_ptr(t), len(text), name.encode(), _ptr(out), out.size,
+                                 C.byref(rows), C.byref(cols))
+        return out
 
     def set_num_threads(self, n: int) -> None:
         self.L.or_set_num_threads(int(n))
@@ -362,6 +391,27 @@ class _Reference:
             "ref_model_load_weights": (_i32, [_p]),
             "ref_model_forward": (_i32, [_p, _p, _p, C.POINTER(_i64), C.POINTER(_i64), _p,
                                          _i64]),
+            "ref_parse_edges": (_p, [C.c_char_p, C.POINTER(_i32)]),
+            "ref_edges_count": (_i64, [_p]),
+            "ref_edges_read": (None, [_p, _p, _p]),
+            "ref_edges_free": (None, [_p]),
+            "ref_parse_features": (_p, [C.c_char_p, C.POINTER(_i32)]),
+            "ref_graph_load": (_p, [C.c_char_p, C.c_char_p, C.POINTER(_i32)]),
+            "ref_graph_adjacency": (_p, [_p]),
+            "ref_graph_features": (_p, [_p]),
+            "ref_graph_counts": (None, [_p, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64)]),
+            "ref_graph_free": (None, [_p]),
+            "ref_load_cora": (_p, [C.c_char_p, C.POINTER(_i32)]),
+            "ref_cora_counts": (None, [_p] + [C.POINTER(_i64)] * 4),
+            "ref_cora_adjacency": (_p, [_p]),
+            "ref_cora_features": (_p, [_p]),
+            "ref_cora_read": (None, [_p, _p, _p, _p, _p]),
+            "ref_cora_free": (None, [_p]),
+            "ref_load_weight_file": (_p, [C.c_char_p, C.POINTER(_i32)]),
+            "ref_weights_accuracy": (_f32, [_p]),
+            "ref_weights_names": (_i64, [_p, _p, _i64]),
+            "ref_weights_tensor": (_p, [_p, C.c_char_p]),
+            "ref_weights_free": (None, [_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -371,6 +421,86 @@ class _Reference:
     def _check(self, rc):
         if rc:
             raise OracleError(_KINDS.get(rc, "exception"), self.L.ref_last_error().decode())
+
+    def _opened(self, h, code):
+        if not h:
+            raise OracleError(_KINDS.get(code.value, "exception"),
+                              self.L.ref_last_error().decode("latin-1"))
+        return h
+
+    def _dense_of(self, t) -> np.ndarray:
+        """Copies a borrowed dense Tensor handle out."""
+        L = self.L
+        out = np.zeros((L.ref_tensor_rows(t), L.ref_tensor_cols(t)), np.float32)
+        L.ref_tensor_read(t, None, None, _ptr(out))
+        return out
+
+    def _csr_of(self, t) -> CSR:
+        L = self.L
+        r, c, nnz = L.ref_tensor_rows(t), L.ref_tensor_cols(t), L.ref_tensor_nnz(t)
+        rp, ci, v = np.zeros(r + 1, np.int32), np.zeros(nnz, np.int32), np.zeros(nnz, np.float32)
+        L.ref_tensor_read(t, _ptr(rp), _ptr(ci), _ptr(v))
+        return CSR(r, c, rp, ci, v)
+
+    # -- file ingestion (graph_loader.cpp:61-326, model.cpp:49-185) ----------
+    def parse_edges_file(self, path: str):
+        code = _i32()
+        h = self._opened(self.L.ref_parse_edges(path.encode(), C.byref(code)), code)
+        n = self.L.ref_edges_count(h)
+        src, dst = np.zeros(n, np.int32), np.zeros(n, np.int32)
+        self.L.ref_edges_read(h, _ptr(src), _ptr(dst))
+        self.L.ref_edges_free(h)
+        return src, dst
+
+    def parse_features_file(self, path: str) -> np.ndarray:
+        code = _i32()
+        h = self._opened(self.L.ref_parse_features(path.encode(), C.byref(code)), code)
+        out = self._dense_of(h)
+        self.L.ref_tensor_free(h)
+        return out
+
+    def load_graph(self, edges_path: str, features_path: str):
+        """(adjacency CSR, features, (num_nodes, num_edges, num_features))."""
+        code = _i32()
+        g = self._opened(self.L.ref_graph_load(edges_path.encode(), features_path.encode(),
+                                               C.byref(code)), code)
+        n, e, f = _i64(), _i64(), _i64()
+        self.L.ref_graph_counts(g, C.byref(n), C.byref(e), C.byref(f))
+        adj = self._csr_of(self.L.ref_graph_adjacency(g))
+        x = self._dense_of(self.L.ref_graph_features(g))
+        self.L.ref_graph_free(g)
+        return adj, x, (n.value, e.value, f.value)
+
+    def load_cora(self, path: str) -> dict:
+        code = _i32()
+        h = self._opened(self.L.ref_load_cora(path.encode(), C.byref(code)), code)
+        cnt = [_i64() for _ in range(4)]
+        self.L.ref_cora_counts(h, *[C.byref(c) for c in cnt])
+        n = cnt[0].value
+        labels = np.zeros(n, np.int32)
+        masks = [np.zeros(n, np.uint8) for _ in range(3)]
+        self.L.ref_cora_read(h, _ptr(labels), *[_ptr(m) for m in masks])
+        out = dict(num_nodes=n, num_features=cnt[1].value, num_classes=cnt[2].value,
+                   num_edges=cnt[3].value, adjacency=self._csr_of(self.L.ref_cora_adjacency(h)),
+                   features=self._dense_of(self.L.ref_cora_features(h)), labels=labels,
+                   train_mask=masks[0], val_mask=masks[1], test_mask=masks[2])
+        self.L.ref_cora_free(h)
+        return out
+
+    def load_weight_file(self, path: str):
+        """(test_accuracy, {name: float32 array})."""
+        code = _i32()
+        h = self._opened(self.L.ref_load_weight_file(path.encode(), C.byref(code)), code)
+        need = self.L.ref_weights_names(h, None, 0)
+        buf = C.create_string_buffer(int(need))
+        self.L.ref_weights_names(h, C.cast(buf, _p), need)
+        names = ([s for s in buf.value.decode("utf-8", "surrogateescape").split("\n") if s]
+                 if need > 1 else [])
+        tensors = {nm: self._dense_of(self.L.ref_weights_tensor(h, nm.encode("utf-8", "surrogateescape")))
+                   for nm in names}
+        acc = float(self.L.ref_weights_accuracy(h))
+        self.L.ref_weights_free(h)
+        return acc, tensors
 
     def _handle(self, h):
         if not h:

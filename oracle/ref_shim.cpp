@@ -300,4 +300,93 @@ int ref_model_forward(void* m, void* adj, void* x, int64_t* out_rows, int64_t* o
     });
 }
 
+// --- file ingestion (graph_loader.cpp:61-326, model.cpp:49-185) -----------
+// Handle-returning entry points store the guard's code in *code.
+struct RefEdges {
+    std::vector<std::pair<int32_t, int32_t>> e;
+};
+
+void* ref_parse_edges(const char* path, int* code) {
+    RefEdges* r = nullptr;
+    *code = guard([&] { r = new RefEdges{GraphLoader::parse_edges(path)}; });
+    return r;
+}
+int64_t ref_edges_count(void* h) { return static_cast<int64_t>(static_cast<RefEdges*>(h)->e.size()); }
+void ref_edges_read(void* h, int32_t* src, int32_t* dst) {
+    const auto& e = static_cast<RefEdges*>(h)->e;
+    for (size_t i = 0; i < e.size(); ++i) {
+        src[i] = e[i].first;
+        dst[i] = e[i].second;
+    }
+}
+void ref_edges_free(void* h) { delete static_cast<RefEdges*>(h); }
+
+void* ref_parse_features(const char* path, int* code) {
+    Tensor* t = nullptr;
+    *code = guard([&] { t = new Tensor(GraphLoader::parse_features(path)); });
+    return t;
+}
+
+void* ref_graph_load(const char* edges_path, const char* features_path, int* code) {
+    GraphData* g = nullptr;
+    *code = guard([&] { g = new GraphData(GraphLoader::load(edges_path, features_path)); });
+    return g;
+}
+void* ref_graph_adjacency(void* g) { return &static_cast<GraphData*>(g)->adjacency; }
+void* ref_graph_features(void* g) { return &static_cast<GraphData*>(g)->node_features; }
+void ref_graph_counts(void* g, int64_t* nodes, int64_t* edges, int64_t* features) {
+    const GraphData& d = *static_cast<GraphData*>(g);
+    *nodes = static_cast<int64_t>(d.num_nodes);
+    *edges = static_cast<int64_t>(d.num_edges);
+    *features = static_cast<int64_t>(d.num_features);
+}
+void ref_graph_free(void* g) { delete static_cast<GraphData*>(g); }
+
+void* ref_load_cora(const char* path, int* code) {
+    CoraData* c = nullptr;
+    *code = guard([&] { c = new CoraData(load_cora_binary(path)); });
+    return c;
+}
+void ref_cora_counts(void* h, int64_t* nodes, int64_t* features, int64_t* classes,
+                     int64_t* edges) {
+    const CoraData& c = *static_cast<CoraData*>(h);
+    *nodes = static_cast<int64_t>(c.num_nodes);
+    *features = static_cast<int64_t>(c.num_features);
+    *classes = static_cast<int64_t>(c.num_classes);
+    *edges = static_cast<int64_t>(c.num_edges);
+}
+void* ref_cora_adjacency(void* h) { return &static_cast<CoraData*>(h)->adjacency; }
+void* ref_cora_features(void* h) { return &static_cast<CoraData*>(h)->features; }
+void ref_cora_read(void* h, int32_t* labels, uint8_t* train, uint8_t* val, uint8_t* test) {
+    const CoraData& c = *static_cast<CoraData*>(h);
+    std::memcpy(labels, c.labels.data(), c.labels.size() * sizeof(int32_t));
+    std::memcpy(train, c.train_mask.data(), c.train_mask.size());
+    std::memcpy(val, c.val_mask.data(), c.val_mask.size());
+    std::memcpy(test, c.test_mask.data(), c.test_mask.size());
+}
+void ref_cora_free(void* h) { delete static_cast<CoraData*>(h); }
+
+void* ref_load_weight_file(const char* path, int* code) {
+    WeightFile* w = nullptr;
+    *code = guard([&] { w = new WeightFile(load_weight_file(path)); });
+    return w;
+}
+float ref_weights_accuracy(void* h) { return static_cast<WeightFile*>(h)->test_accuracy; }
+// Tensor names joined by '\n' into buf (cap bytes); returns the needed size.
+int64_t ref_weights_names(void* h, char* buf, int64_t cap) {
+    std::string all;
+    for (const auto& kv : static_cast<WeightFile*>(h)->tensors) {
+        if (!all.empty()) all += '\n';
+        all += kv.first;
+    }
+    if (buf && cap > static_cast<int64_t>(all.size())) std::memcpy(buf, all.c_str(), all.size() + 1);
+    return static_cast<int64_t>(all.size()) + 1;
+}
+void* ref_weights_tensor(void* h, const char* name) {
+    auto& t = static_cast<WeightFile*>(h)->tensors;
+    auto it = t.find(name);
+    return it == t.end() ? nullptr : &it->second;
+}
+void ref_weights_free(void* h) { delete static_cast<WeightFile*>(h); }
+
 }  // extern "C"

@@ -11,13 +11,15 @@
  */
 #include "tg_oracle.h"
 
+#include <errno.h>
+#include <limits.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <omp.h>
 
-static __thread char g_err[512];
+static __thread char g_err[8192];
 
 const char* or_last_error(void) { return g_err; }
 
@@ -543,4 +545,266 @@ void or_gat_forward(int64_t n, int64_t f_in, int64_t f_out,
     free(dst);
     if (use_bias) or_add_bias(n, f_out, out, bias);
     if (act == 1) or_relu(n * f_out, out);
+}
+
+/* ------------------------------------------------------------------------
+ * graph_loader.cpp:14-206  CSV parsing, over an in-memory text.
+ *   read_lines  :38-53   std::getline at '\n', trim " \t\r\n", skip empty
+ *   is_header   :24-33   a letter or '_' before the first ',' ' ' '\t'
+ *   parse_edges :61-107  first ',' splits; std::stoi of both sides
+ *   parse_features :112-206  std::getline(ss, token, ','); stoi(trim(id)),
+ *               stof(trim(feature)); the first data line fixes the count;
+ *               rows placed by node_id, later lines overwriting earlier
+ * std::stoi / std::stof are libstdc++'s: strtol(c_str, &end, 10) /
+ * strtof(c_str, &end); nothing converted -> invalid_argument, errno ERANGE
+ * (or a long outside int for stoi) -> out_of_range.  Fields are copied into
+ * NUL-terminated buffers, so a NUL byte ends them as it ends c_str().
+ * All errors are std::runtime_error in the reference (return 2 here).
+ * ------------------------------------------------------------------------ */
+typedef struct {
+    int64_t b, e;
+} or_span;
+
+static int or_is_trim(unsigned char c) { return c == ' ' || c == '\t' || c == '\r' || c == '\n'; }
+
+/* Non-empty trimmed lines; *count receives their number.  Caller frees. */
+static or_span* or_read_lines(const char* t, int64_t n, int64_t* count) {
+    int64_t cap = 1;
+    for (int64_t i = 0; i < n; ++i) cap += t[i] == '\n';
+    or_span* s = (or_span*)malloc(sizeof(or_span) * (size_t)cap);
+    int64_t k = 0, b = 0;
+    while (b < n) {
+        const char* nl = (const char*)memchr(t + b, '\n', (size_t)(n - b));
+        int64_t e = nl ? (int64_t)(nl - t) : n;
+        const int64_t next = nl ? e + 1 : n;
+        int64_t lb = b, le = e;
+        while (lb < le && or_is_trim((unsigned char)t[lb])) ++lb;
+        while (le > lb && or_is_trim((unsigned char)t[le - 1])) --le;
+        if (lb < le) {
+            s[k].b = lb;
+            s[k].e = le;
+            ++k;
+        }
+        b = next;
+    }
+    *count = k;
+    return s;
+}
+
+static int or_is_header(const char* t, or_span s) {
+    for (int64_t p = s.b; p < s.e; ++p) {
+        const unsigned char c = (unsigned char)t[p];
+        if (c == ',' || c == ' ' || c == '\t') break;
+        if (((c | 0x20) >= 'a' && (c | 0x20) <= 'z') || c == '_') return 1;
+    }
+    return 0;
+}
+
+/* [b, e) as a NUL-terminated copy; trimmed of " \t\r\n" when trim != 0. */
+static char* or_field(const char* t, int64_t b, int64_t e, int trim) {
+    if (trim) {
+        while (b < e && or_is_trim((unsigned char)t[b])) ++b;
+        while (e > b && or_is_trim((unsigned char)t[e - 1])) --e;
+    }
+    char* f = (char*)malloc((size_t)(e - b) + 1);
+    memcpy(f, t + b, (size_t)(e - b));
+    f[e - b] = '\0';
+    return f;
+}
+
+static int or_stoi(const char* s, int32_t* out) {
+    char* end;
+    errno = 0;
+    const long v = strtol(s, &end, 10);
+    if (end == s) return 1;
+    if (errno == ERANGE || v < INT_MIN || v > INT_MAX) return 2;
+    *out = (int32_t)v;
+    return 0;
+}
+
+static int or_stof(const char* s, float* out) {
+    char* end;
+    errno = 0;
+    const float v = strtof(s, &end);
+    if (end == s) return 1;
+    if (errno == ERANGE) return 2;
+    *out = v;
+    return 0;
+}
+
+/* Appends the first `len` bytes of t[b..] (NULs included) to msg. */
+static void or_err_line(const char* prefix, const char* t, int64_t b, int64_t e,
+                        const char* suffix) {
+    size_t k = (size_t)snprintf(g_err, sizeof g_err, "%s", prefix);
+    for (int64_t p = b; p < e && k + 1 < sizeof g_err; ++p) g_err[k++] = t[p];
+    g_err[k < sizeof g_err ? k : sizeof g_err - 1] = '\0';
+    strncat(g_err, suffix, sizeof g_err - strlen(g_err) - 1);
+}
+
+int or_parse_edges(const char* text, int64_t n, const char* name, int32_t* src,
+                   int32_t* dst, int64_t cap, int64_t* n_out) {
+    int64_t nl;
+    or_span* L = or_read_lines(text, n, &nl);
+    int rc = 0;
+    int64_t cnt = 0;
+    if (nl == 0) {
+        snprintf(g_err, sizeof g_err, "GraphLoader::parse_edges: file is empty: '%s'", name);
+        rc = 2;
+        goto done;
+    }
+    for (int64_t i = or_is_header(text, L[0]); i < nl; ++i) {
+        const char* c = (const char*)memchr(text + L[i].b, ',', (size_t)(L[i].e - L[i].b));
+        char pre[128];
+        if (!c) {
+            snprintf(pre, sizeof pre, "GraphLoader::parse_edges: malformed line %lld: '",
+                     (long long)(i + 1));
+            or_err_line(pre, text, L[i].b, L[i].e, "'");
+            rc = 2;
+            goto done;
+        }
+        const int64_t ci = (int64_t)(c - text);
+        char* f1 = or_field(text, L[i].b, ci, 0);
+        char* f2 = or_field(text, ci + 1, L[i].e, 0);
+        int32_t s = 0, d = 0;
+        const int r1 = or_stoi(f1, &s);
+        const int r2 = r1 ? 0 : or_stoi(f2, &d);
+        free(f1);
+        free(f2);
+        if (r1 || r2) {
+            snprintf(pre, sizeof pre, "GraphLoader::parse_edges: invalid integer on line %lld: '",
+                     (long long)(i + 1));
+            or_err_line(pre, text, L[i].b, L[i].e, "'");
+            rc = 2;
+            goto done;
+        }
+        if (s < 0 || d < 0) {
+            snprintf(g_err, sizeof g_err,
+                     "GraphLoader::parse_edges: negative node ID on line %lld: src=%d, dst=%d",
+                     (long long)(i + 1), s, d);
+            rc = 2;
+            goto done;
+        }
+        if (cnt < cap) {
+            src[cnt] = s;
+            dst[cnt] = d;
+        }
+        ++cnt;
+    }
+done:
+    free(L);
+    *n_out = cnt;
+    return rc;
+}
+
+int or_parse_features(const char* text, int64_t n, const char* name, float* out,
+                      int64_t cap, int64_t* rows_out, int64_t* cols_out) {
+    int64_t nl;
+    or_span* L = or_read_lines(text, n, &nl);
+    int rc = 0;
+    int64_t num_features = 0, nd = 0;
+    int32_t max_id = -1;
+    int32_t* ids = NULL;
+    float* feats = NULL;
+    *rows_out = 0;
+    *cols_out = 0;
+    if (nl == 0) {
+        snprintf(g_err, sizeof g_err, "GraphLoader::parse_features: file is empty: '%s'", name);
+        rc = 2;
+        goto done;
+    }
+    const int64_t start = or_is_header(text, L[0]);
+    nd = nl - start;
+    if (nd == 0) {
+        snprintf(g_err, sizeof g_err, "GraphLoader::parse_features: no data rows in '%s'", name);
+        rc = 2;
+        goto done;
+    }
+    ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)nd);
+    size_t fcap = 1024, fused = 0;
+    feats = (float*)malloc(sizeof(float) * fcap);
+    for (int64_t i = start; i < nl; ++i) {
+        char pre[160];
+        /* first token: node_id */
+        int64_t p = L[i].b;
+        const char* c = (const char*)memchr(text + p, ',', (size_t)(L[i].e - p));
+        int64_t te = c ? (int64_t)(c - text) : L[i].e;
+        char* tok = or_field(text, p, te, 1);
+        int32_t id = 0;
+        const int r = or_stoi(tok, &id);
+        free(tok);
+        if (r) {
+            snprintf(pre, sizeof pre, "GraphLoader::parse_features: invalid node_id on line %lld: '",
+                     (long long)(i + 1));
+            or_err_line(pre, text, p, te, "'");
+            rc = 2;
+            goto done;
+        }
+        if (id < 0) {
+            snprintf(g_err, sizeof g_err, "GraphLoader::parse_features: negative node_id on line %lld",
+                     (long long)(i + 1));
+            rc = 2;
+            goto done;
+        }
+        if (id > max_id) max_id = id;
+        p = c ? te + 1 : L[i].e;
+        int64_t k = 0;
+        const size_t row0 = fused;
+        while (p < L[i].e) { /* std::getline(ss, token, ',') until nothing is left */
+            c = (const char*)memchr(text + p, ',', (size_t)(L[i].e - p));
+            te = c ? (int64_t)(c - text) : L[i].e;
+            tok = or_field(text, p, te, 1);
+            float v = 0.0f;
+            const int rf = or_stof(tok, &v);
+            free(tok);
+            if (rf) {
+                snprintf(pre, sizeof pre,
+                         "GraphLoader::parse_features: invalid feature on line %lld: '",
+                         (long long)(i + 1));
+                or_err_line(pre, text, p, te, "'");
+                rc = 2;
+                goto done;
+            }
+            if (fused == fcap) {
+                fcap *= 2;
+                feats = (float*)realloc(feats, sizeof(float) * fcap);
+            }
+            feats[fused++] = v;
+            ++k;
+            p = c ? te + 1 : L[i].e;
+        }
+        if (num_features == 0) {
+            num_features = k;
+            if (num_features == 0) {
+                snprintf(g_err, sizeof g_err, "GraphLoader::parse_features: no features on line %lld",
+                         (long long)(i + 1));
+                rc = 2;
+                goto done;
+            }
+        } else if (k != num_features) {
+            snprintf(g_err, sizeof g_err,
+                     "GraphLoader::parse_features: inconsistent feature count on line %lld: "
+                     "expected %lld but got %lld",
+                     (long long)(i + 1), (long long)num_features, (long long)k);
+            rc = 2;
+            goto done;
+        }
+        (void)row0;
+        ids[i - start] = id;
+    }
+    {
+        const int64_t rows = (int64_t)max_id + 1;
+        *rows_out = rows;
+        *cols_out = num_features;
+        if (out && cap >= rows * num_features) {
+            memset(out, 0, sizeof(float) * (size_t)(rows * num_features));
+            for (int64_t d = 0; d < nd; ++d)
+                memcpy(out + (int64_t)ids[d] * num_features, feats + d * num_features,
+                       sizeof(float) * (size_t)num_features);
+        }
+    }
+done:
+    free(ids);
+    free(feats);
+    free(L);
+    return rc;
 }

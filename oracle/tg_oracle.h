@@ -101,6 +101,18 @@ void or_gat_forward(int64_t n, int64_t f_in, int64_t f_out,
                     const float* bias, float slope, int use_bias, int act,
                     float* out);
 
+/* graph_loader.cpp:61-107 -- GraphLoader::parse_edges over an in-memory
+ * text (name is used in messages).  Writes up to cap edges; *n_out receives
+ * the count.  Returns 2 (std::runtime_error) on the reference's errors. */
+int or_parse_edges(const char* text, int64_t n, const char* name, int32_t* src,
+                   int32_t* dst, int64_t cap, int64_t* n_out);
+
+/* graph_loader.cpp:112-206 -- GraphLoader::parse_features over an
+ * in-memory text.  *rows_out x *cols_out is the table's shape; out is
+ * written when it holds at least that many floats (else only the shape). */
+int or_parse_features(const char* text, int64_t n, const char* name, float* out,
+                      int64_t cap, int64_t* rows_out, int64_t* cols_out);
+
 /* OpenMP thread count for the parallel loops (<= 0 keeps the default). */
 void or_set_num_threads(int n);
 int or_get_num_threads(void);

@@ -11,6 +11,7 @@ every call raises.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from dataclasses import dataclass
 
 from ._lib import InvalidArgument, NativeLibraryMissing, OutOfRange, TgError, lib  # noqa: F401
@@ -377,7 +378,16 @@ class Model:
         lib.check(lib.tg_model_set_tensor(self.h, name.encode(), a.shape[0], a.shape[1],
                                           a.ctypes.data_as(C.c_void_p)))
 
-    def load_weights(self, weights: dict | None = None) -> None:
+    def load_weights(self, weights=None) -> None:
+        """Model::load_weights (model.cpp:252-305).  ``weights`` is a dict of
+        name -> array, a :class:`WeightFile`, or the path of a TGNN weight
+        file (model.cpp:252-255).  Only the given tensors are looked up, as
+        the reference looks up only the WeightFile it is given."""
+        if isinstance(weights, (str, bytes)) or hasattr(weights, "__fspath__"):
+            weights = load_weight_file(weights)
+        if isinstance(weights, WeightFile):
+            weights = weights.tensors
+        lib.check(lib.tg_model_clear_tensors(self.h))
         for k, v in (weights or {}).items():
             self.set_tensor(k, v)
         lib.check(lib.tg_model_load_weights(self.h))
@@ -432,3 +442,234 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------
+# Ingestion: CSV graphs (GraphLoader, graph_loader.cpp:61-326), the TGNN
+# weight file (model.cpp:134-185) and the Cora binary (model.cpp:49-129).
+# ---------------------------------------------------------------------------
+class CsvText:
+    """A CSV text indexed into lines on the device (tg_csv_open / tg_csv_index).
+
+    ``CsvText.open(path)`` reads the file into device memory;
+    ``CsvText.from_device(u8_tensor, name)`` indexes bytes already there (the
+    tensor is kept alive with the handle)."""
+
+    def __init__(self, handle, keep=None):
+        self.h = handle
+        self._keep = keep
+        n, hdr = C.c_int64(), C.c_int()
+        lib.check(lib.tg_csv_info(self.h, C.byref(n), C.byref(hdr)))
+        self.n_lines, self.has_header = int(n.value), bool(hdr.value)
+
+    @classmethod
+    def open(cls, path, stream=None) -> "CsvText":
+        h = C.c_void_p()
+        lib.check(lib.tg_csv_open(os.fsencode(path), C.byref(h), stream_handle(stream)))
+        return cls(h)
+
+    @classmethod
+    def from_device(cls, text, name: str = "", stream=None) -> "CsvText":
+        torch = _torch()
+        if text.dtype != torch.uint8 or not text.is_contiguous():
+            raise ValueError("CsvText.from_device expects a contiguous uint8 device tensor")
+        h = C.c_void_p()
+        lib.check(lib.tg_csv_index(dptr(text), text.numel(), name.encode(), C.byref(h),
+                                   stream_handle(stream)))
+        return cls(h, keep=text)
+
+    @property
+    def n_data(self) -> int:
+        return self.n_lines - int(self.has_header)
+
+    def parse_edges(self, device=None, stream=None):
+        """GraphLoader::parse_edges (graph_loader.cpp:61-107): (src, dst,
+        max_id) with int32 device tensors of one entry per data line."""
+        torch = _torch()
+        device = device or torch.device("cuda", torch.cuda.current_device())
+        n = max(self.n_data, 0)
+        src = torch.empty(max(n, 1), dtype=torch.int32, device=device)[:n]
+        dst = torch.empty(max(n, 1), dtype=torch.int32, device=device)[:n]
+        mx = C.c_int64()
+        lib.check(lib.tg_csv_parse_edges(self.h, src.data_ptr(), dst.data_ptr(), C.byref(mx),
+                                         stream_handle(stream)))
+        return src, dst, int(mx.value)
+
+    def feature_shape(self, stream=None):
+        rows, cols = C.c_int64(), C.c_int64()
+        lib.check(lib.tg_csv_feature_shape(self.h, C.byref(rows), C.byref(cols),
+                                           stream_handle(stream)))
+        return int(rows.value), int(cols.value)
+
+    def parse_features(self, n_rows: int | None = None, device=None, stream=None):
+        """GraphLoader::parse_features (graph_loader.cpp:112-206): a
+        [rows x cols] float32 device tensor (``n_rows`` > rows zero-pads)."""
+        torch = _torch()
+        device = device or torch.device("cuda", torch.cuda.current_device())
+        rows, cols = self.feature_shape(stream)
+        n_rows = rows if n_rows is None else int(n_rows)
+        out = torch.empty((n_rows, cols), dtype=torch.float32, device=device)
+        lib.check(lib.tg_csv_parse_features(self.h, out.data_ptr() if out.numel() else None,
+                                            n_rows, cols, stream_handle(stream)))
+        return out
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            lib.tg_csv_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def parse_edges(path, stream=None):
+    """GraphLoader::parse_edges on the device: (src, dst) int32 tensors."""
+    t = CsvText.open(path, stream)
+    try:
+        src, dst, _ = t.parse_edges(stream=stream)
+        return src, dst
+    finally:
+        t.close()
+
+
+def parse_features(path, stream=None):
+    """GraphLoader::parse_features on the device: [rows x cols] float32."""
+    t = CsvText.open(path, stream)
+    try:
+        return t.parse_features(stream=stream)
+    finally:
+        t.close()
+
+
+@dataclass
+class GraphData:
+    """GraphData (graph_loader.hpp:17-23): adjacency (values 1.0) and
+    features, both on the device."""
+    adjacency: DeviceCSR
+    node_features: object
+    num_nodes: int
+    num_edges: int
+    num_features: int
+
+
+def load_graph(edges_path, features_path, stream=None) -> GraphData:
+    """GraphLoader::load (graph_loader.cpp:286-326): edges, then features,
+    num_nodes = max(largest endpoint + 1, feature rows), the CSR built on the
+    device and the features zero-padded to num_nodes rows."""
+    te = CsvText.open(edges_path, stream)
+    try:
+        src, dst, max_id = te.parse_edges(stream=stream)
+    finally:
+        te.close()
+    tf = CsvText.open(features_path, stream)
+    try:
+        rows, cols = tf.feature_shape(stream)
+        n_edges = int(src.numel())
+        num_nodes = max(max_id + 1 if n_edges else 0, rows)
+        x = tf.parse_features(n_rows=num_nodes, stream=stream)
+    finally:
+        tf.close()
+    adj = edge_list_to_csr(src, dst, num_nodes, stream=stream)
+    return GraphData(adj, x, num_nodes, n_edges, cols)
+
+
+@dataclass
+class WeightFile:
+    """WeightFile (model.hpp:76-79): test accuracy and named host tensors."""
+    test_accuracy: float
+    tensors: dict
+
+
+def load_weight_file(path) -> WeightFile:
+    """load_weight_file (model.cpp:134-185), read by the native library."""
+    import numpy as np
+    h = C.c_void_p()
+    lib.check(lib.tg_weights_open(os.fsencode(path), C.byref(h)))
+    try:
+        n, acc = C.c_int64(), C.c_float()
+        lib.check(lib.tg_weights_info(h, C.byref(n), C.byref(acc)))
+        tensors = {}
+        for i in range(n.value):
+            name, nlen, rows, cols, data = (C.c_void_p(), C.c_int64(), C.c_int64(), C.c_int64(),
+                                            C.c_void_p())
+            lib.check(lib.tg_weights_tensor(h, i, C.byref(name), C.byref(nlen), C.byref(rows),
+                                            C.byref(cols), C.byref(data)))
+            key = C.string_at(name.value, nlen.value).decode("utf-8", "surrogateescape")
+            count = rows.value * cols.value
+            arr = np.empty((rows.value, cols.value), np.float32)
+            if count:
+                C.memmove(arr.ctypes.data, data.value, count * 4)
+            tensors[key] = arr
+        return WeightFile(float(acc.value), tensors)
+    finally:
+        lib.tg_weights_destroy(h)
+
+
+def save_weight_file(path, tensors: dict, test_accuracy: float = 0.0) -> None:
+    """Writes a TGNN weight file, version 1 (model.hpp:22-33): the format
+    load_weight_file reads.  Tensors are 2-D float32 (1-D arrays are written
+    as one row), in the dict's order."""
+    import struct
+    import numpy as np
+    with open(path, "wb") as f:
+        f.write(b"TGNN")
+        f.write(struct.pack("<IfI", 1, float(test_accuracy), len(tensors)))
+        for name, arr in tensors.items():
+            a = np.ascontiguousarray(arr, dtype="<f4")
+            if a.ndim == 1:
+                a = a.reshape(1, -1)
+            if a.ndim != 2:
+                raise ValueError(f"{name}: expected a 1-D or 2-D array")
+            nb = name.encode("utf-8", "surrogateescape")
+            f.write(struct.pack("<I", len(nb)) + nb + struct.pack("<II", *a.shape))
+            f.write(a.tobytes())
+
+
+@dataclass
+class CoraData:
+    """CoraData (model.hpp:50-62): the graph on the device, labels and masks
+    on the host."""
+    num_nodes: int
+    num_features: int
+    num_classes: int
+    num_edges: int
+    adjacency: DeviceCSR
+    features: object
+    labels: object
+    train_mask: object
+    val_mask: object
+    test_mask: object
+
+
+def load_cora_binary(path, stream=None) -> CoraData:
+    """load_cora_binary (model.cpp:49-129): the file read by the native
+    library, features uploaded, adjacency built on the device."""
+    import numpy as np
+    torch = _torch()
+    dev = torch.device("cuda", torch.cuda.current_device())
+    h = C.c_void_p()
+    lib.check(lib.tg_cora_open(os.fsencode(path), C.byref(h)))
+    try:
+        n, f, c, e = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int64()
+        lib.check(lib.tg_cora_info(h, C.byref(n), C.byref(f), C.byref(c), C.byref(e)))
+        n, f, c, e = n.value, f.value, c.value, e.value
+        x = torch.empty((n, f), dtype=torch.float32, device=dev)
+        rp = torch.empty(n + 1, dtype=torch.int32, device=dev)
+        ci = torch.empty(max(e, 1), dtype=torch.int32, device=dev)[:e]
+        v = torch.empty(max(e, 1), dtype=torch.float32, device=dev)[:e]
+        lib.check(lib.tg_cora_upload(h, x.data_ptr() if x.numel() else None, rp.data_ptr(),
+                                     ci.data_ptr(), v.data_ptr(), stream_handle(stream)))
+        ptrs = [C.c_void_p() for _ in range(4)]
+        lib.check(lib.tg_cora_host(h, *[C.byref(p) for p in ptrs]))
+        labels = np.empty(n, np.int32)
+        masks = [np.empty(n, np.uint8) for _ in range(3)]
+        if n:
+            C.memmove(labels.ctypes.data, ptrs[0].value, n * 4)
+            for m, p in zip(masks, ptrs[1:]):
+                C.memmove(m.ctypes.data, p.value, n)
+        return CoraData(n, f, c, e, DeviceCSR(n, n, rp, ci, v), x, labels, *masks)
+    finally:
+        lib.tg_cora_destroy(h)

@@ -101,6 +101,22 @@ SIGNATURES = {
     "tg_model_set_sage_dataflow": (i32, [vp, i32]),
     "tg_model_set_precision": (i32, [vp, i32]),
     "tg_model_forward": (i32, [vp, i64, i64, vp, vp, vp, i64, vp, vp, i32, vp]),
+    "tg_csv_open": (i32, [C.c_char_p, C.POINTER(vp), vp]),
+    "tg_csv_index": (i32, [vp, i64, C.c_char_p, C.POINTER(vp), vp]),
+    "tg_csv_destroy": (i32, [vp]),
+    "tg_csv_info": (i32, [vp, pi64, C.POINTER(i32)]),
+    "tg_csv_parse_edges": (i32, [vp, vp, vp, pi64, vp]),
+    "tg_csv_feature_shape": (i32, [vp, pi64, pi64, vp]),
+    "tg_csv_parse_features": (i32, [vp, vp, i64, i64, vp]),
+    "tg_weights_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "tg_weights_info": (i32, [vp, pi64, C.POINTER(f32)]),
+    "tg_weights_tensor": (i32, [vp, i64, C.POINTER(vp), pi64, pi64, pi64, C.POINTER(vp)]),
+    "tg_weights_destroy": (i32, [vp]),
+    "tg_cora_open": (i32, [C.c_char_p, C.POINTER(vp)]),
+    "tg_cora_info": (i32, [vp, pi64, pi64, pi64, pi64]),
+    "tg_cora_host": (i32, [vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), C.POINTER(vp)]),
+    "tg_cora_upload": (i32, [vp, vp, vp, vp, vp, vp]),
+    "tg_cora_destroy": (i32, [vp]),
 }
 
 

@@ -8,6 +8,8 @@
 * ``tinygnn_amd/_build/libtinygnn.so`` -- TinyGNN's C++ API
   (include/tinygnn/*.hpp) over the C-ABI, from ``cpp/*.cpp`` (host code).
 * ``tinygnn_amd/_build/test_cpp_api`` -- the C++ API test (tests/cpp).
+* ``tinygnn_amd/_build/test_numparse`` -- the CSV number conversions checked
+  against the host C library (tests/cpp/test_numparse.cpp).
 
 Usage: ``python -m tinygnn_amd.build [-j N] [--quiet]``.
 """
@@ -29,6 +31,7 @@ LIB = os.path.join(BUILD, "libtinygnn_amd.so")
 CPP = os.path.join(HERE, "cpp")
 API_LIB = os.path.join(BUILD, "libtinygnn.so")
 CPP_TEST = os.path.join(BUILD, "test_cpp_api")
+NUMPARSE_TEST = os.path.join(BUILD, "test_numparse")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -89,6 +92,12 @@ def _build_cpp_api() -> None:
     _run(host + [test_src, "-o", tmp, f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd",
                  "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, CPP_TEST)
+    # the CSV number conversions (csrc/numparse.hpp) compiled for the host and
+    # checked against the C library in tests/test_numparse.py
+    tmp = NUMPARSE_TEST + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{CSRC}",
+          os.path.join(ROOT, "tests", "cpp", "test_numparse.cpp"), "-o", tmp])
+    os.replace(tmp, NUMPARSE_TEST)
 
 
 def build(jobs: int | None = None, quiet: bool = True) -> str:

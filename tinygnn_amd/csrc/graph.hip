@@ -44,13 +44,14 @@ __host__ __device__ inline int next_pow2(int x) {
 __global__ __launch_bounds__(256) void edge_count_kernel(const int32_t* __restrict__ src,
                                                          const int32_t* __restrict__ dst,
                                                          int64_t n_edges, int32_t n_nodes,
+                                                         int check_dst,
                                                          int32_t* __restrict__ deg,
                                                          unsigned long long* __restrict__ bad) {
     for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n_edges;
          e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int32_t s = src[e], d = dst[e];
         const bool sbad = s < 0 || s >= n_nodes;
-        const bool dbad = d < 0 || d >= n_nodes;
+        const bool dbad = check_dst && (d < 0 || d >= n_nodes);
         if (sbad || dbad) {
             atomicMin(bad, static_cast<unsigned long long>(2 * e + (sbad ? 0 : 1)));
         } else {
@@ -600,7 +601,7 @@ size_t self_loops_ws(int64_t n) {
 // Host entry used by the C-ABI and the Model.
 void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
                       int32_t* row_ptr, int32_t* col_ind, float* val, void* workspace,
-                      size_t ws_bytes, hipStream_t s) {
+                      size_t ws_bytes, hipStream_t s, bool check_dst) {
     require(n_nodes >= 0 && n_edges >= 0, "GraphLoader::edge_list_to_csr: negative size");
     if (n_nodes == 0) {
         require(n_edges == 0,
@@ -629,7 +630,7 @@ void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, cons
     fill_i32(reinterpret_cast<int32_t*>(w.bad), 2, -1, s);  // UINT64_MAX
     if (n_edges > 0) {
         edge_count_kernel<<<grid_for(n_edges, 256, 16384), 256, 0, s>>>(
-            src, dst, n_edges, static_cast<int32_t>(n_nodes), w.deg, w.bad);
+            src, dst, n_edges, static_cast<int32_t>(n_nodes), check_dst ? 1 : 0, w.deg, w.bad);
         TG_LAUNCH_CHECK();
     }
     classify_rows_kernel<<<grid_for(n_nodes), 256, 0, s>>>(w.deg, n_nodes, w.lists, w.counts);
@@ -735,7 +736,7 @@ int tg_edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, co
                         size_t workspace_bytes, tg_stream_t stream) {
     return tg::guard([&] {
         tg::edge_list_to_csr(n_nodes, n_edges, src, dst, row_ptr, col_ind, val, workspace,
-                             workspace_bytes, static_cast<hipStream_t>(stream));
+                             workspace_bytes, static_cast<hipStream_t>(stream), true);
     });
 }
 
