@@ -22,6 +22,9 @@ Default run (N=1):
     (gcn_norm / add_self_loops inside every forward), the reference's
     Model::forward timed once on the host cores, and the parity of the
     log-softmax logits against it (|err| <= 1e-5 + 1e-4|ref|, argmax).
+  * ``ingest``: GraphLoader's CSV parsing on the device -- a 20M-line edge
+    list and a 50,000 x 602 feature table -- with the text in HBM and through
+    the file path, against the compiled reference's parser on a sample.
 Graphs are generated on the GPU from seeded power-law degrees and built into
 CSR by the library's own edge_list_to_csr (its time is reported).
 
@@ -303,6 +306,108 @@ def run_forward_e(args, torch, tg):
     return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)
 
 
+def run_ingest(args, torch, tg):
+    """GraphLoader on the device (graph_loader.cpp:61-206): CSV parse time
+    with the text already in HBM (the index and parse kernels), the file path
+    end to end (read into pinned staging, copy, parse), and the compiled
+    reference's parse_edges / parse_features timed on a bounded sample of the
+    same texts, whose results must equal the device's bit for bit."""
+    import tempfile
+
+    from tinygnn_amd import synth
+
+    rng = np.random.default_rng(args.seed + 7)
+    n_nodes, f_in = 232_965, 602
+    ne, nr = args.ingest_edges, args.ingest_rows
+    src = rng.integers(0, n_nodes, ne)
+    dst = rng.integers(0, n_nodes, ne)
+    text_e = synth.edges_csv(src, dst)
+    text_f, kf = synth.features_csv(nr, f_in, seed=args.seed + 8)
+    ref = None
+    if not args.no_cpu:
+        import oracle
+        ref = oracle.reference() if oracle.has_reference() else None
+    tmp = tempfile.mkdtemp(prefix="tg_ingest_")
+    out = {}
+    for kind, text in (("edges", text_e), ("features", text_f)):
+        dev_text = torch.from_numpy(np.frombuffer(text, np.uint8).copy()).cuda()
+
+        def parse_dev():
+            c = tg.CsvText.from_device(dev_text, kind)
+            r = c.parse_edges()[:2] if kind == "edges" else c.parse_features()
+            c.close()
+            return r
+
+        parse_dev()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(args.ingest_steps):
+            t0 = time.perf_counter()
+            res = parse_dev()
+            torch.cuda.synchronize()
+            ms.append((time.perf_counter() - t0) * 1e3)
+        gpu_ms = float(np.median(ms))
+        if kind == "edges":
+            exact = bool(np.array_equal(res[0].cpu().numpy(), src) and
+                         np.array_equal(res[1].cpu().numpy(), dst))
+        else:  # decimal fields d.dddddd: within half an ulp of k / 1e6
+            want = kf / 1e6
+            got = res.cpu().numpy().astype(np.float64)
+            exact = bool(np.all(np.abs(got - want) <= np.spacing(np.abs(want).astype(np.float32))
+                                .astype(np.float64) / 2 + 1e-12))
+        del res
+        path = os.path.join(tmp, kind + ".csv")
+        with open(path, "wb") as fh:
+            fh.write(text)
+        fms = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            r2 = tg.parse_edges(path) if kind == "edges" else tg.parse_features(path)
+            torch.cuda.synchronize()
+            fms.append((time.perf_counter() - t0) * 1e3)
+            del r2
+        lines = ne if kind == "edges" else nr
+        e = dict(bytes=len(text), lines=lines, gpu_ms=round(gpu_ms, 3),
+                 gbs=round(len(text) / gpu_ms / 1e6, 1),
+                 lines_per_s=round(lines / gpu_ms * 1e3, 0), values_ok=exact,
+                 file_ms=round(float(np.median(fms)), 2),
+                 file_gbs=round(len(text) / float(np.median(fms)) / 1e6, 2))
+        log(f"ingest {kind}: {len(text) / 1e6:.0f} MB, device parse {gpu_ms:.2f} ms "
+            f"({e['gbs']} GB/s), file path {e['file_ms']} ms, values ok {exact}")
+        if ref is not None:
+            # a bounded sample: the first lines of the same text
+            n_s = min(lines, 2_000_000 if kind == "edges" else 3_000)
+            cut = 0
+            for _ in range(n_s + 1):  # header + n_s lines
+                cut = text.index(b"\n", cut) + 1
+            sample = os.path.join(tmp, kind + "_sample.csv")
+            with open(sample, "wb") as fh:
+                fh.write(text[:cut])
+            t0 = time.perf_counter()
+            want = (ref.parse_edges_file(sample) if kind == "edges"
+                    else ref.parse_features_file(sample))
+            cpu_ms = (time.perf_counter() - t0) * 1e3
+            got = tg.parse_edges(sample) if kind == "edges" else tg.parse_features(sample)
+            if kind == "edges":
+                par = bool(np.array_equal(got[0].cpu().numpy(), want[0]) and
+                           np.array_equal(got[1].cpu().numpy(), want[1]))
+            else:
+                par = bool(np.array_equal(got.cpu().numpy().view(np.int32), want.view(np.int32)))
+            e["cpu_baseline"] = dict(value=round(cut / cpu_ms / 1e6, 3), unit="GB/s", cores=1,
+                                     kind="reference", ms=round(cpu_ms, 1),
+                                     sample=f"first {n_s} data lines ({cut} bytes)")
+            e["parity_sample_bit_exact"] = par
+            e["speedup_vs_reference"] = round(e["gbs"] / (cut / cpu_ms / 1e6), 1)
+            log(f"ingest {kind}: reference {cut / cpu_ms / 1e6:.3f} GB/s on the sample, "
+                f"bit-exact {par}")
+        out[kind] = e
+        del dev_text
+    for fn in os.listdir(tmp):
+        os.remove(os.path.join(tmp, fn))
+    os.rmdir(tmp)
+    return out
+
+
 def cpu_baseline_spmm(rp, ci, val, b, args):
     """The reference spmm on the host cores over rows [0, R) of the same
     matrix with the full B; R is sized for a few seconds per call."""
@@ -357,6 +462,10 @@ def main():
     ap.add_argument("--no-forward", action="store_true", help="skip the config-E forwards")
     ap.add_argument("--fwd-steps", type=int, default=10)
     ap.add_argument("--fwd-warmup", type=int, default=2)
+    ap.add_argument("--no-ingest", action="store_true", help="skip the CSV ingestion leg")
+    ap.add_argument("--ingest-edges", type=int, default=20_000_000)
+    ap.add_argument("--ingest-rows", type=int, default=50_000)
+    ap.add_argument("--ingest-steps", type=int, default=5)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB copy kernel (out = x * 1), the reference "
                          "dispatch for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -385,6 +494,8 @@ def main():
         torch.cuda.synchronize()
         del xc, yc
     fwd = None if args.no_forward else run_forward_e(args, torch, tg)
+    torch.cuda.empty_cache()
+    ingest = None if args.no_ingest else run_ingest(args, torch, tg)
     head = r["head"]
     line = {
         "metric": "CSR SpMM GB/s & % HBM peak; forward ms at 233K nodes / 114.6M edges",
@@ -419,6 +530,7 @@ def main():
         "cpu_baseline": r["cpu"],
         "csr_build_ms": round(r["csr_build_ms"], 2),
         "forward": fwd,
+        "ingest": ingest,
     }
     print(json.dumps(line), flush=True)
 

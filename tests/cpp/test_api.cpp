@@ -6,6 +6,8 @@
 // tests/test_cpp_api_gpu.py; exit status 0 = all checks passed.
 #include <cmath>
 #include <cstdio>
+#include <cstring>
+#include <fstream>
 #include <functional>
 #include <stdexcept>
 #include <string>
@@ -264,10 +266,127 @@ static void test_model() {
     CHECK(finite);
 }
 
+// ---- ingestion (reference tests/test_graph_loader.cpp, model.cpp:49-185) ----
+static std::string write_file(const std::string& name, const std::string& content) {
+    const std::string path = "/tmp/tinygnn_api_test_" + name;
+    std::ofstream f(path, std::ios::binary);
+    f << content;
+    return path;
+}
+
+template <typename T>
+static void put(std::string& s, T v) {
+    s.append(reinterpret_cast<const char*>(&v), sizeof v);
+}
+
+static void test_ingest() {
+    // test_graph_loader.cpp:151-172
+    const std::string ep = write_file("edges.csv",
+                                      "src,dst\n0,1\n0,2\n1,0\n1,3\n2,0\n2,3\n2,4\n3,1\n3,2\n4,2\n");
+    auto edges = GraphLoader::parse_edges(ep);
+    CHECK(edges.size() == 10u);
+    CHECK(edges[0] == std::make_pair(0, 1) && edges[6] == std::make_pair(2, 4) &&
+          edges[9] == std::make_pair(4, 2));
+    // :186-193 CRLF and spaces
+    auto crlf = GraphLoader::parse_edges(write_file("crlf.csv", "src,dst\r\n0, 1\r\n1 ,0\r\n"));
+    CHECK(crlf.size() == 2u && crlf[0] == std::make_pair(0, 1) && crlf[1] == std::make_pair(1, 0));
+    // :228-249
+    const std::string fp = write_file("feat.csv",
+                                      "node_id,feat_0,feat_1,feat_2\n0,1.0,0.0,0.5\n1,0.0,1.0,0.0\n"
+                                      "2,0.5,0.5,1.0\n3,0.0,0.0,1.0\n4,1.0,1.0,0.0\n");
+    Tensor x = GraphLoader::parse_features(fp);
+    CHECK(x.format() == StorageFormat::Dense && x.rows() == 5 && x.cols() == 3);
+    CHECK(x.at(0, 0) == 1.0f && x.at(0, 2) == 0.5f && x.at(2, 1) == 0.5f && x.at(4, 2) == 0.0f);
+    // :268-283 sparse ids
+    Tensor sp = GraphLoader::parse_features(write_file("sparse.csv", "node_id,f0\n0,10.0\n5,50.0\n"));
+    CHECK(sp.rows() == 6 && sp.at(1, 0) == 0.0f && sp.at(5, 0) == 50.0f);
+    // :508-548 full pipeline
+    GraphData gd = GraphLoader::load(ep, fp);
+    CHECK(gd.num_nodes == 5 && gd.num_edges == 10 && gd.num_features == 3);
+    CHECK(gd.adjacency.format() == StorageFormat::SparseCSR && gd.adjacency.nnz() == 10);
+    CHECK(gd.node_features.at(2, 2) == 1.0f);
+    const std::vector<int32_t> rp = {0, 2, 4, 7, 9, 10};  // :330-372
+    CHECK(gd.adjacency.row_ptr() == rp);
+    // :644-663 edges beyond the feature rows
+    GraphData g2 = GraphLoader::load(write_file("e2.csv", "0,5\n5,0\n"),
+                                     write_file("f2.csv", "node_id,f0\n0,1.0\n1,2.0\n"));
+    CHECK(g2.num_nodes == 6 && g2.node_features.rows() == 6 && g2.node_features.at(1, 0) == 2.0f &&
+          g2.node_features.at(5, 0) == 0.0f);
+    // :1546-1640 errors
+    CHECK_THROWS(std::runtime_error, "GraphLoader: cannot open file 'nonexistent_edges_file.csv'",
+                 GraphLoader::parse_edges("nonexistent_edges_file.csv"));
+    CHECK_THROWS(std::runtime_error, "file is empty", GraphLoader::parse_edges(write_file("empty.csv", "")));
+    CHECK_THROWS(std::runtime_error, "malformed line 1: '0 1'",
+                 GraphLoader::parse_edges(write_file("bad1.csv", "0 1\n")));
+    CHECK_THROWS(std::runtime_error, "invalid integer on line 1: '0,abc'",
+                 GraphLoader::parse_edges(write_file("bad2.csv", "0,abc\n")));
+    CHECK_THROWS(std::runtime_error, "negative node ID on line 1: src=-1, dst=2",
+                 GraphLoader::parse_edges(write_file("bad3.csv", "-1,2\n")));
+    CHECK_THROWS(std::runtime_error, "inconsistent feature count on line 2: expected 2 but got 1",
+                 GraphLoader::parse_features(write_file("bad4.csv", "0,1.0,2.0\n1,3.0\n")));
+    CHECK_THROWS(std::runtime_error, "no data rows",
+                 GraphLoader::parse_features(write_file("bad5.csv", "node_id,f0,f1\n")));
+    CHECK(GraphLoader::parse_edges(write_file("hdr.csv", "src,dst\n")).empty());
+
+    // TGNN weight file (model.hpp:22-33) and Model::load_weights(path)
+    std::string wb = "TGNN";
+    put<uint32_t>(wb, 1);
+    put<float>(wb, 0.75f);
+    put<uint32_t>(wb, 2);
+    const std::vector<std::pair<std::string, std::vector<float>>> ts = {
+        {"layer0.weight", {0.5f, -1.0f, 2.0f, 0.25f, 1.5f, -0.5f}}, {"layer0.bias", {0.1f, -0.2f}}};
+    const uint32_t shapes[2][2] = {{3, 2}, {1, 2}};
+    for (int i = 0; i < 2; ++i) {
+        put<uint32_t>(wb, static_cast<uint32_t>(ts[i].first.size()));
+        wb += ts[i].first;
+        put<uint32_t>(wb, shapes[i][0]);
+        put<uint32_t>(wb, shapes[i][1]);
+        wb.append(reinterpret_cast<const char*>(ts[i].second.data()), ts[i].second.size() * 4);
+    }
+    const std::string wp = write_file("w.bin", wb);
+    WeightFile wf = load_weight_file(wp);
+    CHECK(wf.test_accuracy == 0.75f && wf.tensors.size() == 2);
+    CHECK(wf.tensors.at("layer0.weight").rows() == 3 && wf.tensors.at("layer0.weight").at(2, 1) == -0.5f);
+    Model m1, m2;
+    m1.add_gcn_layer(3, 2, true, Activation::None);
+    m2.add_gcn_layer(3, 2, true, Activation::None);
+    m1.load_weights(wf);
+    m2.load_weights(wp);
+    Tensor A = undirected(4, {{0, 1}, {1, 2}, {2, 3}});
+    Tensor X = Tensor::dense(4, 3, {1, 0, 2, 0, 1, 1, 3, 1, 0, 1, 1, 1});
+    CHECK(m1.forward(A, X).data() == m2.forward(A, X).data());
+    CHECK_THROWS(std::runtime_error, "load_weight_file: invalid magic in",
+                 load_weight_file(write_file("badw.bin", "XXXX" + wb.substr(4))));
+    CHECK_THROWS(std::runtime_error, "load_weight_file: unexpected end of file or read error.",
+                 load_weight_file(write_file("truncw.bin", wb.substr(0, wb.size() - 2))));
+
+    // Cora binary export (model.cpp:49-129)
+    std::string cb;
+    const uint32_t N = 5, F = 2, Cc = 3, E = 6;
+    put(cb, N);
+    put(cb, F);
+    put(cb, Cc);
+    put(cb, E);
+    for (uint32_t i = 0; i < N * F; ++i) put<float>(cb, float(i) * 0.5f);
+    for (uint32_t i = 0; i < N; ++i) put<int32_t>(cb, int32_t(i % Cc));
+    for (int m = 0; m < 3; ++m)
+        for (uint32_t i = 0; i < N; ++i) cb.push_back(char((i + m) % 2));
+    const int32_t src[E] = {0, 4, 1, 0, 3, 0}, dst[E] = {3, 2, 1, 1, 0, 2};
+    for (int32_t v : src) put(cb, v);
+    for (int32_t v : dst) put(cb, v);
+    CoraData cd = load_cora_binary(write_file("cora.bin", cb));
+    CHECK(cd.num_nodes == N && cd.num_features == F && cd.num_classes == Cc && cd.num_edges == E);
+    CHECK(cd.features.at(4, 1) == 4.5f && cd.labels[4] == 1 && cd.val_mask[0] == 1);
+    const std::vector<int32_t> crp = {0, 3, 4, 4, 5, 6}, cci = {1, 2, 3, 1, 0, 2};
+    CHECK(cd.adjacency.row_ptr() == crp && cd.adjacency.col_ind() == cci);
+    CHECK_THROWS(std::runtime_error, "load_cora_binary: cannot open", load_cora_binary("/nonexistent.bin"));
+}
+
 int main() {
     const std::pair<const char*, void (*)()> suites[] = {
         {"tensor", test_tensor}, {"ops", test_ops}, {"graph", test_graph},
-        {"layers", test_layers}, {"model", test_model}};
+        {"layers", test_layers}, {"model", test_model},
+        {"ingest", test_ingest}};
     for (auto& s : suites) {
         try {
             s.second();

@@ -8,6 +8,7 @@
 // the coherence of host views with the device copies.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cstring>
 #include <sstream>
 #include <stdexcept>
@@ -904,6 +905,144 @@ Tensor GraphLoader::edge_list_to_csr(const std::vector<std::pair<int32_t, int32_
     check(tg_edge_list_to_csr(i64(num_nodes), i64(e), d_src, d_dst, Access::rp(out),
                               Access::ci(out), Access::val(out), nullptr, 0, nullptr));
     return out;
+}
+
+}  // namespace tinygnn
+
+// ===========================================================================
+// Ingestion: GraphLoader (graph_loader.cpp:61-326), load_weight_file
+// (model.cpp:134-185), load_cora_binary (model.cpp:49-129)
+// ===========================================================================
+namespace tinygnn {
+namespace {
+
+struct CsvHandle {
+    tg_csv_t h = nullptr;
+    explicit CsvHandle(const std::string& path) { check(tg_csv_open(path.c_str(), &h, nullptr)); }
+    ~CsvHandle() {
+        if (h) tg_csv_destroy(h);
+    }
+    CsvHandle(const CsvHandle&) = delete;
+    CsvHandle& operator=(const CsvHandle&) = delete;
+    int64_t n_data() const {
+        int64_t n = 0;
+        int hdr = 0;
+        check(tg_csv_info(h, &n, &hdr));
+        return n > hdr ? n - hdr : 0;
+    }
+};
+
+// Edge endpoints parsed on the device: a 2 x n int32 scratch tensor
+// (row 0 = src, row 1 = dst) and the largest endpoint.
+Tensor device_edges(const CsvHandle& c, int64_t* max_id) {
+    const int64_t n = c.n_data();
+    Tensor ends = Tensor::device_dense(2, static_cast<size_t>(n));
+    int32_t* d = reinterpret_cast<int32_t*>(ends.device_data_mutable());
+    check(tg_csv_parse_edges(c.h, d, d + n, max_id, nullptr));
+    return ends;
+}
+
+}  // namespace
+
+std::vector<std::pair<int32_t, int32_t>> GraphLoader::parse_edges(const std::string& path) {
+    CsvHandle c(path);
+    int64_t max_id = -1;
+    Tensor ends = device_edges(c, &max_id);
+    const size_t n = ends.cols();
+    std::vector<int32_t> buf(2 * n);
+    detail::d2h(buf.data(), ends.device_data(), 2 * n * sizeof(int32_t));
+    std::vector<std::pair<int32_t, int32_t>> out(n);
+    for (size_t i = 0; i < n; ++i) out[i] = {buf[i], buf[n + i]};
+    return out;
+}
+
+Tensor GraphLoader::parse_features(const std::string& path) {
+    CsvHandle c(path);
+    int64_t rows = 0, cols = 0;
+    check(tg_csv_feature_shape(c.h, &rows, &cols, nullptr));
+    Tensor out = Tensor::device_dense(static_cast<size_t>(rows), static_cast<size_t>(cols));
+    check(tg_csv_parse_features(c.h, rows * cols ? out.device_data_mutable() : nullptr, rows,
+                                cols, nullptr));
+    return out;
+}
+
+GraphData GraphLoader::load(const std::string& edges_path, const std::string& features_path) {
+    int64_t max_id = -1;
+    CsvHandle ce(edges_path);
+    Tensor ends = device_edges(ce, &max_id);
+    const int64_t n_edges = static_cast<int64_t>(ends.cols());
+    CsvHandle cf(features_path);
+    int64_t rows = 0, cols = 0;
+    check(tg_csv_feature_shape(cf.h, &rows, &cols, nullptr));
+    const int64_t num_nodes = std::max<int64_t>(n_edges ? max_id + 1 : 0, rows);
+    GraphData gd;
+    gd.node_features = Tensor::device_dense(static_cast<size_t>(num_nodes), static_cast<size_t>(cols));
+    check(tg_csv_parse_features(cf.h,
+                                num_nodes * cols ? gd.node_features.device_data_mutable() : nullptr,
+                                num_nodes, cols, nullptr));
+    gd.adjacency = Tensor::device_csr(static_cast<size_t>(num_nodes), static_cast<size_t>(num_nodes),
+                                      static_cast<size_t>(n_edges));
+    const int32_t* d = reinterpret_cast<const int32_t*>(ends.device_data());
+    check(tg_edge_list_to_csr(num_nodes, n_edges, d, d + n_edges, Access::rp(gd.adjacency),
+                              Access::ci(gd.adjacency), Access::val(gd.adjacency), nullptr, 0,
+                              nullptr));
+    gd.num_nodes = static_cast<size_t>(num_nodes);
+    gd.num_edges = static_cast<size_t>(n_edges);
+    gd.num_features = static_cast<size_t>(cols);
+    return gd;
+}
+
+WeightFile load_weight_file(const std::string& path) {
+    tg_weights_t w = nullptr;
+    check(tg_weights_open(path.c_str(), &w));
+    struct Close {
+        tg_weights_t w;
+        ~Close() { tg_weights_destroy(w); }
+    } close{w};
+    int64_t n = 0;
+    WeightFile wf;
+    check(tg_weights_info(w, &n, &wf.test_accuracy));
+    for (int64_t i = 0; i < n; ++i) {
+        const char* name = nullptr;
+        const float* data = nullptr;
+        int64_t len = 0, rows = 0, cols = 0;
+        check(tg_weights_tensor(w, i, &name, &len, &rows, &cols, &data));
+        wf.tensors[std::string(name, static_cast<size_t>(len))] = Tensor::dense(
+            static_cast<size_t>(rows), static_cast<size_t>(cols),
+            std::vector<float>(data, data + rows * cols));
+    }
+    return wf;
+}
+
+void Model::load_weights(const std::string& path) { load_weights(load_weight_file(path)); }
+
+CoraData load_cora_binary(const std::string& path) {
+    tg_cora_t c = nullptr;
+    check(tg_cora_open(path.c_str(), &c));
+    struct Close {
+        tg_cora_t c;
+        ~Close() { tg_cora_destroy(c); }
+    } close{c};
+    int64_t n = 0, f = 0, k = 0, e = 0;
+    check(tg_cora_info(c, &n, &f, &k, &e));
+    CoraData cd;
+    cd.num_nodes = static_cast<size_t>(n);
+    cd.num_features = static_cast<size_t>(f);
+    cd.num_classes = static_cast<size_t>(k);
+    cd.num_edges = static_cast<size_t>(e);
+    cd.features = Tensor::device_dense(cd.num_nodes, cd.num_features);
+    cd.adjacency = Tensor::device_csr(cd.num_nodes, cd.num_nodes, cd.num_edges);
+    check(tg_cora_upload(c, n * f ? cd.features.device_data_mutable() : nullptr,
+                         Access::rp(cd.adjacency), Access::ci(cd.adjacency),
+                         Access::val(cd.adjacency), nullptr));
+    const int32_t* labels = nullptr;
+    const uint8_t *tr = nullptr, *va = nullptr, *te = nullptr;
+    check(tg_cora_host(c, &labels, &tr, &va, &te));
+    cd.labels.assign(labels, labels + n);
+    cd.train_mask.assign(tr, tr + n);
+    cd.val_mask.assign(va, va + n);
+    cd.test_mask.assign(te, te + n);
+    return cd;
 }
 
 }  // namespace tinygnn

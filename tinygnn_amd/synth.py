@@ -172,3 +172,75 @@ def spec_gat(f_in, hidden, heads, classes):
                  act=0, post=2),
             dict(type="gat", **{"in": hidden * heads}, out=classes, heads=1, concat=True,
                  slope=0.2, act=0, post=0)]
+
+
+# ---------------------------------------------------------------------------
+# CSV texts for the ingestion benchmark (GraphLoader's formats,
+# graph_loader.hpp:26-35), generated with vectorised byte arithmetic.
+# ---------------------------------------------------------------------------
+def _digits(a):
+    a = np.asarray(a, np.int64)
+    nd = np.ones(a.shape, np.int64)
+    t = a // 10
+    while t.any():
+        nd += t > 0
+        t //= 10
+    return nd
+
+
+def edges_csv(src, dst, header: bool = True) -> bytes:
+    """'src,dst' lines (non-negative ids, no padding), optional header.
+    Built as fixed-width rows (right-aligned digits, NUL padding) and
+    compacted by dropping the padding."""
+    src = np.asarray(src, np.int64)
+    dst = np.asarray(dst, np.int64)
+    n = src.shape[0]
+    w = max(int(_digits(np.array([max(int(src.max(initial=0)), int(dst.max(initial=0)))]))[0]), 1)
+    fixed = np.zeros((n, 2 * w + 2), np.uint8)
+    top = max(int(src.max(initial=0)), int(dst.max(initial=0)))
+
+    def right_aligned(a):  # (len(a), w) digits, NUL-padded on the left
+        out = np.zeros((a.shape[0], w), np.uint8)
+        v = a.copy()
+        for k in range(w):
+            out[:, w - 1 - k] = np.where((a >= 10 ** k) | (k == 0), v % 10 + 48, 0)
+            v //= 10
+        return out
+
+    table = right_aligned(np.arange(top + 1, dtype=np.int64)) if top < (1 << 24) else None
+    for a, col0 in ((src, 0), (dst, w + 1)):
+        fixed[:, col0:col0 + w] = table[a] if table is not None else right_aligned(a)
+    fixed[:, w] = ord(",")
+    fixed[:, -1] = ord("\n")
+    flat = fixed.ravel()
+    head = b"src,dst\n" if header else b""
+    return head + flat[flat != 0].tobytes()
+
+
+def features_csv(n_rows: int, n_feat: int, seed: int = 0, header: bool = True):
+    """A feature table of fixed-width fields: zero-padded 7-digit node ids
+    (rows in random order) and values '-d.dddddd' / ' d.dddddd' (a leading
+    space where there is no sign; the parser skips it).  Returns (text,
+    values) with values[i] the row of node i as the decimal strings' exact
+    integers k (value = k / 1e6)."""
+    rng = np.random.default_rng(seed)
+    k = rng.integers(-9_999_999, 10_000_000, size=(n_rows, n_feat), dtype=np.int64)
+    order = rng.permutation(n_rows)
+    w = 10  # ',' + sign + d + '.' + 6 digits
+    row_len = 7 + n_feat * w + 1
+    buf = np.empty((n_rows, row_len), np.uint8)
+    ids = order.astype(np.int64)
+    for j in range(7):
+        buf[:, 6 - j] = (ids // 10 ** j % 10 + 48).astype(np.uint8)
+    kk = k[order]
+    mag = np.abs(kk)
+    tok = buf[:, 7:7 + n_feat * w].reshape(n_rows, n_feat, w)
+    tok[:, :, 0] = ord(",")
+    tok[:, :, 1] = np.where(kk < 0, ord("-"), ord(" ")).astype(np.uint8)
+    tok[:, :, 2] = (mag // 1_000_000 % 10 + 48).astype(np.uint8)
+    tok[:, :, 3] = ord(".")
+    for j in range(6):
+        tok[:, :, 9 - j] = (mag // 10 ** j % 10 + 48).astype(np.uint8)
+    buf[:, -1] = ord("\n")
+    head = ("node_id," + ",".join(f"f{j}" for j in range(n_feat)) + "\n").encode() if header else b""
+    return head + buf.tobytes(), k
