@@ -51,4 +51,13 @@ struct GraphLoader {
     static GraphData load(const std::string& edges_path, const std::string& features_path);
 };
 
+/// The SparseCSR num_nodes x num_nodes adjacency of a COO edge list as the
+/// pybind module's Tensor.from_edge_index builds it (python/tinygnn_ext.cpp:
+/// 116-157): rows = sources, destinations sorted, duplicates kept, values
+/// 1.0f, destinations checked by Tensor::sparse_csr's validation.  A source
+/// outside [0, num_nodes) (undefined behaviour in the reference) throws
+/// std::invalid_argument.  src / dst are host arrays of num_edges entries.
+Tensor csr_from_edge_index(const int32_t* src, const int32_t* dst, std::size_t num_edges,
+                           std::size_t num_nodes);
+
 }  // namespace tinygnn

@@ -80,6 +80,9 @@ struct Tensor {
     /// A tensor whose data lives only in HBM (library results).  For CSR,
     /// `nnz` entries; the device buffers are allocated, contents undefined.
     static Tensor device_dense(std::size_t rows, std::size_t cols);
+    /// A dense device-resident copy of rows x cols row-major floats that are
+    /// already in device memory (zero-copy interop with other device code).
+    static Tensor dense_from_device(std::size_t rows, std::size_t cols, const float* device_ptr);
     static Tensor device_csr(std::size_t rows, std::size_t cols, std::size_t nnz);
     detail::DeviceMirror& mirror() const;  // for the library's own ops
     void mark_device_written();            // device holds the only valid copy

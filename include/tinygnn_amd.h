@@ -77,6 +77,18 @@ int tg_edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src,
  * (src/tensor.cpp:41-96): col_ind within [0, n_cols), row_ptr
  * non-decreasing, row_ptr[n_rows] == nnz.  Synchronises `stream`.
  * ------------------------------------------------------------------------ */
+/* The CSR that the pybind module's Tensor.from_edge_index and
+ * load_cora_binary build (python/tinygnn_ext.cpp:116-157, src/model.cpp:
+ * 87-126): rows = sources, destinations sorted, duplicates kept, values
+ * 1.0f, and destinations checked only afterwards, by Tensor::sparse_csr's
+ * validation (an out-of-range one raises "Tensor::sparse_csr: col_ind[k] =
+ * v is out of bounds for cols=n" at its sorted position).  A source outside
+ * [0, n_nodes) -- undefined behaviour in the reference -- raises
+ * TG_ERR_INVALID_ARGUMENT "<context>: edge[k].src = v out of range [0, n)".
+ * Synchronises. */
+int tg_coo_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
+                  int32_t* row_ptr, int32_t* col_ind, float* val, const char* context,
+                  tg_stream_t stream);
 int tg_csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz,
                     const int32_t* row_ptr, const int32_t* col_ind,
                     tg_stream_t stream);

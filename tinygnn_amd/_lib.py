@@ -61,6 +61,7 @@ SIGNATURES = {
     "tg_edge_list_to_csr_workspace_size": (sz, [i64, i64]),
     "tg_edge_list_to_csr": (i32, [i64, i64, vp, vp, vp, vp, vp, vp, sz, vp]),
     "tg_csr_validate": (i32, [i64, i64, i64, vp, vp, vp]),
+    "tg_coo_to_csr": (i32, [i64, i64, vp, vp, vp, vp, vp, C.c_char_p, vp]),
     "tg_self_loops_workspace_size": (sz, [i64]),
     "tg_add_self_loops": (i32, [i64, i64, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
     "tg_gcn_norm": (i32, [i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),

@@ -92,12 +92,29 @@ def _build_cpp_api() -> None:
     _run(host + [test_src, "-o", tmp, f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd",
                  "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, CPP_TEST)
+    _build_pybind()
     # the CSV number conversions (csrc/numparse.hpp) compiled for the host and
     # checked against the C library in tests/test_numparse.py
     tmp = NUMPARSE_TEST + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{CSRC}",
           os.path.join(ROOT, "tests", "cpp", "test_numparse.cpp"), "-o", tmp])
     os.replace(tmp, NUMPARSE_TEST)
+
+
+def _build_pybind() -> None:
+    """The Python module ``_tinygnn_core`` (pybind/tinygnn_core.cpp) over
+    libtinygnn.so: the reference's binding surface, host code only."""
+    import sysconfig
+
+    import pybind11
+    out = os.path.join(BUILD, "_tinygnn_core" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden", "-Wall",
+          f"-I{os.path.join(ROOT, 'include')}", f"-I{pybind11.get_include()}",
+          f"-I{sysconfig.get_paths()['include']}",
+          os.path.join(HERE, "pybind", "tinygnn_core.cpp"), "-o", tmp,
+          f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
 
 
 def build(jobs: int | None = None, quiet: bool = True) -> str:

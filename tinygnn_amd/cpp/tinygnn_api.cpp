@@ -1046,3 +1046,28 @@ CoraData load_cora_binary(const std::string& path) {
 }
 
 }  // namespace tinygnn
+
+namespace tinygnn {
+
+Tensor Tensor::dense_from_device(std::size_t rows, std::size_t cols, const float* device_ptr) {
+    Tensor t = device_dense(rows, cols);
+    if (rows * cols)
+        detail::d2d(t.device_data_mutable(), device_ptr, rows * cols * sizeof(float));
+    return t;
+}
+
+Tensor csr_from_edge_index(const int32_t* src, const int32_t* dst, std::size_t num_edges,
+                           std::size_t num_nodes) {
+    Tensor ends = Tensor::device_dense(2, num_edges);
+    int32_t* d_src = reinterpret_cast<int32_t*>(ends.device_data_mutable());
+    int32_t* d_dst = d_src + num_edges;
+    detail::h2d(d_src, src, num_edges * sizeof(int32_t));
+    detail::h2d(d_dst, dst, num_edges * sizeof(int32_t));
+    Tensor out = Tensor::device_csr(num_nodes, num_nodes, num_edges);
+    check(tg_coo_to_csr(static_cast<int64_t>(num_nodes), static_cast<int64_t>(num_edges), d_src,
+                        d_dst, Access::rp(out), Access::ci(out), Access::val(out),
+                        "from_edge_index", nullptr));
+    return out;
+}
+
+}  // namespace tinygnn

@@ -601,20 +601,20 @@ size_t self_loops_ws(int64_t n) {
 // Host entry used by the C-ABI and the Model.
 void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
                       int32_t* row_ptr, int32_t* col_ind, float* val, void* workspace,
-                      size_t ws_bytes, hipStream_t s, bool check_dst) {
-    require(n_nodes >= 0 && n_edges >= 0, "GraphLoader::edge_list_to_csr: negative size");
+                      size_t ws_bytes, hipStream_t s, bool check_dst, const char* who) {
+    const std::string W = who ? who : "GraphLoader::edge_list_to_csr";
+    require(n_nodes >= 0 && n_edges >= 0, W + ": negative size");
     if (n_nodes == 0) {
-        require(n_edges == 0,
-                "GraphLoader::edge_list_to_csr: num_nodes is 0 but edges is non-empty");
+        require(n_edges == 0, W + ": num_nodes is 0 but edges is non-empty");
         write_i32_kernel<<<1, 1, 0, s>>>(row_ptr, 0);
         TG_LAUNCH_CHECK();
         return;
     }
     require(n_nodes < (int64_t(1) << 31) && n_edges < (int64_t(1) << 31),
-            "GraphLoader::edge_list_to_csr: sizes must be < 2^31 (int32 CSR)");
-    require(row_ptr != nullptr, "GraphLoader::edge_list_to_csr: row_ptr is null");
+            W + ": sizes must be < 2^31 (int32 CSR)");
+    require(row_ptr != nullptr, W + ": row_ptr is null");
     require(n_edges == 0 || (src && dst && col_ind && val),
-            "GraphLoader::edge_list_to_csr: null pointer");
+            W + ": null pointer");
     Carver probe(nullptr, 0);
     carve_csr_ws(probe, n_nodes);
     DeviceBuffer own;
@@ -645,7 +645,7 @@ void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, cons
         const bool is_dst = (bad & 1) != 0;
         int32_t v = 0;
         TG_HIP(hipMemcpy(&v, (is_dst ? dst : src) + e, sizeof(v), hipMemcpyDeviceToHost));
-        throw std::invalid_argument("GraphLoader::edge_list_to_csr: edge[" + std::to_string(e) +
+        throw std::invalid_argument(W + ": edge[" + std::to_string(e) +
                                     "]." + (is_dst ? "dst" : "src") + " = " +
                                     std::to_string(v) + " out of range [0, " +
                                     std::to_string(n_nodes) + ")");
@@ -736,7 +736,20 @@ int tg_edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, co
                         size_t workspace_bytes, tg_stream_t stream) {
     return tg::guard([&] {
         tg::edge_list_to_csr(n_nodes, n_edges, src, dst, row_ptr, col_ind, val, workspace,
-                             workspace_bytes, static_cast<hipStream_t>(stream), true);
+                             workspace_bytes, static_cast<hipStream_t>(stream), true, nullptr);
+    });
+}
+
+int tg_coo_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
+                  int32_t* row_ptr, int32_t* col_ind, float* val, const char* context,
+                  tg_stream_t stream) {
+    return tg::guard([&] {
+        const auto s = static_cast<hipStream_t>(stream);
+        const std::string who = context ? context : "coo_to_csr";
+        tg::edge_list_to_csr(n_nodes, n_edges, src, dst, row_ptr, col_ind, val, nullptr, 0, s,
+                             /*check_dst=*/false, who.c_str());
+        tg::csr_validate(n_nodes, n_nodes, n_edges, row_ptr, col_ind, s);
+        TG_HIP(hipStreamSynchronize(s));
     });
 }
 

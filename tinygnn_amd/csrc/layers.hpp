@@ -14,9 +14,11 @@ namespace tg {
 // graph.hip
 // check_dst = false leaves destinations unchecked (load_cora_binary's build,
 // whose result Tensor::sparse_csr validates instead).
+// who names the caller in messages (default "GraphLoader::edge_list_to_csr").
 void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, const int32_t* dst,
                       int32_t* row_ptr, int32_t* col_ind, float* val, void* workspace,
-                      size_t ws_bytes, hipStream_t s, bool check_dst = true);
+                      size_t ws_bytes, hipStream_t s, bool check_dst = true,
+                      const char* who = nullptr);
 size_t edge_list_to_csr_ws(int64_t n_nodes);
 void csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz, const int32_t* row_ptr,
                   const int32_t* col_ind, hipStream_t s);

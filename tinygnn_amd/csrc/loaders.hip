@@ -226,16 +226,6 @@ int tg_cora_upload(tg_cora_t c, float* features, int32_t* row_ptr, int32_t* col_
         require(row_ptr != nullptr, "tg_cora_upload: row_ptr is null");
         require(c->e == 0 || (col_ind && val), "tg_cora_upload: null output");
         require(c->n * c->f == 0 || features, "tg_cora_upload: features is null");
-        // model.cpp:89-99 counts only sources below N and then writes through
-        // every source: a source outside [0, N) is undefined behaviour there
-        // and an error here.
-        for (int64_t k = 0; k < c->e; ++k) {
-            const int32_t sv = c->src[static_cast<size_t>(k)];
-            if (sv < 0 || sv >= c->n)
-                throw std::invalid_argument("load_cora_binary: edge[" + std::to_string(k) +
-                                            "].src = " + std::to_string(sv) +
-                                            " out of range [0, " + std::to_string(c->n) + ")");
-        }
         if (c->n * c->f > 0)
             TG_HIP(hipMemcpyAsync(features, c->features.data(),
                                   static_cast<size_t>(c->n * c->f) * sizeof(float),
@@ -249,10 +239,12 @@ int tg_cora_upload(tg_cora_t c, float* features, int32_t* row_ptr, int32_t* col_
             TG_HIP(hipMemcpyAsync(d_dst, c->dst.data(), static_cast<size_t>(c->e) * 4,
                                   hipMemcpyHostToDevice, s));
         }
-        // the reference builds the CSR without checking destinations, then
-        // Tensor::sparse_csr validates it (tensor.cpp:46-86)
+        // model.cpp:89-110 counts only sources below N and then writes through
+        // every source (a source outside [0, N) is undefined behaviour there and
+        // an error here); destinations are checked afterwards by
+        // Tensor::sparse_csr (tensor.cpp:46-86)
         tg::edge_list_to_csr(c->n, c->e, d_src, d_dst, row_ptr, col_ind, val, nullptr, 0, s,
-                             /*check_dst=*/false);
+                             /*check_dst=*/false, "load_cora_binary");
         tg::csr_validate(c->n, c->n, c->e, row_ptr, col_ind, s);
         TG_HIP(hipStreamSynchronize(s));
     });
