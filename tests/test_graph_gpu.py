@@ -154,6 +154,42 @@ def test_gcn_norm_bitexact(gpu, restate, seed, unsorted, weights):
     np.testing.assert_array_equal(bits(v), bits(want.val))
 
 
+@pytest.mark.parametrize("weights", ["unit", "real", "big_int", "neg_int"])
+def test_self_loops_long_rows(gpu, restate, weights):
+    """Rows up to 9,000 entries (the workgroup-per-row kernels) with
+    diagonals present and absent.  Unit and small signed integers take the
+    exact parallel degree; real values and integers whose magnitudes sum past
+    2^24 take the sequential one."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(17)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=20, max_deg=9000)
+    rows = np.repeat(np.arange(n), np.diff(a.row_ptr))
+    diag = rng.choice(n, size=n // 3, replace=False)
+    src = np.concatenate([rows, diag]).astype(np.int32)
+    dst = np.concatenate([a.col_ind, diag]).astype(np.int32)
+    g = restate.edge_list_to_csr(src, dst, n)
+    if weights == "unit":
+        g.val[:] = 1.0
+    elif weights == "real":
+        g.val[:] = (rng.random(g.nnz) * 2 + 0.01).astype(np.float32)
+    elif weights == "big_int":
+        g.val[:] = rng.integers(1, 20000, g.nnz).astype(np.float32)
+    else:
+        g.val[:] = rng.integers(-5, 6, g.nnz).astype(np.float32)
+    assert np.diff(g.row_ptr).max() > 2048
+    want = restate.add_self_loops(g)
+    rp, ci, v = tg.add_self_loops(_dev(gpu, g)).to_numpy()
+    np.testing.assert_array_equal(rp, want.row_ptr)
+    np.testing.assert_array_equal(ci, want.col_ind)
+    np.testing.assert_array_equal(bits(v), bits(want.val))
+    want, wdeg, wdis = restate.gcn_norm(g, with_degrees=True)
+    got, deg, dis = tg.gcn_norm(_dev(gpu, g), with_degrees=True)
+    np.testing.assert_array_equal(bits(deg.cpu().numpy()), bits(wdeg))
+    np.testing.assert_array_equal(bits(dis.cpu().numpy()), bits(wdis))
+    np.testing.assert_array_equal(bits(got.val.cpu().numpy()), bits(want.val))
+
+
 def test_gcn_norm_degree_sweep(gpu, restate):
     """1/sqrt(deg) correctly rounded for every integer degree 1..4096 (star-like
     rows of unit weights): the device sqrt and divide must round exactly as

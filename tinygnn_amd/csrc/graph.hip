@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <climits>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 namespace tg {
@@ -270,7 +271,9 @@ __global__ __launch_bounds__(256) void csr_check_kernel(const int32_t* __restric
 // ---------------------------------------------------------------------------
 // Self-loops and normalisation
 // ---------------------------------------------------------------------------
-constexpr int kGroup = 16;  // lanes per row in the row-wise passes
+constexpr int kGroup = 16;      // lanes per row in the row-wise passes
+constexpr int kLongRow = 2048;  // longer rows: one workgroup each (the *_long kernels)
+constexpr int kLongBlock = 256;
 
 // Correctly rounded (round-to-nearest) float sqrt and reciprocal for
 // positive finite inputs, as the host's sqrtss / divss give them.  The
@@ -318,10 +321,34 @@ __device__ float cr_rcp(float s) {
     return r;
 }
 
+// Loads VEC consecutive entries starting at index q (VEC = 4: q is a multiple
+// of 4 and the arrays are 16-byte aligned, so the 16-byte granule holding a
+// valid entry is readable even past the array's end).
+template <int VEC, typename T>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, int q, T (&out)[VEC]) {
+    if constexpr (VEC == 4) {
+        using V4 = typename std::conditional<std::is_same<T, float>::value, float4, int4>::type;
+        const V4 v = *reinterpret_cast<const V4*>(p + q);
+        out[0] = v.x;
+        out[1] = v.y;
+        out[2] = v.z;
+        out[3] = v.w;
+    } else {
+        out[0] = p[q];
+    }
+}
+
 // Per row of A (n x n): has_diag, first position (row order) of a column > i,
 // the row length of A + I, and -- for gcn_norm -- the degree (sequential fp32
 // sum of A + I's row values, in row order) and 1/sqrt(deg).
-template <bool NORM>
+//
+// The degree.  When every value of the row (after the diagonal's +1) is an
+// integer and the sum of their magnitudes is at most 2^24, every partial sum
+// of any order is an exactly representable integer, so the row's sum in any
+// order equals the reference's sequential fp32 sum: the group adds them in
+// parallel (in int64).  Other rows take the sequential path in row order.
+// Each lane of the 16-lane group reads VEC consecutive entries per step.
+template <bool NORM, int VEC>
 __global__ __launch_bounds__(256) void self_loop_info_kernel(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_ind,
     const float* __restrict__ val, int64_t n, int32_t* __restrict__ first_ins,
@@ -330,41 +357,71 @@ __global__ __launch_bounds__(256) void self_loop_info_kernel(
     const int g = threadIdx.x % kGroup;
     if (row >= n) return;
     const int b = row_ptr[row], e = row_ptr[row + 1];
+    if (e - b > kLongRow) return;  // self_loop_info_long_kernel
     const int32_t i = static_cast<int32_t>(row);
     int has = 0;
     int first_gt = e - b;  // row-relative position of the first column > i
-    for (int nz = b + g; nz < e; nz += kGroup) {
-        const int32_t c = col_ind[nz];
-        has |= (c == i);
-        if (c > i) first_gt = min(first_gt, nz - b);
+    long long isum = 0, iabs = 0;
+    int integral = 1;
+    const int start = VEC == 4 ? (b & ~3) : b;
+    for (int q = start + g * VEC; q < e; q += kGroup * VEC) {
+        int32_t c[VEC];
+        float v[VEC];
+        load_vec<VEC>(col_ind, q, c);
+        if constexpr (NORM) load_vec<VEC>(val, q, v);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const int nz = q + k;
+            if (nz < b || nz >= e) continue;
+            has |= (c[k] == i);
+            if (c[k] > i) first_gt = min(first_gt, nz - b);
+            if constexpr (NORM) {
+                const float x = c[k] == i ? v[k] + 1.0f : v[k];
+                const bool ok = fabsf(x) <= 16777216.0f && x == rintf(x);
+                integral &= ok ? 1 : 0;
+                if (ok) {
+                    isum += static_cast<long long>(x);
+                    iabs += static_cast<long long>(fabsf(x));
+                }
+            }
+        }
     }
 #pragma unroll
     for (int d = kGroup / 2; d > 0; d >>= 1) {
         has |= __shfl_xor(has, d, kGroup);
         first_gt = min(first_gt, __shfl_xor(first_gt, d, kGroup));
+        if constexpr (NORM) {
+            isum += __shfl_xor(isum, d, kGroup);
+            iabs += __shfl_xor(iabs, d, kGroup);
+            integral &= __shfl_xor(integral, d, kGroup);
+        }
     }
     if (g == 0) {
         first_ins[row] = has ? -1 : first_gt;
         new_len[row] = (e - b) + (has ? 0 : 1);
     }
     if constexpr (NORM) {
-        // Sequential sum in row order of A + I: chunks of kGroup values are
-        // loaded by the group and added one by one by lane 0.
         float d = 0.0f;
-        for (int base = b; base < e; base += kGroup) {
-            const int nz = base + g;
-            float v = 0.0f;
-            if (nz < e) {
-                v = val[nz];
-                if (col_ind[nz] == i) v = v + 1.0f;
+        if (integral && iabs + (has ? 0 : 1) <= (1ll << 24)) {
+            d = static_cast<float>(isum + (has ? 0 : 1));
+        } else {
+            // Sequential sum in row order of A + I: chunks of kGroup values
+            // are loaded by the group and added one by one.
+            for (int base = b; base < e; base += kGroup) {
+                const int nz = base + g;
+                float v = 0.0f;
+                if (nz < e) {
+                    v = val[nz];
+                    if (col_ind[nz] == i) v = v + 1.0f;
+                }
+                const int cnt = min(kGroup, e - base);
+                for (int t = 0; t < cnt; ++t) {
+                    if (!has && base - b + t == first_gt) d = d + 1.0f;
+                    d = d + __shfl(v, t, kGroup);
+                }
             }
-            const int cnt = min(kGroup, e - base);
-            for (int t = 0; t < cnt; ++t) {
-                if (!has && base - b + t == first_gt) d = d + 1.0f;
-                d = d + __shfl(v, t, kGroup);
-            }
+            if (!has && first_gt == e - b) d = d + 1.0f;
         }
-        if (!has && first_gt == e - b) d = d + 1.0f;
         if (g == 0) {
             const float dis = d > 0.0f ? cr_rcp(cr_sqrt(d)) : 0.0f;
             deg_out[row] = d;
@@ -373,10 +430,67 @@ __global__ __launch_bounds__(256) void self_loop_info_kernel(
     }
 }
 
+// Copies entries [b, e) of row i into A + I (shifted by one past the
+// inserted diagonal at `ins`), scaled when NORM.  `lanes` threads share the
+// row (this one is `lane`); each keeps kCopyUnroll granules of VEC entries in
+// flight, so the loads of four steps (and then their dis[c] gathers) overlap.
+constexpr int kCopyUnroll = 4;
+template <bool NORM, int VEC, int LANES>
+__device__ __forceinline__ void copy_span(const int32_t* __restrict__ col_ind,
+                                          const float* __restrict__ val, int b, int e, int lane,
+                                          int32_t i, int ins, int ob, float dis_i,
+                                          const float* __restrict__ dis,
+                                          int32_t* __restrict__ col_out,
+                                          float* __restrict__ val_out) {
+    const int start = VEC == 4 ? (b & ~3) : b;
+    constexpr int kStep = LANES * VEC;
+    for (int q0 = start + lane * VEC; q0 < e; q0 += kStep * kCopyUnroll) {
+        int32_t c[kCopyUnroll][VEC];
+        float v[kCopyUnroll][VEC];
+        float dj[kCopyUnroll][VEC];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+            const int q = q0 + u * kStep;
+            if (q < e) {
+                load_vec<VEC>(col_ind, q, c[u]);
+                load_vec<VEC>(val, q, v[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+            const int q = q0 + u * kStep;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const int nz = q + k;
+                dj[u][k] = 1.0f;
+                if constexpr (NORM)
+                    if (q < e && nz >= b && nz < e) dj[u][k] = dis[c[u][k]];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+            const int q = q0 + u * kStep;
+            if (q >= e) continue;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const int nz = q + k;
+                if (nz < b || nz >= e) continue;
+                const int t = nz - b;
+                float x = v[u][k];
+                if (c[u][k] == i) x = x + 1.0f;
+                if constexpr (NORM) x = (x * dis_i) * dj[u][k];
+                const int o = ob + t + ((ins >= 0 && t >= ins) ? 1 : 0);
+                col_out[o] = c[u][k];
+                val_out[o] = x;
+            }
+        }
+    }
+}
+
 // Copies A into A + I: out position of input entry t of row i is
 // row_ptr_out[i] + t (+1 past the inserted diagonal).  With NORM the values
-// are scaled: ((v) * dis_i) * dis_j.
-template <bool NORM>
+// are scaled: ((v) * dis_i) * dis_j.  Reads VEC entries per lane and step.
+template <bool NORM, int VEC>
 __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_ind,
     const float* __restrict__ val, int64_t n, const int32_t* __restrict__ first_ins,
@@ -386,26 +500,155 @@ __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     const int g = threadIdx.x % kGroup;
     if (row >= n) return;
     const int b = row_ptr[row], e = row_ptr[row + 1];
+    if (e - b > kLongRow) return;  // self_loop_copy_long_kernel
     const int32_t i = static_cast<int32_t>(row);
     const int ins = first_ins[row];
     const int ob = row_ptr_out[row];
     float dis_i = 1.0f;
     if constexpr (NORM) dis_i = dis[row];
-    for (int nz = b + g; nz < e; nz += kGroup) {
-        const int t = nz - b;
-        const int32_t c = col_ind[nz];
-        float v = val[nz];
-        if (c == i) v = v + 1.0f;
-        if constexpr (NORM) v = (v * dis_i) * dis[c];
-        const int o = ob + t + ((ins >= 0 && t >= ins) ? 1 : 0);
-        col_out[o] = c;
-        val_out[o] = v;
-    }
+    copy_span<NORM, VEC, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out, val_out);
     if (g == 0 && ins >= 0) {
-        float v = 1.0f;
-        if constexpr (NORM) v = (1.0f * dis_i) * dis_i;
+        float x = 1.0f;
+        if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
         col_out[ob + ins] = i;
-        val_out[ob + ins] = v;
+        val_out[ob + ins] = x;
+    }
+}
+
+// Rows longer than kLongRow, listed for the workgroup-per-row kernels
+// (list[0..*count)); count starts at zero.
+__global__ __launch_bounds__(256) void long_rows_kernel(const int32_t* __restrict__ row_ptr,
+                                                        int64_t n, int32_t* __restrict__ list,
+                                                        int32_t* __restrict__ count) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r < n && row_ptr[r + 1] - row_ptr[r] > kLongRow)
+        list[atomicAdd(count, 1)] = static_cast<int32_t>(r);
+}
+
+template <typename T>
+__device__ __forceinline__ T block_reduce(T v, T* lds, int op) {  // op: 0 sum, 1 min, 2 or/and
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        const T o = __shfl_xor(v, d, kWave);
+        v = op == 0 ? v + o : op == 1 ? (o < v ? o : v) : (v & o);
+    }
+    __syncthreads();
+    if (lane == 0) lds[wid] = v;
+    __syncthreads();
+    v = lds[0];
+    for (int w = 1; w < kLongBlock / kWave; ++w)
+        v = op == 0 ? v + lds[w] : op == 1 ? (lds[w] < v ? lds[w] : v) : (v & lds[w]);
+    return v;
+}
+
+// self_loop_info for the listed long rows: one workgroup per row (grid-stride
+// over the list).  The sequential degree (rows that fail the integral test)
+// stages 1,024 values of A + I in LDS per step and adds them in row order on
+// one thread.
+template <bool NORM, int VEC>
+__global__ __launch_bounds__(kLongBlock) void self_loop_info_long_kernel(
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_ind,
+    const float* __restrict__ val, const int32_t* __restrict__ list,
+    const int32_t* __restrict__ count, int32_t* __restrict__ first_ins,
+    int32_t* __restrict__ new_len, float* __restrict__ deg_out, float* __restrict__ dis_out) {
+    __shared__ long long red64[kLongBlock / kWave];
+    __shared__ int red32[kLongBlock / kWave];
+    __shared__ float stage[kLongBlock * 4];
+    const int n_long = *count;
+    for (int li = blockIdx.x; li < n_long; li += gridDim.x) {
+        const int32_t i = list[li];
+        const int b = row_ptr[i], e = row_ptr[i + 1];
+        int has = 0, first_gt = e - b, integral = 1;
+        long long isum = 0, iabs = 0;
+        const int start = VEC == 4 ? (b & ~3) : b;
+        for (int q = start + static_cast<int>(threadIdx.x) * VEC; q < e; q += kLongBlock * VEC) {
+            int32_t c[VEC];
+            float v[VEC];
+            load_vec<VEC>(col_ind, q, c);
+            if constexpr (NORM) load_vec<VEC>(val, q, v);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const int nz = q + k;
+                if (nz < b || nz >= e) continue;
+                has |= (c[k] == i);
+                if (c[k] > i) first_gt = min(first_gt, nz - b);
+                if constexpr (NORM) {
+                    const float x = c[k] == i ? v[k] + 1.0f : v[k];
+                    const bool ok = fabsf(x) <= 16777216.0f && x == rintf(x);
+                    integral &= ok ? 1 : 0;
+                    if (ok) {
+                        isum += static_cast<long long>(x);
+                        iabs += static_cast<long long>(fabsf(x));
+                    }
+                }
+            }
+        }
+        has = block_reduce(has, red32, 0) != 0 ? 1 : 0;
+        first_gt = block_reduce(first_gt, red32, 1);
+        if (threadIdx.x == 0) {
+            first_ins[i] = has ? -1 : first_gt;
+            new_len[i] = (e - b) + (has ? 0 : 1);
+        }
+        if constexpr (NORM) {
+            integral = block_reduce(integral, red32, 2);
+            isum = block_reduce(isum, red64, 0);
+            iabs = block_reduce(iabs, red64, 0);
+            float d = 0.0f;
+            if (integral && iabs + (has ? 0 : 1) <= (1ll << 24)) {
+                d = static_cast<float>(isum + (has ? 0 : 1));
+            } else {
+                for (int base = b; base < e; base += kLongBlock * 4) {
+                    const int cnt = min(kLongBlock * 4, e - base);
+                    __syncthreads();
+                    for (int t = threadIdx.x; t < cnt; t += kLongBlock) {
+                        float x = val[base + t];
+                        if (col_ind[base + t] == i) x = x + 1.0f;
+                        stage[t] = x;
+                    }
+                    __syncthreads();
+                    if (threadIdx.x == 0) {
+                        for (int t = 0; t < cnt; ++t) {
+                            if (!has && base - b + t == first_gt) d = d + 1.0f;
+                            d = d + stage[t];
+                        }
+                    }
+                }
+                if (!has && first_gt == e - b) d = d + 1.0f;
+            }
+            if (threadIdx.x == 0) {
+                deg_out[i] = d;
+                dis_out[i] = d > 0.0f ? cr_rcp(cr_sqrt(d)) : 0.0f;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// self_loop_copy for the listed long rows: one workgroup per row.
+template <bool NORM, int VEC>
+__global__ __launch_bounds__(kLongBlock) void self_loop_copy_long_kernel(
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_ind,
+    const float* __restrict__ val, const int32_t* __restrict__ list,
+    const int32_t* __restrict__ count, const int32_t* __restrict__ first_ins,
+    const int32_t* __restrict__ row_ptr_out, const float* __restrict__ dis,
+    int32_t* __restrict__ col_out, float* __restrict__ val_out) {
+    const int n_long = *count;
+    for (int li = blockIdx.x; li < n_long; li += gridDim.x) {
+        const int32_t i = list[li];
+        const int b = row_ptr[i], e = row_ptr[i + 1];
+        const int ins = first_ins[i];
+        const int ob = row_ptr_out[i];
+        float dis_i = 1.0f;
+        if constexpr (NORM) dis_i = dis[i];
+        copy_span<NORM, VEC, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x), i, ins,
+                                         ob, dis_i, dis, col_out, val_out);
+        if (threadIdx.x == 0 && ins >= 0) {
+            float x = 1.0f;
+            if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
+            col_out[ob + ins] = i;
+            val_out[ob + ins] = x;
+        }
     }
 }
 
@@ -552,6 +795,7 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
     probe.take<float>(n);
     probe.take<float>(n);
     probe.take<int64_t>(scan_temp_elems(n));
+    probe.take<int32_t>(n + 1);  // long-row list + its count
     DeviceBuffer own;
     if (workspace == nullptr) {
         own.resize(probe.bytes());
@@ -564,24 +808,77 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
     float* deg = c.take<float>(n);
     float* dis = c.take<float>(n);
     int64_t* scan = c.take<int64_t>(scan_temp_elems(n));
+    int32_t* long_list = c.take<int32_t>(n + 1);
+    int32_t* long_count = long_list + n;
     if (deg_out) deg = deg_out;
     if (dis_out) dis = dis_out;
     const unsigned blocks = static_cast<unsigned>(ceil_div(n * kGroup, 256));
-    if (norm)
-        self_loop_info_kernel<true><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
-                                                           new_len, deg, dis);
+    fill_i32(long_count, 1, 0, s);
+    long_rows_kernel<<<grid_for(n), 256, 0, s>>>(row_ptr, n, long_list, long_count);
+    TG_LAUNCH_CHECK();
+    const unsigned long_grid = 8192;  // grid-stride over the (device-side) long-row list
+    // 128-bit reads when both arrays are 16-byte aligned
+    const bool v4 = (reinterpret_cast<uintptr_t>(col_ind) | reinterpret_cast<uintptr_t>(val)) % 16 == 0;
+    if (norm && v4)
+        self_loop_info_kernel<true, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
+                                                              new_len, deg, dis);
+    else if (norm)
+        self_loop_info_kernel<true, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
+                                                              new_len, deg, dis);
+    else if (v4)
+        self_loop_info_kernel<false, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n,
+                                                               first_ins, new_len, nullptr,
+                                                               nullptr);
     else
-        self_loop_info_kernel<false><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
-                                                            new_len, nullptr, nullptr);
+        self_loop_info_kernel<false, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n,
+                                                               first_ins, new_len, nullptr,
+                                                               nullptr);
+    TG_LAUNCH_CHECK();
+    if (norm && v4)
+        self_loop_info_long_kernel<true, 4><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, new_len, deg, dis);
+    else if (norm)
+        self_loop_info_long_kernel<true, 1><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, new_len, deg, dis);
+    else if (v4)
+        self_loop_info_long_kernel<false, 4><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, new_len, nullptr, nullptr);
+    else
+        self_loop_info_long_kernel<false, 1><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, new_len, nullptr, nullptr);
     TG_LAUNCH_CHECK();
     exclusive_scan_i32(new_len, row_ptr_out, n, scan, s);
-    if (norm)
-        self_loop_copy_kernel<true><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
-                                                           row_ptr_out, dis, col_out, val_out);
+    if (norm && v4)
+        self_loop_copy_kernel<true, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
+                                                              row_ptr_out, dis, col_out, val_out);
+    else if (norm)
+        self_loop_copy_kernel<true, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
+                                                              row_ptr_out, dis, col_out, val_out);
+    else if (v4)
+        self_loop_copy_kernel<false, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n,
+                                                               first_ins, row_ptr_out, nullptr,
+                                                               col_out, val_out);
     else
-        self_loop_copy_kernel<false><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
-                                                            row_ptr_out, nullptr, col_out,
-                                                            val_out);
+        self_loop_copy_kernel<false, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n,
+                                                               first_ins, row_ptr_out, nullptr,
+                                                               col_out, val_out);
+    TG_LAUNCH_CHECK();
+    if (norm && v4)
+        self_loop_copy_long_kernel<true, 4><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
+            val_out);
+    else if (norm)
+        self_loop_copy_long_kernel<true, 1><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
+            val_out);
+    else if (v4)
+        self_loop_copy_long_kernel<false, 4><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, nullptr,
+            col_out, val_out);
+    else
+        self_loop_copy_long_kernel<false, 1><<<long_grid, kLongBlock, 0, s>>>(
+            row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, nullptr,
+            col_out, val_out);
     TG_LAUNCH_CHECK();
     if (own.get()) TG_HIP(hipStreamSynchronize(s));  // own workspace is freed on return
 }
@@ -593,6 +890,7 @@ size_t self_loops_ws(int64_t n) {
     c.take<float>(n);
     c.take<float>(n);
     c.take<int64_t>(scan_temp_elems(n));
+    c.take<int32_t>(n + 1);
     return c.bytes();
 }
 
