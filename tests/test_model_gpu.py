@@ -13,7 +13,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import assert_close, random_csr
+from helpers import assert_close, bits, random_csr
 
 pytestmark = pytest.mark.gpu
 
@@ -186,3 +186,75 @@ def test_zero_weights_default(gpu):
                                  np.ones(2, np.float32))
     out = m.forward(da, gpu.ones((2, 3), device="cuda")).cpu().numpy()
     assert not out.any()
+
+
+@pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
+                                  "sage_concat", "sage_transform_first", "sage_split_rows"])
+def test_blocked_aggregation(gpu, restate, case):
+    """Column-blocked GCN / SAGE-mean aggregation (forced on small graphs
+    with few rows per block): against the oracle at the fast-precision
+    tolerance, deterministic from call to call, and equal to the unblocked
+    path within the same tolerance.  Covers several 256-column sweeps
+    (hidden width 300), a narrow last layer, empty rows, unsorted rows and
+    rows of more than one plan chunk inside a block."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(31)
+    split = case.endswith("split_rows")
+    n = 4000 if split else 3000
+    rows_per_block = 2000 if split else 100
+    a = random_csr(rng, n, n, avg_deg=40, max_deg=3600 if split else 2800, empty_frac=0.05,
+                   sorted_cols=case != "gcn_unsorted")
+    if split:  # a row with more than 1024 entries in each of the two blocks
+        assert (np.diff(a.row_ptr) > 3000).any()
+    if case.startswith("gcn"):
+        # positive edge weights: signed ones put row degrees near 0, whose
+        # 1/sqrt(deg) blows up the normalised weights and the cancellation
+        a.val[:] = np.abs(a.val) + 0.01
+        spec = synth.spec_gcn(48, 300, 7)
+    else:
+        spec = synth.spec_sage(96, 300, 10)
+    w = synth.model_weights(spec, seed=3)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = rng.standard_normal(w[k].shape).astype(np.float32)
+    x = rng.standard_normal((n, spec[0]["in"])).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = {}
+    for blocking in (rows_per_block, 0):
+        m = tg.Model.from_spec(spec, w)
+        if case == "sage_concat":
+            m.set_sage_dataflow(tg.SAGE_CONCAT)
+        elif case.startswith("sage"):
+            m.set_sage_dataflow(tg.SAGE_TRANSFORM_FIRST)
+        m.set_blocking(blocking)
+        got = m.forward(da, _t(gpu, x)).cpu().numpy()
+        again = m.forward(da, _t(gpu, x)).cpu().numpy()
+        np.testing.assert_array_equal(bits(got), bits(again))
+        assert_close(got, want, what=f"{case} blocking={blocking}")
+        outs[blocking] = got
+    assert_close(outs[rows_per_block], outs[0], what=f"{case} blocked vs unblocked")
+    # the blocked passes regroup the sums: some output rounds differently,
+    # which shows the blocked path ran
+    assert (bits(outs[rows_per_block]) != bits(outs[0])).any(), "blocking had no effect"
+
+
+def test_blocking_setting(gpu):
+    """The default leaves small graphs unblocked (bit-identical to blocking
+    off); a negative size other than -1 is rejected."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(4)
+    n = 500
+    a = random_csr(rng, n, n, avg_deg=20)
+    spec = synth.spec_gcn(16, 32, 4)
+    w = synth.model_weights(spec, seed=2)
+    x = _t(gpu, rng.standard_normal((n, 16)).astype(np.float32))
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = []
+    for blocking in (-1, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(blocking)
+        outs.append(m.forward(da, x).cpu().numpy())
+    np.testing.assert_array_equal(bits(outs[0]), bits(outs[1]))
+    with pytest.raises(tg.InvalidArgument, match="rows_per_block"):
+        tg.Model.from_spec(spec, w).set_blocking(-2)

@@ -5,13 +5,17 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <memory>
+#include <vector>
 
 #include "spmm_plan.hpp"
 
 namespace tg {
 
 // Applied to a finished output row element, in this order:
-//   x *= 1/deg (mean; deg = row length, skipped for deg == 0)
+//   x  = out[row, :] + x   (if acc: a column-block pass after the first)
+//   x *= 1/deg (mean; deg = row length, or deg_rp's when given; skipped for
+//               deg == 0)
 //   x += self[row, :]       (if self)
 //   x += bias[:]            (if bias)
 //   x  = act(x)             (TG_ACT_NONE / TG_ACT_RELU)
@@ -25,13 +29,59 @@ struct AggEpilogue {
     int act = 0;
     int post = 0;
     int vec_io = 1;  // set by run_aggregate: stores and epilogue loads are full vectors
+    const int32_t* deg_rp = nullptr;  // mean: degrees from this row_ptr (the unblocked rows)
+    int acc = 0;         // add the row's previous value in out
+    int skip_empty = 0;  // rows with no entries in this pass keep their value in out
 };
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is
 // val[nz] (fma, in nonzero order) or, when val is null, 1 (plain add); with
 // epi.max the element-wise maximum of B[col, :] over the row instead.
+//
+// tile_cols = 0 picks the lane layout from f.  tile_cols = 32 makes every
+// lane group cover one 32-float (one cache line) column tile, tiles running
+// in grid order, so the workgroups resident at a time gather one line per
+// row of B from one or two tiles (the column-blocked passes size their
+// blocks for that).
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
-                   const AggEpilogue& epi, hipStream_t s);
+                   const AggEpilogue& epi, hipStream_t s, int tile_cols = 0);
+
+// Column-blocked form of a CSR structure for aggregations whose gathered
+// matrix is larger than an XCD's L2: the columns (source nodes) are cut into
+// blocks of `rows_per_block`, and each block's nonzeros form a CSR of their
+// own ([block][row] order, the row's order kept inside a block), with one
+// row plan per block.  An aggregation then runs one pass per block, so the
+// lines of B it gathers in a pass (rows_per_block x 128 bytes per 32-column
+// tile) stay in L2; passes add into out in block order (deterministic).
+struct BlockedCSR {
+    int64_t n = 0, nnz = 0, rows_per_block = 0, n_blocks = 0;
+    const int32_t* rp = nullptr;  // row_ptr of the source structure (full row degrees)
+    bool weighted = false;
+    DeviceBuffer brp;  // int32 [n_blocks * n + 1]
+    DeviceBuffer bci;  // int32 [nnz]
+    DeviceBuffer bv;   // float [nnz] (weighted structures)
+    std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
+};
+
+// Blocks with at most 64 column blocks; v may be null (structure only).
+void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
+                   const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
+                   hipStream_t s);
+
+// Rows per block for an n-node structure with nnz entries: `requested` > 0
+// is taken as given, 0 disables blocking, < 0 picks the default (28672
+// rows: 3.5 MB of one 128-byte tile line per row, inside a 4 MB L2) when the
+// passes pay for their extra output traffic (a mean of at least 8 entries
+// per row and block).  Returns 0 when the structure should not be blocked.
+int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
+
+// The same aggregation as run_aggregate over the unblocked structure (same
+// epilogue; weights from the blocked values when bk is weighted), computed
+// block by block.  Each row's sum is regrouped into per-block partial sums,
+// so it equals the unblocked result up to rounding, not bit for bit.
+// epi.max is not supported.
+void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s);
 
 }  // namespace tg

@@ -1,0 +1,160 @@
+// blocked.hip -- column-blocked CSR aggregation for graphs whose gathered
+// feature matrix is larger than the L2 of an XCD.
+//
+// A plain CSR aggregation gathers B[col, :] for every nonzero; with 114.6M
+// nonzeros over 233K source rows almost every gather misses L2 (4 MB per
+// XCD) and the pass runs at HBM/MALL speed.  Cutting the columns into blocks
+// of R source rows and running one pass per block keeps a pass's gathered
+// lines (R x 128 bytes of the 32-column tile being processed) resident in
+// L2, at the cost of re-reading and re-writing the output once per block.
+// That trade pays when rows hold many entries per block (dense, high-degree
+// graphs) and is skipped otherwise (resolve_block_rows).
+//
+// Layout in HBM: the nonzeros of block b, row i are
+// bci/bv[brp[b*n + i] .. brp[b*n + i + 1]), blocks outermost, in the order
+// they have in row i of the source structure.  brp[b*n + n] = brp[(b+1)*n],
+// so block b's row pointer is the slice brp + b*n and ordinary row plans
+// (absolute offsets) index it.
+#include "aggregate.hpp"
+#include "common.hpp"
+#include "spmm_plan.hpp"
+
+#include <algorithm>
+
+namespace tg {
+
+namespace {
+
+constexpr int kMaxBlocks = 64;   // one lane of a wave per column block
+// 28672 rows x one 128-byte line per row and tile = 3.5 MB, inside the 4 MB
+// L2 of an XCD (measured at 233K nodes / 114.6M entries: 16384 and 40960
+// rows per block are both slower)
+constexpr int64_t kDefaultBlockRows = 28672;
+
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+        static_cast<uint32_t>(m >> 32),
+        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
+}
+
+// One wave per row.  The row is walked in 64-entry batches in order; for
+// each block b the wave ballots the entries of the batch that fall in b, so
+// an entry's rank among the row's entries of its block is the count of
+// earlier batches plus the ballot bits below its lane (a stable partition).
+// Lane b keeps block b's running count (COUNT: written to cnt[b*n + row]) or
+// running output position (SCATTER: starting at brp[b*n + row]).
+template <bool SCATTER>
+__global__ __launch_bounds__(256) void block_split_kernel(
+    const int32_t* __restrict__ rp, const int32_t* __restrict__ ci,
+    const float* __restrict__ v, int64_t n, int rows_per_block, int nb,
+    int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;  // uniform per wave
+    const int s = rp[row], e = rp[row + 1];
+    int run = 0;
+    if (SCATTER && lane < nb) run = cnt_or_brp[static_cast<int64_t>(lane) * n + row];
+    for (int i = s; i < e; i += 64) {
+        const int idx = i + lane;
+        const bool valid = idx < e;
+        const int c = valid ? ci[idx] : 0;
+        const int blk = valid ? c / rows_per_block : -1;
+        int pos = 0;
+        for (int b = 0; b < nb; ++b) {
+            const uint64_t m = __ballot(blk == b);
+            if (m == 0) continue;  // uniform: the ballot is the wave's
+            const int base = __shfl(run, b);
+            if (blk == b) pos = base + lanes_below(m);
+            if (lane == b) run += __popcll(m);
+        }
+        if (SCATTER && valid) {
+            bci[pos] = c;
+            if (bv) bv[pos] = v[idx];
+        }
+    }
+    if (!SCATTER && lane < nb) cnt_or_brp[static_cast<int64_t>(lane) * n + row] = run;
+}
+
+}  // namespace
+
+int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz) {
+    if (requested == 0 || n <= 0) return 0;
+    int64_t r = requested > 0 ? requested : kDefaultBlockRows;
+    r = std::max<int64_t>(r, ceil_div(n, kMaxBlocks));
+    const int64_t nb = ceil_div(n, r);
+    if (nb < 2) return 0;
+    if (requested < 0 && nnz < 8 * n * nb) return 0;
+    return r;
+}
+
+void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
+                   const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
+                   hipStream_t s) {
+    require(n > 0 && rows_per_block > 0, "blocked CSR: empty structure or block");
+    require(nnz >= 0 && nnz < (int64_t(1) << 31), "blocked CSR: nnz must be < 2^31");
+    const int64_t nb = ceil_div(n, rows_per_block);
+    require(nb <= kMaxBlocks, "blocked CSR: at most 64 column blocks");
+    require(nb * n < (int64_t(1) << 31), "blocked CSR: blocks x rows must be < 2^31");
+    require(rp != nullptr && (nnz == 0 || ci != nullptr), "blocked CSR: null structure");
+    bk.n = n;
+    bk.nnz = nnz;
+    bk.rows_per_block = rows_per_block;
+    bk.n_blocks = nb;
+    bk.rp = rp;
+    bk.weighted = v != nullptr;
+    bk.brp.resize(static_cast<size_t>(nb * n + 1) * sizeof(int32_t));
+    bk.bci.resize(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(int32_t));
+    if (v) bk.bv.resize(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
+    else bk.bv.resize(0);
+
+    Carver cv(nullptr, 0);
+    cv.take<int32_t>(nb * n);
+    cv.take<int64_t>(scan_temp_elems(nb * n));
+    DeviceBuffer tmp(cv.bytes());
+    Carver c(tmp.get(), tmp.size());
+    int32_t* cnt = c.take<int32_t>(nb * n);
+    int64_t* scan_tmp = c.take<int64_t>(scan_temp_elems(nb * n));
+
+    const unsigned grid = static_cast<unsigned>(ceil_div(n, 4));
+    block_split_kernel<false><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
+                                                   static_cast<int>(nb), cnt, nullptr, nullptr);
+    TG_LAUNCH_CHECK();
+    int32_t* brp = bk.brp.as<int32_t>();
+    exclusive_scan_i32(cnt, brp, nb * n, scan_tmp, s);
+    block_split_kernel<true><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
+                                                  static_cast<int>(nb), brp, bk.bci.as<int32_t>(),
+                                                  v ? bk.bv.as<float>() : nullptr);
+    TG_LAUNCH_CHECK();
+    bk.plans.clear();
+    for (int64_t b = 0; b < nb; ++b) {
+        auto p = std::make_unique<tg_spmm_plan_s>();
+        build_plan(*p, n, nnz, brp + b * n, max_f, 0, s);  // synchronises s
+        bk.plans.push_back(std::move(p));
+    }
+}
+
+void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s) {
+    require(!epi.max, "blocked aggregation: max is not supported");
+    require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
+    if (bk.n == 0 || f == 0) return;
+    const int32_t* bci = bk.bci.as<int32_t>();
+    const float* bv = bk.weighted ? bk.bv.as<float>() : nullptr;
+    // One launch per block over all 32-column tiles of f (grid.y), blocks
+    // in order: the first pass stores every row (zero where the block has no
+    // entries), middle passes touch only rows with entries, the last pass
+    // adds and applies the epilogue to every row.
+    for (int64_t blk = 0; blk < bk.n_blocks; ++blk) {
+        const bool first = blk == 0, last = blk + 1 == bk.n_blocks;
+        AggEpilogue e;
+        if (last) {
+            e = epi;
+            if (e.mean) e.deg_rp = bk.rp;
+        }
+        e.acc = first ? 0 : 1;
+        e.skip_empty = (!first && !last) ? 1 : 0;
+        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32);
+    }
+}
+
+}  // namespace tg

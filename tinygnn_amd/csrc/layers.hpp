@@ -11,6 +11,8 @@
 
 namespace tg {
 
+struct BlockedCSR;
+
 // graph.hip
 // check_dst = false leaves destinations unchecked (load_cora_binary's build,
 // whose result Tensor::sparse_csr validates instead).
@@ -31,14 +33,18 @@ void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col
 size_t self_loops_workspace(int64_t n);
 
 // sage.hip
+// `blocked` (optional): the column-blocked form of the same structure; the
+// mean aggregation then runs block by block (run_aggregate_blocked).
 void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* ci,
-                    const float* h, int64_t ldh, float* out, int64_t ldo, hipStream_t s);
+                    const float* h, int64_t ldh, float* out, int64_t ldo, hipStream_t s,
+                    const BlockedCSR* blocked = nullptr);
 size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
                        int64_t nnz);
 void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
-                  size_t work_bytes, hipStream_t s, int gemm_algo = TG_GEMM_AUTO);
+                  size_t work_bytes, hipStream_t s, int gemm_algo = TG_GEMM_AUTO,
+                  const BlockedCSR* blocked = nullptr);
 
 // gat.hip
 void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,

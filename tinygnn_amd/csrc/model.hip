@@ -15,6 +15,9 @@
 //   * GCN and GAT share A + I's structure (gcn_norm's output has the
 //     structure of add_self_loops' output; GAT reads structure only), so when
 //     both are present the self-loop pass runs once;
+//   * in fast precision and cached mode, the GCN and SAGE-mean aggregations
+//     over large, dense graphs run column blocked (blocked.hip): one pass per
+//     block of source nodes, so the gathered rows of a pass stay in L2;
 //   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
 //     while the adjacency pointers and sizes are unchanged;
 //     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
@@ -77,6 +80,9 @@ struct tg_model_s {
     int sage_dataflow = TG_SAGE_AUTO;
     int precision = TG_PRECISION_FAST;
     int built_precision = -1;  // precision the cached plans were built for
+    int64_t block_rows = -1;   // column blocking (tg_model_set_blocking)
+    int64_t built_block_rows = -2;
+    bool built_cached = false;  // the state was built by a cached-mode call
 
     // adjacency-derived state
     bool have_cache = false;
@@ -86,6 +92,9 @@ struct tg_model_s {
     int64_t key_n = -1, key_nnz = -1;
     DeviceBuffer sl_rp, sl_ci, sl_v;  // A + I (normalised values when GCN is present)
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
+    // column-blocked copies for the large aggregations (fast precision):
+    // A_norm for GCN, A's structure for SAGE-mean
+    std::unique_ptr<tg::BlockedCSR> blk_sl, blk_raw;
 
     // per-forward buffers
     DeviceBuffer act[2], tmp, scores, work;
@@ -100,6 +109,10 @@ struct tg_model_s {
     }
     bool need_raw() const {
         for (auto& l : layers) if (l.type == LType::SAGE) return true;
+        return false;
+    }
+    bool need_raw_mean() const {
+        for (auto& l : layers) if (l.type == LType::SAGE && l.agg == TG_AGG_MEAN) return true;
         return false;
     }
     int64_t max_wide() const {
@@ -212,7 +225,8 @@ void load_weights(tg_model_s& m) {
 void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
-                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision;
+                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision &&
+                      m.built_block_rows == m.block_rows && m.built_cached;
     if (mode == TG_FORWARD_CACHED && same) return;
     m.have_cache = false;
     const int64_t maxf = m.max_wide();
@@ -241,8 +255,27 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     } else {
         m.plan_sl.reset();
     }
+    // column blocking: fast precision (it regroups each row's sum) and cached
+    // mode (its build is paid once, not per call)
+    m.blk_sl.reset();
+    m.blk_raw.reset();
+    if (m.precision == TG_PRECISION_FAST && mode == TG_FORWARD_CACHED) {
+        const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
+        if (m.need_norm() && r_sl > 0) {
+            m.blk_sl = std::make_unique<BlockedCSR>();
+            build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                          m.sl_v.as<float>(), r_sl, maxf, s);
+        }
+        const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
+        if (m.need_raw_mean() && r_raw > 0) {
+            m.blk_raw = std::make_unique<BlockedCSR>();
+            build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s);
+        }
+    }
     m.have_cache = true;
     m.built_precision = m.precision;
+    m.built_block_rows = m.block_rows;
+    m.built_cached = mode == TG_FORWARD_CACHED;
     m.key_rp = rp;
     m.key_ci = ci;
     m.key_v = v;
@@ -329,12 +362,16 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             epi.bias = l.bias ? l.b.as<float>() : nullptr;
             epi.act = l.act;
             epi.post = l.post;
-            run_aggregate(*m.plan_sl, l.out, m.sl_ci.as<int32_t>(), m.sl_v.as<float>(), hw, ldhw,
-                          y, l.out, epi, s);
+            if (m.blk_sl)
+                run_aggregate_blocked(*m.blk_sl, l.out, hw, ldhw, y, l.out, epi, s);
+            else
+                run_aggregate(*m.plan_sl, l.out, m.sl_ci.as<int32_t>(), m.sl_v.as<float>(), hw,
+                              ldhw, y, l.out, epi, s);
         } else if (l.type == LType::SAGE) {
             sage_forward(*m.plan_raw, n, l.in, l.out, l.agg, ci, h, l.wn.as<float>(),
                          l.ws.as<float>(), l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
-                         dataflow, y, m.work.get(), m.work.size(), s, algo);
+                         dataflow, y, m.work.get(), m.work.size(), s, algo,
+                         l.agg == TG_AGG_MEAN ? m.blk_raw.get() : nullptr);
         } else {
             const int64_t wide = l.heads * l.out;
             const int64_t ldwh = gather_pitch(wide);  // line-aligned rows for the gathers
@@ -469,6 +506,14 @@ int tg_model_set_precision(tg_model_t model, int precision) {
         require(precision == TG_PRECISION_FAST || precision == TG_PRECISION_EXACT,
                 "unknown precision");
         model->precision = precision;
+    });
+}
+
+int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        require(rows_per_block >= -1, "tg_model_set_blocking: rows_per_block must be >= -1");
+        model->block_rows = rows_per_block;
     });
 }
 

@@ -43,12 +43,16 @@ size_t sage_ws(int64_t n, int64_t f_in, int64_t f_out, int dataflow) {
 }  // namespace
 
 void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* ci,
-                    const float* h, int64_t ldh, float* out, int64_t ldo, hipStream_t s) {
+                    const float* h, int64_t ldh, float* out, int64_t ldo, hipStream_t s,
+                    const BlockedCSR* blocked) {
     require(agg == TG_AGG_MEAN || agg == TG_AGG_MAX, "SAGELayer: unknown aggregator");
     AggEpilogue epi;
     epi.mean = agg == TG_AGG_MEAN;
     epi.max = agg == TG_AGG_MAX;
-    run_aggregate(p, f, ci, nullptr, h, ldh, out, ldo, epi, s);
+    if (blocked && agg == TG_AGG_MEAN)
+        run_aggregate_blocked(*blocked, f, h, ldh, out, ldo, epi, s);
+    else
+        run_aggregate(p, f, ci, nullptr, h, ldh, out, ldo, epi, s);
 }
 
 size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
@@ -59,7 +63,8 @@ size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int data
 void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
-                  size_t work_bytes, hipStream_t s, int gemm_algo) {
+                  size_t work_bytes, hipStream_t s, int gemm_algo,
+                  const BlockedCSR* blocked) {
     require(n == p.m, "SAGELayer::forward: plan rows differ from n");
     require(f_in >= 0 && f_out >= 0, "SAGELayer::forward: negative size");
     require(act == TG_ACT_NONE || act == TG_ACT_RELU, "SAGELayer: unknown activation");
@@ -80,7 +85,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
     Carver c(work, work_bytes);
     if (dataflow == TG_SAGE_CONCAT) {
         float* aggb = c.take<float>(n * f_in);
-        sage_aggregate(p, f_in, agg, ci, h, f_in, aggb, f_in, s);
+        sage_aggregate(p, f_in, agg, ci, h, f_in, aggb, f_in, s, blocked);
         GemmArgs g;
         g.m = n;
         g.n = f_out;
@@ -132,7 +137,10 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         epi.bias = bias;
         epi.act = act;
         epi.post = post;
-        run_aggregate(p, f_out, ci, nullptr, t + fp, 2 * fp, out, f_out, epi, s);
+        if (blocked)
+            run_aggregate_blocked(*blocked, f_out, t + fp, 2 * fp, out, f_out, epi, s);
+        else
+            run_aggregate(p, f_out, ci, nullptr, t + fp, 2 * fp, out, f_out, epi, s);
     }
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
 }
@@ -152,7 +160,7 @@ int tg_sage_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t f, int agg,
         require(row_ptr == plan->row_ptr, "sage_aggregate: row_ptr differs from the plan's");
         require(n == plan->m, "sage_aggregate: n differs from the plan's rows");
         tg::sage_aggregate(*plan, f, agg, col_ind, h, ldh, out, ldo,
-                           static_cast<hipStream_t>(stream));
+                           static_cast<hipStream_t>(stream), nullptr);
     });
 }
 
@@ -171,7 +179,7 @@ int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
         require(row_ptr == plan->row_ptr, "SAGELayer::forward: row_ptr differs from the plan's");
         tg::sage_forward(*plan, n, f_in, f_out, agg, col_ind, h, w_neigh, w_self, bias, act, post,
                          dataflow, out, workspace, workspace_bytes,
-                         static_cast<hipStream_t>(stream), TG_GEMM_AUTO);
+                         static_cast<hipStream_t>(stream), TG_GEMM_AUTO, nullptr);
     });
 }
 

@@ -292,6 +292,21 @@ template <int VEC>
 __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, int64_t fo,
                                              int64_t f, float* __restrict__ c, int64_t ldc,
                                              const AggEpilogue& epi) {
+    if (epi.acc) {
+        // the sum of the earlier column-block passes, then this pass's
+        const float* prev = c + static_cast<int64_t>(row) * ldc + fo;
+        if (epi.vec_io) {
+            float t[VEC];
+            load_vec<VEC>(prev, t);
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) x[k] = t[k] + x[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k)
+                if (fo + k < f) x[k] = prev[k] + x[k];
+        }
+    }
+    if (epi.deg_rp) deg = epi.deg_rp[row + 1] - epi.deg_rp[row];
     if (epi.mean && deg > 0) {
         const float inv = 1.0f / static_cast<float>(deg);
 #pragma unroll
@@ -367,6 +382,7 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
     if (cid >= n_chunks) return;
     const int4 ch = chunks[cid];
+    if (epi.skip_empty && ch.z == ch.y) return;  // the row keeps its value in C
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
 
     int64_t fo[VPL], fl[VPL];
@@ -375,7 +391,9 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     for (int v = 0; v < VPL; ++v) {
         fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
         ok[v] = fo[v] < f;
-        fl[v] = ok[v] ? fo[v] : 0;  // lanes past f load the row's first vector, never stored
+        // lanes past f load the tile's first vector (the same cache line as
+        // the tile's valid columns; fbase < f), never stored
+        fl[v] = ok[v] ? fo[v] : fbase;
     }
     float acc[VPL][VEC];
 #pragma unroll
@@ -499,6 +517,8 @@ void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const i
     float* partials = p.partials.as<float>();
     const int64_t ldp = round_up(f, VEC);  // padded partial rows
     if (p.n_chunks > 0) {
+        // grid.y = column tile: the workgroups resident at a time (dispatched
+        // in x order) gather from one or two tiles of B
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_chunk_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
@@ -536,7 +556,7 @@ void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const
 
 void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const float* av,
                    const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
-                   hipStream_t s) {
+                   hipStream_t s, int tile_cols) {
     if (p.m == 0 || f == 0) return;
     require(ldb >= f && ldc >= f, "aggregate: leading dimension smaller than f");
     require(epi.self == nullptr || epi.ld_self >= f, "aggregate: self ld smaller than f");
@@ -550,7 +570,14 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
     const int vec = pick_load_vec(f, ldb, B);
     AggEpilogue e = epi;
     e.vec_io = pick_vec(f, {ldc, epi.self ? epi.ld_self : vec}, {C, epi.self, epi.bias}) >= vec;
-    const LaneLayout L = choose_layout(f, vec);
+    require(tile_cols == 0 || tile_cols == 32, "aggregate: tile_cols must be 0 or 32");
+    LaneLayout L = choose_layout(f, vec);
+    if (tile_cols == 32) {
+        L.lpr = 32 / vec;
+        L.vpl = 1;
+        L.tile = 32;
+        L.n_tiles = static_cast<int>(ceil_div(f, 32));
+    }
 #define TG_AGG_MODE(M_)                                                                \
     if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
     if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
