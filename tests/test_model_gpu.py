@@ -189,14 +189,16 @@ def test_zero_weights_default(gpu):
 
 
 @pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
-                                  "sage_concat", "sage_transform_first", "sage_split_rows"])
+                                  "sage_concat", "sage_transform_first", "sage_split_rows",
+                                  "gat", "gat_split_rows"])
 def test_blocked_aggregation(gpu, restate, case):
-    """Column-blocked GCN / SAGE-mean aggregation (forced on small graphs
-    with few rows per block): against the oracle at the fast-precision
-    tolerance, deterministic from call to call, and equal to the unblocked
-    path within the same tolerance.  Covers several 256-column sweeps
-    (hidden width 300), a narrow last layer, empty rows, unsorted rows and
-    rows of more than one plan chunk inside a block."""
+    """Column-blocked GCN / SAGE-mean / GAT aggregation (forced on small
+    graphs with few rows per block): against the oracle at the
+    fast-precision tolerance, deterministic from call to call, and equal to
+    the unblocked path within the same tolerance.  Covers wide layers (300
+    columns: ten tiles), a narrow last layer, three 32-column GAT heads,
+    empty rows, unsorted rows and rows of more than one plan chunk inside a
+    block."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(31)
     split = case.endswith("split_rows")
@@ -211,6 +213,8 @@ def test_blocked_aggregation(gpu, restate, case):
         # 1/sqrt(deg) blows up the normalised weights and the cancellation
         a.val[:] = np.abs(a.val) + 0.01
         spec = synth.spec_gcn(48, 300, 7)
+    elif case.startswith("gat"):
+        spec = synth.spec_gat(48, 32, 3, 7)
     else:
         spec = synth.spec_sage(96, 300, 10)
     w = synth.model_weights(spec, seed=3)
@@ -237,6 +241,30 @@ def test_blocked_aggregation(gpu, restate, case):
     # the blocked passes regroup the sums: some output rounds differently,
     # which shows the blocked path ran
     assert (bits(outs[rows_per_block]) != bits(outs[0])).any(), "blocking had no effect"
+
+
+def test_blocked_gat_fallback(gpu, restate):
+    """GAT layers whose heads are not whole 32-column tiles, or whose heads
+    are averaged, keep the unblocked kernel under blocking (bit-identical to
+    blocking off)."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(8)
+    n = 1500
+    a = random_csr(rng, n, n, avg_deg=30, max_deg=1200, empty_frac=0.05)
+    spec = [dict(type="gat", **{"in": 24}, out=20, heads=2, concat=True, slope=0.2, act=0,
+                 post=2),
+            dict(type="gat", **{"in": 40}, out=32, heads=2, concat=False, slope=0.2, act=0,
+                 post=0)]
+    w = synth.model_weights(spec, seed=6)
+    x = _t(gpu, rng.standard_normal((n, 24)).astype(np.float32))
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = []
+    for blocking in (100, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(blocking)
+        outs.append(m.forward(da, x).cpu().numpy())
+    np.testing.assert_array_equal(bits(outs[0]), bits(outs[1]))
+    assert_close(outs[0], restate.model_forward(spec, w, a, x.cpu().numpy()), what="gat fallback")
 
 
 def test_blocking_setting(gpu):

@@ -16,6 +16,7 @@ namespace tg {
 //   x  = out[row, :] + x   (if acc: a column-block pass after the first)
 //   x *= 1/deg (mean; deg = row length, or deg_rp's when given; skipped for
 //               deg == 0)
+//   x *= row_scale[row * scale_ld + col / scale_cols]   (if row_scale)
 //   x += self[row, :]       (if self)
 //   x += bias[:]            (if bias)
 //   x  = act(x)             (TG_ACT_NONE / TG_ACT_RELU)
@@ -32,6 +33,22 @@ struct AggEpilogue {
     const int32_t* deg_rp = nullptr;  // mean: degrees from this row_ptr (the unblocked rows)
     int acc = 0;         // add the row's previous value in out
     int skip_empty = 0;  // rows with no entries in this pass keep their value in out
+    const float* row_scale = nullptr;  // per row and column group (GAT: 1/sum per head)
+    int64_t scale_ld = 0;
+    int scale_cols = 1;
+};
+
+// Per-edge weights of a GAT layer (instead of CSR values):
+//   w_ij = exp(LeakyReLU(src[i, h] + dst[j, h]) - rmax[i, h])
+// for the head h = (first column of the lane group's tile) / f; the caller
+// guarantees that no tile straddles two heads.
+struct AggGat {
+    const float* src = nullptr;   // [n x heads]
+    const float* dst = nullptr;   // [n x heads]
+    const float* rmax = nullptr;  // [n x heads]: each row's maximum score
+    int heads = 1;
+    int f = 1;                    // columns per head
+    float slope = 0.2f;
 };
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is
@@ -43,9 +60,12 @@ struct AggEpilogue {
 // in grid order, so the workgroups resident at a time gather one line per
 // row of B from one or two tiles (the column-blocked passes size their
 // blocks for that).
+//
+// gat (optional) replaces val by the per-edge attention weights above.
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
-                   const AggEpilogue& epi, hipStream_t s, int tile_cols = 0);
+                   const AggEpilogue& epi, hipStream_t s, int tile_cols = 0,
+                   const AggGat* gat = nullptr);
 
 // Column-blocked form of a CSR structure for aggregations whose gathered
 // matrix is larger than an XCD's L2: the columns (source nodes) are cut into
@@ -82,6 +102,7 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
 // so it equals the unblocked result up to rounding, not bit for bit.
 // epi.max is not supported.
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
-                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s);
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
+                           const AggGat* gat = nullptr);
 
 }  // namespace tg

@@ -134,12 +134,13 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
 }
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
-                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s) {
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
+                           const AggGat* gat) {
     require(!epi.max, "blocked aggregation: max is not supported");
     require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
     if (bk.n == 0 || f == 0) return;
     const int32_t* bci = bk.bci.as<int32_t>();
-    const float* bv = bk.weighted ? bk.bv.as<float>() : nullptr;
+    const float* bv = bk.weighted && !gat ? bk.bv.as<float>() : nullptr;
     // One launch per block over all 32-column tiles of f (grid.y), blocks
     // in order: the first pass stores every row (zero where the block has no
     // entries), middle passes touch only rows with entries, the last pass
@@ -153,7 +154,7 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         }
         e.acc = first ? 0 : 1;
         e.skip_empty = (!first && !last) ? 1 : 0;
-        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32);
+        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32, gat);
     }
 }
 

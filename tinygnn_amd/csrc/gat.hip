@@ -19,6 +19,11 @@
 //   * rows longer than one chunk: every chunk stores its unnormalised sum
 //     with its own (max, sum); gat_reduce_kernel merges them in chunk order
 //     (max of maxima, sums rescaled by exp(m_c - M)).
+//   * column-blocked form (large, dense graphs): gat_stats_kernel first
+//     finds each row's max score and 1/sum per head; the blocked passes
+//     (blocked.hip) then aggregate exp(e_ij - max_i) Wh_j block by block and
+//     the last pass scales by 1/sum_i.
+#include "aggregate.hpp"
 #include "common.hpp"
 #include "device_utils.hpp"
 #include "spmm_plan.hpp"
@@ -486,6 +491,145 @@ void dispatch_gat(const tg_spmm_plan_s& p, const LaneLayout& L, GatArgs& a, hipS
     throw std::logic_error("gat: no kernel for this lane layout");
 }
 
+// Merges two (max, sum of exp(e - max)) pairs of one head; -inf maxima
+// carry an empty sum.
+__device__ __forceinline__ void softmax_merge(float& m, float& s, float mo, float so) {
+    const float M = (m < mo) ? mo : m;
+    const float a = (m == -INFINITY) ? 0.0f : s * expf(m - M);
+    const float c = (mo == -INFINITY) ? 0.0f : so * expf(mo - M);
+    m = M;
+    s = a + c;
+}
+
+// Scores of up to four heads h0.. of entry i: LeakyReLU(src_i + dst_j).
+// vec4 (heads in fours, 16-byte aligned dst): dst_j's four values are one
+// 16-byte load.
+__device__ __forceinline__ void gat_entry_scores(const float* __restrict__ dst, int heads,
+                                                 int h0, int nh, int col, const float (&si)[4],
+                                                 float slope, bool vec4, float (&x)[4]) {
+    const float* dj = dst + static_cast<int64_t>(col) * heads + h0;
+    float d[4];
+    if (vec4) {
+        const float4 t = *reinterpret_cast<const float4*>(dj);
+        d[0] = t.x;
+        d[1] = t.y;
+        d[2] = t.z;
+        d[3] = t.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) d[k] = k < nh ? dj[k] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = lrelu(si[k] + d[k], slope);
+}
+
+// One wave per plan chunk (at most `chunk` entries of one row), heads in
+// groups of four: a first sweep over the chunk takes each head's maximum
+// score e_ij = LeakyReLU(src_i + dst_j), a second sums exp(e_ij - max), four
+// entries' loads in flight per lane; the lanes' values are combined by
+// butterflies (max, then a sum: every lane ends with the same values).  A
+// whole row writes its max and 1/sum (0 for an empty row, as the
+// reference's zero sum gives a zero row before the bias); a split row's
+// chunk writes its (max, sum) pair to its partial slot for
+// gat_stats_merge_kernel.
+__global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__ chunks,
+                                                        int64_t n_chunks,
+                                                        const int32_t* __restrict__ ci,
+                                                        int heads,
+                                                        const float* __restrict__ src,
+                                                        const float* __restrict__ dst,
+                                                        float slope, int vec4,
+                                                        float* __restrict__ rmax,
+                                                        float* __restrict__ rinv,
+                                                        float* __restrict__ pstats) {
+    const int lane = threadIdx.x & 63;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (cid >= n_chunks) return;  // uniform per wave
+    const int4 ch = chunks[cid];
+    const int64_t row = ch.x;
+    constexpr int UN = 4;
+    for (int h0 = 0; h0 < heads; h0 += 4) {
+        const int nh = heads - h0 < 4 ? heads - h0 : 4;
+        float si[4], m[4], sm[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            si[k] = k < nh ? src[row * heads + h0 + k] : 0.0f;
+            m[k] = -INFINITY;
+            sm[k] = 0.0f;
+        }
+        for (int pass = 0; pass < 2; ++pass) {
+            for (int i0 = ch.y; i0 < ch.z; i0 += 64 * UN) {
+                float x[UN][4];
+                bool ok[UN];
+#pragma unroll
+                for (int u = 0; u < UN; ++u) {
+                    const int i = i0 + u * 64 + lane;
+                    ok[u] = i < ch.z;
+                    gat_entry_scores(dst, heads, h0, nh, ok[u] ? ci[i] : 0, si, slope,
+                                     vec4 != 0, x[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < UN; ++u)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if (pass == 0) {
+                            const float y = ok[u] ? x[u][k] : -INFINITY;
+                            m[k] = (m[k] < y) ? y : m[k];
+                        } else {
+                            const float p = expf(x[u][k] - m[k]);
+                            sm[k] = ok[u] ? sm[k] + p : sm[k];
+                        }
+                    }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (pass == 0) {
+                        const float o = __shfl_xor(m[k], off);
+                        m[k] = (m[k] < o) ? o : m[k];
+                    } else {
+                        sm[k] = sm[k] + __shfl_xor(sm[k], off);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (k < nh && lane == k) {
+                if (ch.w < 0) {
+                    rmax[row * heads + h0 + k] = m[k];
+                    rinv[row * heads + h0 + k] = (sm[k] > 0.0f) ? 1.0f / sm[k] : 0.0f;
+                } else {
+                    float* st = pstats + (static_cast<int64_t>(ch.w) * heads + h0 + k) * 2;
+                    st[0] = m[k];
+                    st[1] = sm[k];
+                }
+            }
+        }
+    }
+}
+
+// Split rows: the chunks' (max, sum) pairs merged in chunk order, one
+// thread per row and head.
+__global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __restrict__ split,
+                                                              int64_t n_split, int heads,
+                                                              const float* __restrict__ pstats,
+                                                              float* __restrict__ rmax,
+                                                              float* __restrict__ rinv) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n_split * heads) return;
+    const int4 sp = split[t / heads];
+    const int h = static_cast<int>(t % heads);
+    float m = -INFINITY, s = 0.0f;
+    for (int c = 0; c < sp.z; ++c) {
+        const float* st = pstats + (static_cast<int64_t>(sp.y + c) * heads + h) * 2;
+        softmax_merge(m, s, st[0], st[1]);
+    }
+    rmax[static_cast<int64_t>(sp.x) * heads + h] = m;
+    rinv[static_cast<int64_t>(sp.x) * heads + h] = (s > 0.0f) ? 1.0f / s : 0.0f;
+}
+
 size_t gat_ws(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
     Carver c(nullptr, 0);
     c.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
@@ -579,6 +723,55 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
         TG_LAUNCH_CHECK();
     }
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
+}
+
+bool gat_blocked_ok(int64_t heads, int64_t f, int concat, const float* wh, int64_t ldwh) {
+    if (!concat && heads > 1) return false;             // head average: unblocked kernel
+    if (heads > 1 && f % 32 != 0) return false;         // 32-column tiles inside one head
+    return pick_load_vec(heads * f, ldwh, wh) == 4;     // whole 128-bit lane vectors
+}
+
+void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
+                           int64_t heads, int64_t f, const int32_t* ci, const float* wh,
+                           int64_t ldwh, const float* src, const float* dst, float slope,
+                           const float* bias, int act, int post, float* out, int64_t ldo,
+                           float* rmax, float* rinv, void* work, size_t work_bytes,
+                           hipStream_t s) {
+    require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
+    require(gat_blocked_ok(heads, f, 1, wh, ldwh), "GATLayer: layout not supported blocked");
+    require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
+    if (n == 0) return;
+    // per-chunk (max, sum) pairs of split rows: the unblocked path's pstats
+    Carver cw(work, work_bytes);
+    float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+    if (p.n_chunks > 0) {
+        gat_stats_kernel<<<static_cast<unsigned>(ceil_div(p.n_chunks, 4)), 256, 0, s>>>(
+            p.chunks.as<int4>(), p.n_chunks, ci, static_cast<int>(heads), src, dst, slope,
+            (heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) ? 1 : 0, rmax, rinv,
+            pstats);
+        TG_LAUNCH_CHECK();
+    }
+    if (p.n_split > 0) {
+        gat_stats_merge_kernel<<<static_cast<unsigned>(ceil_div(p.n_split * heads, 256)), 256, 0,
+                                 s>>>(p.split.as<int4>(), p.n_split, static_cast<int>(heads),
+                                      pstats, rmax, rinv);
+        TG_LAUNCH_CHECK();
+    }
+    AggGat g;
+    g.src = src;
+    g.dst = dst;
+    g.rmax = rmax;
+    g.heads = static_cast<int>(heads);
+    g.f = static_cast<int>(f);
+    g.slope = slope;
+    AggEpilogue epi;
+    epi.bias = bias;
+    epi.act = act;
+    epi.post = post;
+    epi.row_scale = rinv;
+    epi.scale_ld = heads;
+    epi.scale_cols = static_cast<int>(f);
+    run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, &g);
 }
 
 }  // namespace tg

@@ -15,9 +15,10 @@
 //   * GCN and GAT share A + I's structure (gcn_norm's output has the
 //     structure of add_self_loops' output; GAT reads structure only), so when
 //     both are present the self-loop pass runs once;
-//   * in fast precision and cached mode, the GCN and SAGE-mean aggregations
-//     over large, dense graphs run column blocked (blocked.hip): one pass per
-//     block of source nodes, so the gathered rows of a pass stay in L2;
+//   * in fast precision and cached mode, the GCN, SAGE-mean and GAT
+//     aggregations over large, dense graphs run column blocked (blocked.hip):
+//     one pass per block of source nodes, so the gathered rows of a pass
+//     stay in L2;
 //   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
 //     while the adjacency pointers and sizes are unchanged;
 //     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
@@ -260,11 +261,12 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     m.blk_sl.reset();
     m.blk_raw.reset();
     if (m.precision == TG_PRECISION_FAST && mode == TG_FORWARD_CACHED) {
+        // A + I: GCN's normalised values, or the structure alone for GAT
         const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
-        if (m.need_norm() && r_sl > 0) {
+        if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
             m.blk_sl = std::make_unique<BlockedCSR>();
             build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                          m.sl_v.as<float>(), r_sl, maxf, s);
+                          m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s);
         }
         const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
         if (m.need_raw_mean() && r_raw > 0) {
@@ -334,7 +336,8 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     m.act[0].reserve(n * wmax * sizeof(float));
     m.act[1].reserve(n * wmax * sizeof(float));
     m.tmp.reserve(n * gather_pitch(wmax) * sizeof(float));
-    m.scores.reserve(2 * n * heads_max * sizeof(float) + 256);
+    // GAT: src and dst scores, then the blocked path's row max and 1/sum
+    m.scores.reserve(4 * n * heads_max * sizeof(float) + 256);
     m.work.reserve(ws);
 
     const float* h = x;
@@ -391,9 +394,19 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             float* dst = src + n * l.heads;
             gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
                        s);
-            gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh, src,
-                          dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
-                          l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s, exact);
+            if (m.blk_sl && gat_blocked_ok(l.heads, l.out, l.concat, wh, ldwh)) {
+                float* rmax = dst + n * l.heads;
+                float* rinv = rmax + n * l.heads;
+                gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,
+                                      m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
+                                      l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
+                                      l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s);
+            } else {
+                gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh,
+                              src, dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act,
+                              l.post, l.concat, y, l.out_cols(), m.work.get(), m.work.size(), s,
+                              exact);
+            }
         }
         h = y;
     }
