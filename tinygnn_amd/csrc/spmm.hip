@@ -420,20 +420,40 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     // with one coalesced access, and the group broadcasts them with
     // shuffles, so the per-edge cost is the row gather alone.  Edges stay in
     // nonzero order (entry t of a batch is lane t / CPL, slot t % CPL).
+    // The next batch's pairs are loaded once the current batch's first
+    // gathers are issued, so their latency overlaps the gathers'.
     constexpr int CPL = U > LPR ? U / LPR : 1;
     constexpr int BE = LPR * CPL;
     const int e = ch.z;
+    // Gather address = the lane's base (B + its column offset) + col * row
+    // pitch in bytes: one 32 x 32 -> 64-bit multiply-add per gather (col >= 0;
+    // the host keeps the pitch in bytes below 2^32).
+    const char* bl[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) bl[v] = reinterpret_cast<const char*>(B + fl[v]);
+    const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
+    int ncl[CPL];
+    float nwl[CPL];
+    auto fetch = [&](int base) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int idx = base + l * CPL + j;
+            ncl[j] = idx < e ? ci[idx] : 0;
+            nwl[j] = 1.0f;
+            if constexpr (MODE == kAggWeighted) nwl[j] = idx < e ? av[idx] : 0.0f;
+        }
+    };
+    fetch(ch.y);
     for (int base = ch.y; base < e; base += BE) {
         int cl[CPL];
         float wl[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int idx = base + l * CPL + j;
-            cl[j] = idx < e ? ci[idx] : 0;
-            wl[j] = 1.0f;
-            if constexpr (MODE == kAggWeighted) wl[j] = idx < e ? av[idx] : 0.0f;
+            cl[j] = ncl[j];
+            wl[j] = nwl[j];
             if constexpr (MODE == kAggGat) {
                 // exp(LeakyReLU(src_i + dst_j) - max_i) (layers.cpp:1056-1109)
+                const int idx = base + l * CPL + j;
                 float x = gsi + gat.dst[static_cast<int64_t>(cl[j]) * gat.heads + gh];
                 x = (x >= 0.0f) ? x : gat.slope * x;
                 wl[j] = idx < e ? expf(x - gmi) : 0.0f;
@@ -458,20 +478,32 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
                 float bv[U][VPL][VEC];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const float* brow = B + static_cast<int64_t>(col[u]) * ldb;
-#pragma unroll
-                    for (int v = 0; v < VPL; ++v) load_vec<VEC>(brow + fl[v], bv[u][v]);
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const bool valid = s0 + u < cnt;  // a select, not a branch
+                    const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
 #pragma unroll
                     for (int v = 0; v < VPL; ++v)
+                        load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                }
+                if (s0 == 0) fetch(base + BE);
+                if (cnt == BE) {  // a full batch: every slot is an entry
 #pragma unroll
-                        for (int k = 0; k < VEC; ++k) {
-                            const float nx = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
-                            acc[v][k] = valid ? nx : acc[v][k];
-                        }
+                    for (int u = 0; u < U; ++u)
+#pragma unroll
+                        for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                            for (int k = 0; k < VEC; ++k)
+                                acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const bool valid = s0 + u < cnt;  // a select, not a branch
+#pragma unroll
+                        for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                            for (int k = 0; k < VEC; ++k) {
+                                const float nx = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
+                                acc[v][k] = valid ? nx : acc[v][k];
+                            }
+                    }
                 }
             }
         }
@@ -579,6 +611,7 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
                    hipStream_t s, int tile_cols, const AggGat* gat) {
     if (p.m == 0 || f == 0) return;
     require(ldb >= f && ldc >= f, "aggregate: leading dimension smaller than f");
+    require(ldb < (int64_t(1) << 30), "aggregate: B's leading dimension must be < 2^30");
     require(epi.self == nullptr || epi.ld_self >= f, "aggregate: self ld smaller than f");
     if (p.n_split > 0)
         require(f <= p.max_f,
