@@ -190,7 +190,7 @@ def test_zero_weights_default(gpu):
 
 @pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
                                   "sage_concat", "sage_transform_first", "sage_split_rows",
-                                  "gat", "gat_split_rows"])
+                                  "gat", "gat_split_rows", "gat_negative_slope"])
 def test_blocked_aggregation(gpu, restate, case):
     """Column-blocked GCN / SAGE-mean / GAT aggregation (forced on small
     graphs with few rows per block): against the oracle at the
@@ -215,6 +215,9 @@ def test_blocked_aggregation(gpu, restate, case):
         spec = synth.spec_gcn(48, 300, 7)
     elif case.startswith("gat"):
         spec = synth.spec_gat(48, 32, 3, 7)
+        if case == "gat_negative_slope":  # LeakyReLU not monotone: per-entry score maxima
+            for layer in spec:
+                layer["slope"] = -0.3
     else:
         spec = synth.spec_sage(96, 300, 10)
     w = synth.model_weights(spec, seed=3)

@@ -501,15 +501,12 @@ __device__ __forceinline__ void softmax_merge(float& m, float& s, float mo, floa
     s = a + c;
 }
 
-// Scores of up to four heads h0.. of entry i: LeakyReLU(src_i + dst_j).
-// vec4 (heads in fours, 16-byte aligned dst): dst_j's four values are one
-// 16-byte load.
-__device__ __forceinline__ void gat_entry_scores(const float* __restrict__ dst, int heads,
-                                                 int h0, int nh, int col, const float (&si)[4],
-                                                 float slope, bool vec4, float (&x)[4]) {
+// dst_j's values for the NH heads h0.. (NH = 4: one 16-byte load).
+template <int NH>
+__device__ __forceinline__ void gat_dst(const float* __restrict__ dst, int heads, int h0,
+                                        int col, float (&d)[NH]) {
     const float* dj = dst + static_cast<int64_t>(col) * heads + h0;
-    float d[4];
-    if (vec4) {
+    if constexpr (NH == 4) {
         const float4 t = *reinterpret_cast<const float4*>(dj);
         d[0] = t.x;
         d[1] = t.y;
@@ -517,29 +514,30 @@ __device__ __forceinline__ void gat_entry_scores(const float* __restrict__ dst, 
         d[3] = t.w;
     } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) d[k] = k < nh ? dj[k] : 0.0f;
+        for (int k = 0; k < NH; ++k) d[k] = dj[k];
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) x[k] = lrelu(si[k] + d[k], slope);
 }
 
 // One wave per plan chunk (at most `chunk` entries of one row), heads in
-// groups of four: a first sweep over the chunk takes each head's maximum
-// score e_ij = LeakyReLU(src_i + dst_j), a second sums exp(e_ij - max), four
-// entries' loads in flight per lane; the lanes' values are combined by
-// butterflies (max, then a sum: every lane ends with the same values).  A
+// groups of NH (4: heads in fours with 16-byte aligned dst; else 1), one
+// sweep over the chunk: each lane takes four entries at a time, computes
+// their scores e_ij = LeakyReLU(src_i + dst_j), raises its running max to
+// the batch's maximum (rescaling its running sum once per batch) and adds
+// exp(e - max) for the batch -- one L2 request per entry and head group,
+// which bounds this kernel.  The lanes' (max, sum) pairs are merged by a
+// butterfly (commutative merges: every lane ends with the same values).  A
 // whole row writes its max and 1/sum (0 for an empty row, as the
 // reference's zero sum gives a zero row before the bias); a split row's
 // chunk writes its (max, sum) pair to its partial slot for
 // gat_stats_merge_kernel.
+template <int NH>
 __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__ chunks,
                                                         int64_t n_chunks,
                                                         const int32_t* __restrict__ ci,
                                                         int heads,
                                                         const float* __restrict__ src,
                                                         const float* __restrict__ dst,
-                                                        float slope, int vec4,
-                                                        float* __restrict__ rmax,
+                                                        float slope, float* __restrict__ rmax,
                                                         float* __restrict__ rinv,
                                                         float* __restrict__ pstats) {
     const int lane = threadIdx.x & 63;
@@ -548,55 +546,53 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
     const int4 ch = chunks[cid];
     const int64_t row = ch.x;
     constexpr int UN = 4;
-    for (int h0 = 0; h0 < heads; h0 += 4) {
-        const int nh = heads - h0 < 4 ? heads - h0 : 4;
-        float si[4], m[4], sm[4];
+    for (int h0 = 0; h0 < heads; h0 += NH) {
+        float si[NH], m[NH], sm[NH];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            si[k] = k < nh ? src[row * heads + h0 + k] : 0.0f;
+        for (int k = 0; k < NH; ++k) {
+            si[k] = src[row * heads + h0 + k];
             m[k] = -INFINITY;
             sm[k] = 0.0f;
         }
-        for (int pass = 0; pass < 2; ++pass) {
-            for (int i0 = ch.y; i0 < ch.z; i0 += 64 * UN) {
-                float x[UN][4];
-                bool ok[UN];
+        for (int i0 = ch.y; i0 < ch.z; i0 += 64 * UN) {
+            float x[UN][NH];
+            bool ok[UN];
 #pragma unroll
-                for (int u = 0; u < UN; ++u) {
-                    const int i = i0 + u * 64 + lane;
-                    ok[u] = i < ch.z;
-                    gat_entry_scores(dst, heads, h0, nh, ok[u] ? ci[i] : 0, si, slope,
-                                     vec4 != 0, x[u]);
-                }
-#pragma unroll
-                for (int u = 0; u < UN; ++u)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        if (pass == 0) {
-                            const float y = ok[u] ? x[u][k] : -INFINITY;
-                            m[k] = (m[k] < y) ? y : m[k];
-                        } else {
-                            const float p = expf(x[u][k] - m[k]);
-                            sm[k] = ok[u] ? sm[k] + p : sm[k];
-                        }
-                    }
+            for (int u = 0; u < UN; ++u) {
+                const int i = i0 + u * 64 + lane;
+                ok[u] = i < ch.z;
+                gat_dst<NH>(dst, heads, h0, ok[u] ? ci[i] : 0, x[u]);
             }
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
+            for (int k = 0; k < NH; ++k) {
+                float bm = m[k];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    if (pass == 0) {
-                        const float o = __shfl_xor(m[k], off);
-                        m[k] = (m[k] < o) ? o : m[k];
-                    } else {
-                        sm[k] = sm[k] + __shfl_xor(sm[k], off);
-                    }
+                for (int u = 0; u < UN; ++u) {
+                    x[u][k] = lrelu(si[k] + x[u][k], slope);
+                    const float y = ok[u] ? x[u][k] : -INFINITY;
+                    bm = (bm < y) ? y : bm;
                 }
+                // the running sum in units of the new max (an unchanged max
+                // scales by exactly 1; the first batch's by exp(-inf) = 0)
+                float acc = (bm == -INFINITY) ? 0.0f : sm[k] * expf(m[k] - bm);
+#pragma unroll
+                for (int u = 0; u < UN; ++u) {
+                    const float p = expf(x[u][k] - bm);
+                    acc = ok[u] ? acc + p : acc;
+                }
+                m[k] = bm;
+                sm[k] = acc;
             }
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (k < nh && lane == k) {
+        for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+            for (int k = 0; k < NH; ++k)
+                softmax_merge(m[k], sm[k], __shfl_xor(m[k], off), __shfl_xor(sm[k], off));
+        }
+#pragma unroll
+        for (int k = 0; k < NH; ++k) {
+            if (lane == k) {
                 if (ch.w < 0) {
                     rmax[row * heads + h0 + k] = m[k];
                     rinv[row * heads + h0 + k] = (sm[k] > 0.0f) ? 1.0f / sm[k] : 0.0f;
@@ -745,10 +741,15 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
     Carver cw(work, work_bytes);
     float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
     if (p.n_chunks > 0) {
-        gat_stats_kernel<<<static_cast<unsigned>(ceil_div(p.n_chunks, 4)), 256, 0, s>>>(
-            p.chunks.as<int4>(), p.n_chunks, ci, static_cast<int>(heads), src, dst, slope,
-            (heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0) ? 1 : 0, rmax, rinv,
-            pstats);
+        const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
+        if (heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0)
+            gat_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                     static_cast<int>(heads), src, dst, slope,
+                                                     rmax, rinv, pstats);
+        else
+            gat_stats_kernel<1><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                     static_cast<int>(heads), src, dst, slope,
+                                                     rmax, rinv, pstats);
         TG_LAUNCH_CHECK();
     }
     if (p.n_split > 0) {
