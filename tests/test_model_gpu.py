@@ -289,3 +289,37 @@ def test_blocking_setting(gpu):
     np.testing.assert_array_equal(bits(outs[0]), bits(outs[1]))
     with pytest.raises(tg.InvalidArgument, match="rows_per_block"):
         tg.Model.from_spec(spec, w).set_blocking(-2)
+
+
+def test_blocking_across_modes(gpu):
+    """Reference-mode forwards never block; a cached forward after one adds
+    the blocked copy to the reused state, and a later reference-mode call
+    drops it again: each result equals a fresh model's in that mode, bit for
+    bit."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(21)
+    n = 2000
+    a = random_csr(rng, n, n, avg_deg=30, max_deg=1500, empty_frac=0.02)
+    a.val[:] = np.abs(a.val) + 0.01
+    spec = synth.spec_gcn(24, 64, 5)
+    w = synth.model_weights(spec, seed=9)
+    x = _t(gpu, rng.standard_normal((n, 24)).astype(np.float32))
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+
+    def fresh(blocking, mode):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(blocking)
+        return bits(m.forward(da, x, mode=mode).cpu().numpy())
+
+    unblocked, blocked = fresh(0, tg.FORWARD_CACHED), fresh(100, tg.FORWARD_CACHED)
+    assert (unblocked != blocked).any()
+    m = tg.Model.from_spec(spec, w)
+    m.set_blocking(100)
+    seq = [(tg.FORWARD_REFERENCE, unblocked), (tg.FORWARD_CACHED, blocked),
+           (tg.FORWARD_CACHED, blocked), (tg.FORWARD_REFERENCE, unblocked),
+           (tg.FORWARD_CACHED, blocked)]
+    for i, (mode, want) in enumerate(seq):
+        got = bits(m.forward(da, x, mode=mode).cpu().numpy())
+        np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode}")
+    m.set_blocking(0)  # a new setting rebuilds the blocked state on the next cached call
+    np.testing.assert_array_equal(bits(m.forward(da, x).cpu().numpy()), unblocked)

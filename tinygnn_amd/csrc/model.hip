@@ -82,8 +82,7 @@ struct tg_model_s {
     int precision = TG_PRECISION_FAST;
     int built_precision = -1;  // precision the cached plans were built for
     int64_t block_rows = -1;   // column blocking (tg_model_set_blocking)
-    int64_t built_block_rows = -2;
-    bool built_cached = false;  // the state was built by a cached-mode call
+    int64_t built_block_rows = -2;  // blocking the blocked copies were built for (-2: none)
 
     // adjacency-derived state
     bool have_cache = false;
@@ -223,13 +222,43 @@ void load_weights(tg_model_s& m) {
     }
 }
 
+// Column-blocked copies (fast precision: they regroup each row's sum), built
+// by cached-mode calls only (the build is paid once, not per call).
+void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
+                     const int32_t* ci, hipStream_t s) {
+    m.blk_sl.reset();
+    m.blk_raw.reset();
+    m.built_block_rows = m.block_rows;
+    if (m.precision != TG_PRECISION_FAST) return;
+    const int64_t maxf = m.max_wide();
+    // A + I: GCN's normalised values, or the structure alone for GAT
+    const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
+    if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
+        m.blk_sl = std::make_unique<BlockedCSR>();
+        build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                      m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s);
+    }
+    const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
+    if (m.need_raw_mean() && r_raw > 0) {
+        m.blk_raw = std::make_unique<BlockedCSR>();
+        build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s);
+    }
+}
+
 void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
-                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision &&
-                      m.built_block_rows == m.block_rows && m.built_cached;
-    if (mode == TG_FORWARD_CACHED && same) return;
+                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision;
+    if (mode == TG_FORWARD_CACHED && same) {
+        // a cached call after a reference-mode one (or a new blocking
+        // setting) adds the blocked copies to the state it reuses
+        if (m.built_block_rows != m.block_rows) prepare_blocked(m, n, nnz, rp, ci, s);
+        return;
+    }
     m.have_cache = false;
+    m.blk_sl.reset();
+    m.blk_raw.reset();
+    m.built_block_rows = -2;  // no blocked copies
     const int64_t maxf = m.max_wide();
     // exact: no row is split, so every row is one fma chain in nonzero order
     const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
@@ -256,33 +285,14 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     } else {
         m.plan_sl.reset();
     }
-    // column blocking: fast precision (it regroups each row's sum) and cached
-    // mode (its build is paid once, not per call)
-    m.blk_sl.reset();
-    m.blk_raw.reset();
-    if (m.precision == TG_PRECISION_FAST && mode == TG_FORWARD_CACHED) {
-        // A + I: GCN's normalised values, or the structure alone for GAT
-        const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
-        if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
-            m.blk_sl = std::make_unique<BlockedCSR>();
-            build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                          m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s);
-        }
-        const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
-        if (m.need_raw_mean() && r_raw > 0) {
-            m.blk_raw = std::make_unique<BlockedCSR>();
-            build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s);
-        }
-    }
     m.have_cache = true;
     m.built_precision = m.precision;
-    m.built_block_rows = m.block_rows;
-    m.built_cached = mode == TG_FORWARD_CACHED;
     m.key_rp = rp;
     m.key_ci = ci;
     m.key_v = v;
     m.key_n = n;
     m.key_nnz = nnz;
+    if (mode == TG_FORWARD_CACHED) prepare_blocked(m, n, nnz, rp, ci, s);
 }
 
 void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int32_t* ci,
