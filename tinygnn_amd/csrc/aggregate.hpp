@@ -13,7 +13,9 @@
 namespace tg {
 
 // Applied to a finished output row element, in this order:
-//   x  = out[row, :] + x   (if acc: a column-block pass after the first)
+//   x  = out[row, :] + x   (if acc, for rows split into several chunks: a
+//                           column-block pass after the first; an unsplit
+//                           row's pass starts its sum from out[row, :])
 //   x *= 1/deg (mean; deg = row length, or deg_rp's when given; skipped for
 //               deg == 0)
 //   x *= row_scale[row * scale_ld + col / scale_cols]   (if row_scale)
@@ -78,16 +80,21 @@ struct BlockedCSR {
     int64_t n = 0, nnz = 0, rows_per_block = 0, n_blocks = 0;
     const int32_t* rp = nullptr;  // row_ptr of the source structure (full row degrees)
     bool weighted = false;
+    // every row's entries fall in non-decreasing blocks (e.g. sorted
+    // columns): block order is nonzero order, so unsplit rows (plans built
+    // with chunk >= the longest row) sum in the unblocked order bit for bit
+    bool in_order = false;
     DeviceBuffer brp;  // int32 [n_blocks * n + 1]
     DeviceBuffer bci;  // int32 [nnz]
     DeviceBuffer bv;   // float [nnz] (weighted structures)
     std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
 };
 
-// Blocks with at most 64 column blocks; v may be null (structure only).
+// Blocks with at most 64 column blocks; v may be null (structure only);
+// chunk: the per-block plans' chunk size (0 = default).
 void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
-                   hipStream_t s);
+                   hipStream_t s, int64_t chunk = 0);
 
 // Rows per block for an n-node structure with nnz entries: `requested` > 0
 // is taken as given, 0 disables blocking, < 0 picks the default (28672
@@ -98,8 +105,9 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
 
 // The same aggregation as run_aggregate over the unblocked structure (same
 // epilogue; weights from the blocked values when bk is weighted), computed
-// block by block.  Each row's sum is regrouped into per-block partial sums,
-// so it equals the unblocked result up to rounding, not bit for bit.
+// block by block, each pass continuing the rows' sums.  With bk.in_order and
+// plans that split no row, the result is bit-identical to the unblocked
+// in-order sums; rows split into chunks are summed from per-chunk partials.
 // epi.max is not supported.
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
                            float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,

@@ -43,11 +43,14 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 // earlier batches plus the ballot bits below its lane (a stable partition).
 // Lane b keeps block b's running count (COUNT: written to cnt[b*n + row]) or
 // running output position (SCATTER: starting at brp[b*n + row]).
+// COUNT also flags (*disorder = 1) a row whose entries step back to an
+// earlier block.
 template <bool SCATTER>
 __global__ __launch_bounds__(256) void block_split_kernel(
     const int32_t* __restrict__ rp, const int32_t* __restrict__ ci,
     const float* __restrict__ v, int64_t n, int rows_per_block, int nb,
-    int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv) {
+    int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv,
+    int32_t* __restrict__ disorder) {
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // uniform per wave
@@ -59,6 +62,10 @@ __global__ __launch_bounds__(256) void block_split_kernel(
         const bool valid = idx < e;
         const int c = valid ? ci[idx] : 0;
         const int blk = valid ? c / rows_per_block : -1;
+        if (!SCATTER) {
+            const bool back = valid && idx > s && ci[idx - 1] / rows_per_block > blk;
+            if (__ballot(back) != 0 && lane == 0) atomicOr(disorder, 1);
+        }
         int pos = 0;
         for (int b = 0; b < nb; ++b) {
             const uint64_t m = __ballot(blk == b);
@@ -89,7 +96,7 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz) {
 
 void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
-                   hipStream_t s) {
+                   hipStream_t s, int64_t chunk) {
     require(n > 0 && rows_per_block > 0, "blocked CSR: empty structure or block");
     require(nnz >= 0 && nnz < (int64_t(1) << 31), "blocked CSR: nnz must be < 2^31");
     const int64_t nb = ceil_div(n, rows_per_block);
@@ -110,27 +117,35 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     Carver cv(nullptr, 0);
     cv.take<int32_t>(nb * n);
     cv.take<int64_t>(scan_temp_elems(nb * n));
+    cv.take<int32_t>(1);
     DeviceBuffer tmp(cv.bytes());
     Carver c(tmp.get(), tmp.size());
     int32_t* cnt = c.take<int32_t>(nb * n);
     int64_t* scan_tmp = c.take<int64_t>(scan_temp_elems(nb * n));
+    int32_t* disorder = c.take<int32_t>(1);
 
+    fill_i32(disorder, 1, 0, s);
     const unsigned grid = static_cast<unsigned>(ceil_div(n, 4));
     block_split_kernel<false><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
-                                                   static_cast<int>(nb), cnt, nullptr, nullptr);
+                                                   static_cast<int>(nb), cnt, nullptr, nullptr,
+                                                   disorder);
     TG_LAUNCH_CHECK();
     int32_t* brp = bk.brp.as<int32_t>();
     exclusive_scan_i32(cnt, brp, nb * n, scan_tmp, s);
     block_split_kernel<true><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
                                                   static_cast<int>(nb), brp, bk.bci.as<int32_t>(),
-                                                  v ? bk.bv.as<float>() : nullptr);
+                                                  v ? bk.bv.as<float>() : nullptr, nullptr);
     TG_LAUNCH_CHECK();
+    int32_t h_disorder = 1;
+    TG_HIP(hipMemcpyAsync(&h_disorder, disorder, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     bk.plans.clear();
     for (int64_t b = 0; b < nb; ++b) {
         auto p = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*p, n, nnz, brp + b * n, max_f, 0, s);  // synchronises s
+        build_plan(*p, n, nnz, brp + b * n, max_f, chunk, s);  // synchronises s
         bk.plans.push_back(std::move(p));
     }
+    TG_HIP(hipStreamSynchronize(s));  // h_disorder, and tmp's last readers
+    bk.in_order = h_disorder == 0;
 }
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,

@@ -15,10 +15,11 @@
 //   * GCN and GAT share A + I's structure (gcn_norm's output has the
 //     structure of add_self_loops' output; GAT reads structure only), so when
 //     both are present the self-loop pass runs once;
-//   * in fast precision and cached mode, the GCN, SAGE-mean and GAT
+//   * in cached mode, the GCN, SAGE-mean and (fast precision) GAT
 //     aggregations over large, dense graphs run column blocked (blocked.hip):
 //     one pass per block of source nodes, so the gathered rows of a pass
-//     stay in L2;
+//     stay in L2; each pass continues the rows' sums, which keeps exact
+//     precision's in-order sums when the rows are in block order;
 //   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
 //     while the adjacency pointers and sizes are unchanged;
 //     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
@@ -222,26 +223,32 @@ void load_weights(tg_model_s& m) {
     }
 }
 
-// Column-blocked copies (fast precision: they regroup each row's sum), built
-// by cached-mode calls only (the build is paid once, not per call).
+// Column-blocked copies, built by cached-mode calls only (the build is paid
+// once, not per call).  Exact precision keeps them only for structures whose
+// rows are in block order, with plans that split no row: each row is then
+// still one chain in nonzero order, continued across the passes.
 void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                      const int32_t* ci, hipStream_t s) {
     m.blk_sl.reset();
     m.blk_raw.reset();
     m.built_block_rows = m.block_rows;
-    if (m.precision != TG_PRECISION_FAST) return;
+    const bool exact = m.precision == TG_PRECISION_EXACT;
     const int64_t maxf = m.max_wide();
-    // A + I: GCN's normalised values, or the structure alone for GAT
+    const int64_t chunk = exact ? (int64_t(1) << 24) : 0;
+    // A + I: GCN's normalised values, or the structure alone for GAT (fast
+    // precision; exact GAT keeps its three sequential passes)
     const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
-    if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
+    if ((m.need_norm() || (m.need_sl() && !exact)) && r_sl > 0) {
         m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                      m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s);
+                      m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s, chunk);
+        if (exact && !m.blk_sl->in_order) m.blk_sl.reset();
     }
     const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
     if (m.need_raw_mean() && r_raw > 0) {
         m.blk_raw = std::make_unique<BlockedCSR>();
-        build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s);
+        build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s, chunk);
+        if (exact && !m.blk_raw->in_order) m.blk_raw.reset();
     }
 }
 
@@ -404,7 +411,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             float* dst = src + n * l.heads;
             gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
                        s);
-            if (m.blk_sl && gat_blocked_ok(l.heads, l.out, l.concat, wh, ldwh)) {
+            if (m.blk_sl && !exact && gat_blocked_ok(l.heads, l.out, l.concat, wh, ldwh)) {
                 float* rmax = dst + n * l.heads;
                 float* rinv = rmax + n * l.heads;
                 gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,

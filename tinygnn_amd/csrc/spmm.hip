@@ -288,11 +288,14 @@ __device__ __forceinline__ float apply_act(float x, int act, int post) {
     return x;
 }
 
+// add_prev: x is the sum of this pass only, to be added to the row's value
+// stored by the earlier column-block passes (split rows); an unsplit row's
+// pass starts its chain from that value instead (see agg_chunk_kernel).
 template <int VEC>
 __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, int64_t fo,
                                              int64_t f, float* __restrict__ c, int64_t ldc,
-                                             const AggEpilogue& epi) {
-    if (epi.acc) {
+                                             const AggEpilogue& epi, bool add_prev) {
+    if (add_prev) {
         // the sum of the earlier column-block passes, then this pass's
         const float* prev = c + static_cast<int64_t>(row) * ldc + fo;
         if (epi.vec_io) {
@@ -414,6 +417,24 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     for (int v = 0; v < VPL; ++v)
 #pragma unroll
         for (int k = 0; k < VEC; ++k) acc[v][k] = MODE == kAggMax ? -INFINITY : 0.0f;
+    // A column-block pass after the first continues an unsplit row's chain
+    // from the value the earlier passes stored.  With the row's entries in
+    // block order equal to their nonzero order (the host checks), the passes
+    // together run the row's one chain in nonzero order, as unblocked.
+    const bool chain = epi.acc && ch.w < 0;
+    if (chain) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+            if (!ok[v]) continue;
+            const float* prev = C + static_cast<int64_t>(ch.x) * ldc + fo[v];
+            if (epi.vec_io) {
+                load_vec<VEC>(prev, acc[v]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) acc[v][k] = fo[v] + k < f ? prev[k] : 0.0f;
+            }
+        }
+    }
 
     // The chunk's entries are walked in batches of BE = max(LPR, U): each
     // lane of the group loads CPL consecutive (col, val) pairs of the batch
@@ -519,7 +540,7 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
         }
 #pragma unroll
         for (int v = 0; v < VPL; ++v)
-            if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], f, C, ldc, epi);
+            if (ok[v]) finish_store<VEC>(acc[v], ch.x, ch.z - ch.y, fo[v], f, C, ldc, epi, false);
     } else {
         float* prow = partials + static_cast<int64_t>(ch.w) * ldp;
 #pragma unroll
@@ -557,7 +578,7 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
             for (int k = 0; k < VEC; ++k)
                 acc[k] = MODE == kAggMax ? ((acc[k] < t[k]) ? t[k] : acc[k]) : acc[k] + t[k];
         }
-        finish_store<VEC>(acc, sp.x, sp.w, fo, f, C, ldc, epi);
+        finish_store<VEC>(acc, sp.x, sp.w, fo, f, C, ldc, epi, epi.acc != 0);
     }
 }
 
