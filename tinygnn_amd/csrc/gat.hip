@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void gat_exact_kernel(GatArgs a) {
     for (int v = 0; v < VPL; ++v) {
         fo[v] = fbase + static_cast<int64_t>(l + v * LPR) * VEC;
         ok[v] = fo[v] < a.ftot;
-        fl[v] = ok[v] ? fo[v] : 0;
+        fl[v] = ok[v] ? fo[v] : fbase;  // the tile's first vector: in bounds, never stored
         hv[v] = ok[v] ? static_cast<int>(fo[v] / a.f) : 0;
         si[v] = srow[hv[v]];
         m[v] = -INFINITY;
@@ -336,8 +336,8 @@ __global__ __launch_bounds__(256) void gat_chunk_kernel(GatArgs a) {
 #pragma unroll
                 for (int v = 0; v < VPL; ++v) {
                     ev[u][v] = a.dst[static_cast<int64_t>(col[u]) * H + hv[v]];
-                    // lanes past ftot load the row's first vector, never stored
-                    ldv<VEC>(wr + (ok[v] ? fo[v] : 0), w[u][v]);
+                    // lanes past ftot load the tile's first vector, never stored
+                    ldv<VEC>(wr + (ok[v] ? fo[v] : fbase), w[u][v]);
                 }
             }
 #pragma unroll
@@ -485,8 +485,6 @@ void dispatch_gat(const tg_spmm_plan_s& p, const LaneLayout& L, GatArgs& a, hipS
     TG_GAT_CASE(16, 1)
     TG_GAT_CASE(32, 1)
     TG_GAT_CASE(64, 1)
-    TG_GAT_CASE(64, 2)
-    TG_GAT_CASE(64, 4)
 #undef TG_GAT_CASE
     throw std::logic_error("gat: no kernel for this lane layout");
 }

@@ -207,18 +207,15 @@ LaneLayout choose_layout(int64_t f, int vec) {
     LaneLayout L{};
     L.vec = vec;
     const int64_t nvec = ceil_div(std::max<int64_t>(f, 1), vec);
-    if (nvec <= 64) {
-        int lpr = 4;
-        while (lpr < nvec) lpr <<= 1;
-        L.lpr = lpr;
-        L.vpl = 1;
-    } else if (nvec <= 128) {
-        L.lpr = 64;
-        L.vpl = 2;
-    } else {
-        L.lpr = 64;
-        L.vpl = 4;
-    }
+    // One vector per lane; rows wider than a wavefront's 64 vectors are cut
+    // into 64-lane column tiles (grid.y), each re-reading the chunk's
+    // indices.  Measured at config D, F=512: two tiles with 16 gathers in
+    // flight per lane take 15.5 ms, one tile of two vectors per lane (8 in
+    // flight) 16.7 ms.
+    int lpr = 4;
+    while (lpr < nvec && lpr < 64) lpr <<= 1;
+    L.lpr = lpr;
+    L.vpl = 1;
     L.tile = L.lpr * L.vpl * L.vec;
     L.n_tiles = static_cast<int>(ceil_div(std::max<int64_t>(f, 1), L.tile));
     return L;
@@ -367,7 +364,8 @@ __device__ __forceinline__ float combine(float acc, float x, float w) {
 
 // Gathers in flight per lane (row vectors of B loaded before they are used):
 // 16 single vectors (measured 2-4% faster than 8 on the column-blocked
-// passes and the narrow SpMM, at lower occupancy), 8 pairs, 4 quads.
+// passes and the narrow SpMM, at lower occupancy); VPL > 1 layouts (no longer
+// chosen) would keep 8 pairs or 4 quads.
 template <int VPL>
 struct Unroll {
     static constexpr int value = VPL == 1 ? 16 : VPL == 2 ? 8 : 4;
@@ -621,8 +619,6 @@ void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const
     TG_AGG_CASE(16, 1)
     TG_AGG_CASE(32, 1)
     TG_AGG_CASE(64, 1)
-    TG_AGG_CASE(64, 2)
-    TG_AGG_CASE(64, 4)
 #undef TG_AGG_CASE
     throw std::logic_error("aggregate: no kernel for this lane layout");
 }

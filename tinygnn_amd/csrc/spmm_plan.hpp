@@ -40,8 +40,9 @@ constexpr int64_t kDefaultChunk = 1024;
 void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
                 int64_t max_f, int64_t chunk, hipStream_t s);
 
-// Lane layout for an aggregation of width f: each lane owns VPL vectors of
-// VEC consecutive floats, LPR lanes own one row's feature tile.
+// Lane layout for an aggregation of width f: each lane owns VPL (= 1)
+// vectors of VEC consecutive floats, LPR lanes own one row's feature tile,
+// and n_tiles tiles cover f.
 struct LaneLayout {
     int vec;     // 1, 2 or 4 floats per access
     int lpr;     // lanes per row group: 4, 8, 16, 32 or 64
