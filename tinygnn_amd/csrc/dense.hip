@@ -57,10 +57,9 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = 0.0f;
 
-    bool tail[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-        tail[j] = DUAL && g.tail_from >= 0 && (n0 + tx * TN + j) >= g.tail_from;
+    // tail columns (dual only): tail_from is a multiple of 8, so a thread's
+    // TN consecutive columns are all tail or all not
+    const bool tail = DUAL && g.tail_from >= 0 && (n0 + tx * TN) >= g.tail_from;
 
     for (int64_t k0 = 0; k0 < K; k0 += BK) {
 #pragma unroll
@@ -94,17 +93,21 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
                 for (int i = 0; i < TM; ++i) a2[i] = As[NP - 1][kk][ty * TM + i];
 #pragma unroll
                 for (int j = 0; j < TN; ++j) b2[j] = Bs[NP - 1][kk][tx * TN + j];
+                if (tail) {
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                    for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) {
-                        if (tail[j]) {
+                        for (int j = 0; j < TN; ++j)
                             acc[i][j] = acc[i][j] + __builtin_fmaf(a[i], b[j], a2[i] * b2[j]);
-                        } else {
+                } else {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) {
                             const float t = __builtin_fmaf(a[i], b[j], acc[i][j]);
                             acc[i][j] = __builtin_fmaf(a2[i], b2[j], t);
                         }
-                    }
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
@@ -196,9 +199,9 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
     for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
-    bool tail[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) tail[j] = DUAL && g.tail_from >= 0 && (n0 + tx * 8 + j) >= g.tail_from;
+    // tail columns (dual only): tail_from is a multiple of 8, so a thread's
+    // eight consecutive columns are all tail or all not
+    const bool tail = DUAL && g.tail_from >= 0 && (n0 + tx * 8) >= g.tail_from;
 
     if (nt > 0) {
         fetch(0);
@@ -222,21 +225,30 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
                 b[p][0] = b0.x; b[p][1] = b0.y; b[p][2] = b0.z; b[p][3] = b0.w;
                 b[p][4] = b1.x; b[p][5] = b1.y; b[p][6] = b1.z; b[p][7] = b1.w;
             }
+            if constexpr (DUAL) {
+                if (tail) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+                    for (int i = 0; i < 8; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if constexpr (DUAL) {
-                        if (tail[j]) {
-                            acc[i][j] = acc[i][j] + __builtin_fmaf(a[0][i], b[0][j], a[1][i] * b[1][j]);
-                        } else {
+                        for (int j = 0; j < 8; ++j)
+                            acc[i][j] = acc[i][j] +
+                                        __builtin_fmaf(a[0][i], b[0][j], a[NP - 1][i] * b[NP - 1][j]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
                             const float t = __builtin_fmaf(a[0][i], b[0][j], acc[i][j]);
-                            acc[i][j] = __builtin_fmaf(a[1][i], b[1][j], t);
+                            acc[i][j] = __builtin_fmaf(a[NP - 1][i], b[NP - 1][j], t);
                         }
-                    } else {
-                        acc[i][j] = __builtin_fmaf(a[0][i], b[0][j], acc[i][j]);
-                    }
                 }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        acc[i][j] = __builtin_fmaf(a[0][i], b[0][j], acc[i][j]);
+            }
         }
         if (kt + 1 < nt) stage(cb ^ 1);
         __syncthreads();
@@ -604,6 +616,8 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
     }
     if (dual) {
         require(g.k1 == g.k2, "matmul: the in-order dual product needs equal k");
+        require(g.tail_from < 0 || g.tail_from % 8 == 0,
+                "matmul: the dual product's tail columns must start at a multiple of 8");
         return dispatch_inorder<true>(g, s);
     }
     dispatch_inorder<false>(g, s);

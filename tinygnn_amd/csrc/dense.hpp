@@ -36,7 +36,7 @@ struct GemmArgs {
     int64_t ldc = 0;
     const float* bias = nullptr;
     int epi = 0;
-    int64_t tail_from = -1;  // in-order dual only; -1 = no tail columns
+    int64_t tail_from = -1;  // in-order dual only; -1 = no tail columns, else a multiple of 8
 };
 
 // Resolves TG_GEMM_AUTO: MFMA when n >= 64 and k >= 32, else in order.
