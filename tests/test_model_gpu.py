@@ -325,27 +325,37 @@ def test_blocking_across_modes(gpu):
     np.testing.assert_array_equal(bits(m.forward(da, x).cpu().numpy()), unblocked)
 
 
-@pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gcn", False),
-                                               ("sage", False)])
+@pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),
+                                               ("gcn", False), ("sage", False), ("gat", False)])
 def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
     """PRECISION_EXACT with forced column blocking: with sorted rows each pass
     continues the rows' fma / add chains in nonzero order, so GCN and SAGE
     outputs still equal the reference's bytes (rows of up to 3,000 entries
-    span many blocks).  Unsorted rows are not in block order: the model then
-    keeps the unblocked exact path, with the same bytes."""
+    span many blocks), and GAT's equal the unblocked exact path's (the
+    reference's order; exp as in that path).  Unsorted rows are not in block
+    order: the model then keeps the unblocked exact path, with the same
+    bytes."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(78)
     n = 3000
     a = random_csr(rng, n, n, avg_deg=25, max_deg=3000, empty_frac=0.02,
                    sorted_cols=sorted_cols)
     x = rng.standard_normal((n, 70)).astype(np.float32)
-    spec = {"gcn": synth.spec_gcn(70, 96, 41), "sage": synth.spec_sage(70, 96, 41)}[model]
+    spec = {"gcn": synth.spec_gcn(70, 96, 41), "sage": synth.spec_sage(70, 96, 41),
+            "gat": synth.spec_gat(70, 32, 3, 41)}[model]
     w = synth.model_weights(spec, seed=4)
     for k in w:
         if k.endswith("bias"):
             w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
     want = restate.model_forward(spec, w, a, x)
     da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    if model == "gat":
+        m0 = tg.Model.from_spec(spec, w)
+        m0.set_precision(tg.PRECISION_EXACT)
+        m0.set_blocking(0)
+        unblocked = m0.forward(da, _t(gpu, x)).cpu().numpy()
+        assert_close(unblocked, want, rtol=2e-6, atol=2e-7, what="gat exact")
+        want = unblocked
     m = tg.Model.from_spec(spec, w)
     m.set_precision(tg.PRECISION_EXACT)
     m.set_blocking(100)

@@ -38,19 +38,23 @@ struct AggEpilogue {
     const float* row_scale = nullptr;  // per row and column group (GAT: 1/sum per head)
     int64_t scale_ld = 0;
     int scale_cols = 1;
+    int exact_exp = 0;  // ELU's exp evaluated as exp_rn (the exact GAT path)
 };
 
 // Per-edge weights of a GAT layer (instead of CSR values):
 //   w_ij = exp(LeakyReLU(src[i, h] + dst[j, h]) - rmax[i, h])
 // for the head h = (first column of the lane group's tile) / f; the caller
-// guarantees that no tile straddles two heads.
+// guarantees that no tile straddles two heads.  exact: the reference's
+// alpha_ij = exp_rn(e_ij - max_i) * rinv[i, h] (layers.cpp:1076-1090).
 struct AggGat {
     const float* src = nullptr;   // [n x heads]
     const float* dst = nullptr;   // [n x heads]
     const float* rmax = nullptr;  // [n x heads]: each row's maximum score
+    const float* rinv = nullptr;  // [n x heads]: 1 / the row's sum (exact only)
     int heads = 1;
     int f = 1;                    // columns per head
     float slope = 0.2f;
+    int exact = 0;
 };
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is

@@ -9,6 +9,14 @@ namespace tg {
 
 constexpr int kWave = 64;  // CDNA wavefront width
 
+// exp evaluated in double and rounded once: the correctly rounded float
+// exp except when the double result falls within an ulp of a float
+// midpoint; the host libm's expf is within 0.502 ulp, so the two agree but
+// for rare last-ulp cases.
+__device__ __forceinline__ float exp_rn(float x) {
+    return static_cast<float>(exp(static_cast<double>(x)));
+}
+
 // Inclusive scan across the 64 lanes of a wavefront.
 template <typename T>
 __device__ __forceinline__ T wave_inclusive_scan(T v) {

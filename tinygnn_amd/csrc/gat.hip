@@ -61,11 +61,6 @@ __device__ __forceinline__ void stv(float* p, const float (&x)[VEC]) {
 
 __device__ __forceinline__ float lrelu(float e, float slope) { return (e >= 0.0f) ? e : slope * e; }
 
-// exp evaluated in double and rounded once: the correctly rounded float
-// exp except when the double result falls within an ulp of a float
-// midpoint; the host libm's expf is within 0.502 ulp, so the two agree but
-// for rare last-ulp cases.
-__device__ __forceinline__ float exp_rn(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
 
 __device__ __forceinline__ float finish_val(float x, const float* bias, int64_t fo, int act,
                                             int post, bool exact = false) {
@@ -604,6 +599,80 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
     }
 }
 
+// Exact statistics (the plan splits no row): one wave per row, heads in
+// groups of NH.  The row's maximum score (order-independent, the max kept as
+// (m < x) ? x : m), then the reference's sum of t_ij = exp_rn(e_ij - max) in
+// nonzero order (layers.cpp:1076-1084): the lanes evaluate 64 entries' t at
+// a time and the wave adds them one by one, in order, through readlane.
+template <int NH>
+__global__ __launch_bounds__(256) void gat_exact_stats_kernel(const int4* __restrict__ chunks,
+                                                              int64_t n_chunks,
+                                                              const int32_t* __restrict__ ci,
+                                                              int heads,
+                                                              const float* __restrict__ src,
+                                                              const float* __restrict__ dst,
+                                                              float slope,
+                                                              float* __restrict__ rmax,
+                                                              float* __restrict__ rinv) {
+    const int lane = threadIdx.x & 63;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (cid >= n_chunks) return;  // uniform per wave
+    const int4 ch = chunks[cid];
+    const int64_t row = ch.x;
+    for (int h0 = 0; h0 < heads; h0 += NH) {
+        float si[NH], m[NH], sum[NH];
+#pragma unroll
+        for (int k = 0; k < NH; ++k) {
+            si[k] = src[row * heads + h0 + k];
+            m[k] = -INFINITY;
+            sum[k] = 0.0f;
+        }
+        for (int i = ch.y + lane; i < ch.z; i += 64) {
+            float d[NH];
+            gat_dst<NH>(dst, heads, h0, ci[i], d);
+#pragma unroll
+            for (int k = 0; k < NH; ++k) {
+                const float x = lrelu(si[k] + d[k], slope);
+                m[k] = (m[k] < x) ? x : m[k];
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+            for (int k = 0; k < NH; ++k) {
+                const float o = __shfl_xor(m[k], off);
+                m[k] = (m[k] < o) ? o : m[k];
+            }
+        }
+        for (int i0 = ch.y; i0 < ch.z; i0 += 64) {
+            const int i = i0 + lane;
+            float t[NH];
+            if (i < ch.z) {
+                float d[NH];
+                gat_dst<NH>(dst, heads, h0, ci[i], d);
+#pragma unroll
+                for (int k = 0; k < NH; ++k) t[k] = exp_rn(lrelu(si[k] + d[k], slope) - m[k]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < NH; ++k) t[k] = 0.0f;
+            }
+            const int cnt = ch.z - i0 < 64 ? ch.z - i0 : 64;
+            for (int q = 0; q < cnt; ++q) {
+#pragma unroll
+                for (int k = 0; k < NH; ++k)
+                    sum[k] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[k]), q));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NH; ++k) {
+            if (lane == k) {
+                rmax[row * heads + h0 + k] = m[k];
+                rinv[row * heads + h0 + k] = (sum[k] > 0.0f) ? 1.0f / sum[k] : 0.0f;
+            }
+        }
+    }
+}
+
 // Split rows: the chunks' (max, sum) pairs merged in chunk order, one
 // thread per row and head.
 __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __restrict__ split,
@@ -730,17 +799,52 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
                            float* rmax, float* rinv, void* work, size_t work_bytes,
-                           hipStream_t s) {
+                           hipStream_t s, bool exact) {
     require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
     require(gat_blocked_ok(heads, f, 1, wh, ldwh), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
     if (n == 0) return;
+    const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+    if (exact) {
+        // the reference's operation order: the plan splits no row, the
+        // blocked rows are in block order, each pass continues the chains
+        require(p.n_split == 0 && bk.in_order,
+                "GATLayer: the exact blocked path needs unsplit, in-order rows");
+        if (p.n_chunks > 0) {
+            const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
+            if (vec4)
+                gat_exact_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks,
+                                                               ci, static_cast<int>(heads), src,
+                                                               dst, slope, rmax, rinv);
+            else
+                gat_exact_stats_kernel<1><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks,
+                                                               ci, static_cast<int>(heads), src,
+                                                               dst, slope, rmax, rinv);
+            TG_LAUNCH_CHECK();
+        }
+        AggGat g;
+        g.src = src;
+        g.dst = dst;
+        g.rmax = rmax;
+        g.rinv = rinv;
+        g.heads = static_cast<int>(heads);
+        g.f = static_cast<int>(f);
+        g.slope = slope;
+        g.exact = 1;
+        AggEpilogue epi;
+        epi.bias = bias;
+        epi.act = act;
+        epi.post = post;
+        epi.exact_exp = 1;
+        run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, &g);
+        return;
+    }
     // per-chunk (max, sum) pairs of split rows: the unblocked path's pstats
     Carver cw(work, work_bytes);
     float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
     if (p.n_chunks > 0) {
         const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
-        if (heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0)
+        if (vec4)
             gat_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
                                                      static_cast<int>(heads), src, dst, slope,
                                                      rmax, rinv, pstats);

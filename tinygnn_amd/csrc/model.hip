@@ -15,8 +15,8 @@
 //   * GCN and GAT share A + I's structure (gcn_norm's output has the
 //     structure of add_self_loops' output; GAT reads structure only), so when
 //     both are present the self-loop pass runs once;
-//   * in cached mode, the GCN, SAGE-mean and (fast precision) GAT
-//     aggregations over large, dense graphs run column blocked (blocked.hip):
+//   * in cached mode, the GCN, SAGE-mean and GAT aggregations over large,
+//     dense graphs run column blocked (blocked.hip):
 //     one pass per block of source nodes, so the gathered rows of a pass
 //     stay in L2; each pass continues the rows' sums, which keeps exact
 //     precision's in-order sums when the rows are in block order;
@@ -235,10 +235,9 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const bool exact = m.precision == TG_PRECISION_EXACT;
     const int64_t maxf = m.max_wide();
     const int64_t chunk = exact ? (int64_t(1) << 24) : 0;
-    // A + I: GCN's normalised values, or the structure alone for GAT (fast
-    // precision; exact GAT keeps its three sequential passes)
+    // A + I: GCN's normalised values, or the structure alone for GAT
     const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
-    if ((m.need_norm() || (m.need_sl() && !exact)) && r_sl > 0) {
+    if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s, chunk);
@@ -411,13 +410,14 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             float* dst = src + n * l.heads;
             gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
                        s);
-            if (m.blk_sl && !exact && gat_blocked_ok(l.heads, l.out, l.concat, wh, ldwh)) {
+            if (m.blk_sl && gat_blocked_ok(l.heads, l.out, l.concat, wh, ldwh)) {
                 float* rmax = dst + n * l.heads;
                 float* rinv = rmax + n * l.heads;
                 gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,
                                       m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
                                       l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
-                                      l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s);
+                                      l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s,
+                                      exact);
             } else {
                 gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh,
                               src, dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act,

@@ -35,7 +35,10 @@ size_t sage_ws(int64_t n, int64_t f_in, int64_t f_out, int dataflow) {
         c.take<float>(n * 2 * fp);
         c.take<float>(f_in * 2 * fp);
     } else {
-        c.take<float>(n * f_in);
+        // the aggregate, and a copy of H, at a 4-float pitch (128-bit gathers)
+        const int64_t fp = round_up(f_in, 4);
+        c.take<float>(n * fp);
+        if (fp != f_in) c.take<float>(n * fp);
     }
     return c.bytes();
 }
@@ -84,18 +87,29 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
     }
     Carver c(work, work_bytes);
     if (dataflow == TG_SAGE_CONCAT) {
-        float* aggb = c.take<float>(n * f_in);
-        sage_aggregate(p, f_in, agg, ci, h, f_in, aggb, f_in, s, blocked);
+        // H at a row pitch of a multiple of 4 floats (a copy when f_in is
+        // not): the aggregation gathers 128-bit vectors and stores the
+        // aggregate at the same pitch; the padding is loaded, never stored.
+        const int64_t fp = round_up(f_in, 4);
+        float* aggb = c.take<float>(n * fp);
+        const float* hg = h;
+        if (fp != f_in) {
+            float* hp = c.take<float>(n * fp);
+            TG_HIP(hipMemcpy2DAsync(hp, fp * sizeof(float), h, f_in * sizeof(float),
+                                    f_in * sizeof(float), n, hipMemcpyDeviceToDevice, s));
+            hg = hp;
+        }
+        sage_aggregate(p, f_in, agg, ci, hg, fp, aggb, fp, s, blocked);
         GemmArgs g;
         g.m = n;
         g.n = f_out;
         g.a1 = aggb;
-        g.lda1 = f_in;
+        g.lda1 = fp;
         g.b1 = wn;
         g.ldb1 = f_out;
         g.k1 = f_in;
-        g.a2 = h;
-        g.lda2 = f_in;
+        g.a2 = hg;
+        g.lda2 = fp;
         g.b2 = ws;
         g.ldb2 = f_out;
         g.k2 = f_in;

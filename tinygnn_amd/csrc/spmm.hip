@@ -275,12 +275,12 @@ __device__ __forceinline__ void store_vec(float* p, const float (&x)[VEC]) {
     *reinterpret_cast<T*>(p) = t;
 }
 
-__device__ __forceinline__ float apply_act(float x, int act, int post) {
+__device__ __forceinline__ float apply_act(float x, int act, int post, int exact_exp = 0) {
     if (act == TG_ACT_RELU) x = (0.0f < x) ? x : 0.0f;
     if (post == TG_POST_RELU) {
         x = (0.0f < x) ? x : 0.0f;
     } else if (post == TG_POST_ELU) {
-        if (x < 0.0f) x = 1.0f * (expf(x) - 1.0f);
+        if (x < 0.0f) x = 1.0f * ((exact_exp ? exp_rn(x) : expf(x)) - 1.0f);
     }
     return x;
 }
@@ -326,7 +326,7 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
             float v = x[k];
             if (epi.self) v += epi.self[static_cast<int64_t>(row) * epi.ld_self + fo + k];
             if (epi.bias) v += epi.bias[fo + k];
-            c[static_cast<int64_t>(row) * ldc + fo + k] = apply_act(v, epi.act, epi.post);
+            c[static_cast<int64_t>(row) * ldc + fo + k] = apply_act(v, epi.act, epi.post, epi.exact_exp);
         }
         return;
     }
@@ -344,7 +344,7 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
     }
     if (epi.act | epi.post) {
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) x[k] = apply_act(x[k], epi.act, epi.post);
+        for (int k = 0; k < VEC; ++k) x[k] = apply_act(x[k], epi.act, epi.post, epi.exact_exp);
     }
     store_vec<VEC>(c + static_cast<int64_t>(row) * ldc + fo, x);
 }
@@ -395,11 +395,12 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
     // GAT: the tile's head, the row's source score and score maximum
     int gh = 0;
-    float gsi = 0.0f, gmi = 0.0f;
+    float gsi = 0.0f, gmi = 0.0f, gri = 1.0f;
     if constexpr (MODE == kAggGat) {
         gh = static_cast<int>(fbase / gat.f);
         gsi = gat.src[static_cast<int64_t>(ch.x) * gat.heads + gh];
         gmi = gat.rmax[static_cast<int64_t>(ch.x) * gat.heads + gh];
+        if (gat.exact) gri = gat.rinv[static_cast<int64_t>(ch.x) * gat.heads + gh];
     }
 
     int64_t fo[VPL], fl[VPL];
@@ -477,7 +478,8 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
                 const int idx = base + l * CPL + j;
                 float x = gsi + gat.dst[static_cast<int64_t>(cl[j]) * gat.heads + gh];
                 x = (x >= 0.0f) ? x : gat.slope * x;
-                wl[j] = idx < e ? expf(x - gmi) : 0.0f;
+                const float t = gat.exact ? exp_rn(x - gmi) * gri : expf(x - gmi);
+                wl[j] = idx < e ? t : 0.0f;
             }
         }
         // U gathers in flight per step; in the chunk's last, partial batch
