@@ -39,6 +39,11 @@ struct AggEpilogue {
     int64_t scale_ld = 0;
     int scale_cols = 1;
     int exact_exp = 0;  // ELU's exp evaluated as exp_rn (the exact GAT path)
+    // B's layout (tile_cols = 32 only): > 0 = tile-major, 32-column tile t
+    // of row j at B + t * b_tile_stride + j * ldb (ldb = 32); 0 = row-major
+    int64_t b_tile_stride = 0;
+    // self's layout: > 0 = tile-major as B (ld_self = 32); 0 = row-major
+    int64_t self_tile_stride = 0;
 };
 
 // Per-edge weights of a GAT layer (instead of CSR values):

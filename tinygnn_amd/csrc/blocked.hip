@@ -169,6 +169,8 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         }
         e.acc = first ? 0 : 1;
         e.skip_empty = (!first && !last) ? 1 : 0;
+        e.b_tile_stride = epi.b_tile_stride;  // B's layout, in every pass
+        e.exact_exp = epi.exact_exp;
         run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32, gat);
     }
 }

@@ -22,6 +22,11 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Element (m, n) of the output, row-major or tile-major (GemmArgs).
+__device__ __forceinline__ int64_t c_index(const GemmArgs& g, int64_t m, int64_t n) {
+    return g.c_tile_stride > 0 ? (n >> 5) * g.c_tile_stride + m * 32 + (n & 31) : m * g.ldc + n;
+}
+
 __device__ __forceinline__ float epi_apply(float x, const float* __restrict__ bias, int64_t n,
                                            int epi) {
     if (bias) x = x + bias[n];
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int64_t gn = n0 + tx * TN + j;
-            if (gn < N) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+            if (gn < N) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j], g.bias, gn, g.epi);
         }
     }
 }
@@ -260,7 +265,7 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int64_t gn = n0 + tx * 8 + j;
-            if (gn < N) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+            if (gn < N) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j], g.bias, gn, g.epi);
         }
     }
 }
@@ -391,7 +396,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int64_t gm = m0 + wm + i * 16 + 4 * q + rr;
-                if (gm < M) g.c[gm * g.ldc + gn] = epi_apply(acc[i][j][rr], g.bias, gn, g.epi);
+                if (gm < M) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j][rr], g.bias, gn, g.epi);
             }
         }
 }
@@ -584,7 +589,10 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
     require(algo == TG_GEMM_AUTO || algo == TG_GEMM_INORDER || algo == TG_GEMM_MFMA,
             "matmul: unknown algorithm");
     if (g.m == 0 || g.n == 0) return;
-    require(g.c != nullptr && g.ldc >= g.n, "matmul: bad output");
+    require(g.c != nullptr && (g.c_tile_stride > 0 ? g.ldc == 32 : g.ldc >= g.n),
+            "matmul: bad output");
+    require(g.c_tile_stride == 0 || g.c_tile_stride >= g.m * 32,
+            "matmul: tile-major output stride smaller than a tile");
     require(g.k1 == 0 || (g.a1 && g.b1 && g.lda1 >= g.k1 && g.ldb1 >= g.n),
             "matmul: bad first operand pair");
     const bool dual = g.a2 != nullptr;

@@ -37,6 +37,10 @@ struct GemmArgs {
     const float* bias = nullptr;
     int epi = 0;
     int64_t tail_from = -1;  // in-order dual only; -1 = no tail columns, else a multiple of 8
+    // C's layout: 0 = row-major (ldc); > 0 = tile-major, column n of row m at
+    // c[(n / 32) * c_tile_stride + m * 32 + n % 32] (ldc = 32): the layout the
+    // column-blocked aggregations gather from
+    int64_t c_tile_stride = 0;
 };
 
 // Resolves TG_GEMM_AUTO: MFMA when n >= 64 and k >= 32, else in order.

@@ -788,10 +788,9 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
 }
 
-bool gat_blocked_ok(int64_t heads, int64_t f, int concat, const float* wh, int64_t ldwh) {
-    if (!concat && heads > 1) return false;             // head average: unblocked kernel
-    if (heads > 1 && f % 32 != 0) return false;         // 32-column tiles inside one head
-    return pick_load_vec(heads * f, ldwh, wh) == 4;     // whole 128-bit lane vectors
+bool gat_blocked_ok(int64_t heads, int64_t f, int concat) {
+    if (!concat && heads > 1) return false;      // head average: unblocked kernel
+    return heads == 1 || f % 32 == 0;            // 32-column tiles inside one head
 }
 
 void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
@@ -801,7 +800,7 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
                            float* rmax, float* rinv, void* work, size_t work_bytes,
                            hipStream_t s, bool exact) {
     require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
-    require(gat_blocked_ok(heads, f, 1, wh, ldwh), "GATLayer: layout not supported blocked");
+    require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
     if (n == 0) return;
     const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;

@@ -56,13 +56,13 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
                    int concat, float* out, int64_t ldo, void* work, size_t work_bytes,
                    hipStream_t s, bool exact = false);
 // Column-blocked GAT aggregation: whether a layer's layout
-// allows it (concatenated or single head, heads of whole 32-column tiles,
-// 16-byte aligned rows of Wh), and the aggregation itself over the blocked
+// allows it (concatenated or single head, heads of whole 32-column tiles),
+// and the aggregation itself over the blocked
 // form of the structure (p, ci: the unblocked structure's plan and columns,
 // for the softmax statistics; rmax, rinv: n x heads scratch; work: at least
 // gat_workspace(p, ...) bytes; exact: the reference's operation order, for
 // a plan that splits no row and a blocked structure in block order).
-bool gat_blocked_ok(int64_t heads, int64_t f, int concat, const float* wh, int64_t ldwh);
+bool gat_blocked_ok(int64_t heads, int64_t f, int concat);
 void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,

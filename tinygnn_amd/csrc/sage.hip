@@ -17,6 +17,8 @@
 #include "dense.hpp"
 #include "spmm_plan.hpp"
 
+#include <algorithm>
+
 namespace tg {
 
 namespace {
@@ -38,7 +40,7 @@ size_t sage_ws(int64_t n, int64_t f_in, int64_t f_out, int dataflow) {
         // the aggregate, and a copy of H, at a 4-float pitch (128-bit gathers)
         const int64_t fp = round_up(f_in, 4);
         c.take<float>(n * fp);
-        if (fp != f_in) c.take<float>(n * fp);
+        c.take<float>(n * std::max(fp, ceil_div(f_in, 32) * 32));
     }
     return c.bytes();
 }
@@ -93,13 +95,28 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         const int64_t fp = round_up(f_in, 4);
         float* aggb = c.take<float>(n * fp);
         const float* hg = h;
-        if (fp != f_in) {
-            float* hp = c.take<float>(n * fp);
-            TG_HIP(hipMemcpy2DAsync(hp, fp * sizeof(float), h, f_in * sizeof(float),
-                                    f_in * sizeof(float), n, hipMemcpyDeviceToDevice, s));
-            hg = hp;
+        if (blocked && agg == TG_AGG_MEAN) {
+            // tile-major copy of H for the blocked passes
+            const int64_t nt = ceil_div(f_in, 32);
+            float* ht = c.take<float>(n * nt * 32);
+            for (int64_t t = 0; t < nt; ++t)
+                TG_HIP(hipMemcpy2DAsync(ht + t * n * 32, 32 * sizeof(float), h + t * 32,
+                                        f_in * sizeof(float),
+                                        std::min<int64_t>(32, f_in - t * 32) * sizeof(float), n,
+                                        hipMemcpyDeviceToDevice, s));
+            AggEpilogue epi;
+            epi.mean = 1;
+            epi.b_tile_stride = n * 32;
+            run_aggregate_blocked(*blocked, f_in, ht, 32, aggb, fp, epi, s);
+        } else {
+            if (fp != f_in) {
+                float* hp = c.take<float>(n * fp);
+                TG_HIP(hipMemcpy2DAsync(hp, fp * sizeof(float), h, f_in * sizeof(float),
+                                        f_in * sizeof(float), n, hipMemcpyDeviceToDevice, s));
+                hg = hp;
+            }
+            sage_aggregate(p, f_in, agg, ci, hg, fp, aggb, fp, s, blocked);
         }
-        sage_aggregate(p, f_in, agg, ci, hg, fp, aggb, fp, s, blocked);
         GemmArgs g;
         g.m = n;
         g.n = f_out;
@@ -109,7 +126,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         g.ldb1 = f_out;
         g.k1 = f_in;
         g.a2 = hg;
-        g.lda2 = fp;
+        g.lda2 = hg == h ? f_in : fp;
         g.b2 = ws;
         g.ldb2 = f_out;
         g.k2 = f_in;
@@ -133,6 +150,10 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
                                 f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
         TG_HIP(hipMemcpy2DAsync(wcat + fp, 2 * fp * sizeof(float), wn, f_out * sizeof(float),
                                 f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
+        // The blocked passes gather T tile-major (32-column tiles of n rows
+        // each, the GEMM's store layout): a tile's rows are one contiguous
+        // slab instead of lines 2 fp floats apart.
+        const bool tiled = blocked != nullptr && fp % 32 == 0;
         GemmArgs g;
         g.m = n;
         g.n = 2 * fp;
@@ -142,19 +163,25 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         g.ldb1 = 2 * fp;
         g.k1 = f_in;
         g.c = t;
-        g.ldc = 2 * fp;
+        g.ldc = tiled ? 32 : 2 * fp;
+        g.c_tile_stride = tiled ? n * 32 : 0;
         gemm(g, gemm_algo, s);
         AggEpilogue epi;
         epi.mean = 1;
         epi.self = t;
-        epi.ld_self = 2 * fp;
+        epi.ld_self = tiled ? 32 : 2 * fp;
+        epi.self_tile_stride = tiled ? n * 32 : 0;
         epi.bias = bias;
         epi.act = act;
         epi.post = post;
-        if (blocked)
+        if (tiled) {
+            epi.b_tile_stride = n * 32;
+            run_aggregate_blocked(*blocked, f_out, t + (fp / 32) * n * 32, 32, out, f_out, epi, s);
+        } else if (blocked) {
             run_aggregate_blocked(*blocked, f_out, t + fp, 2 * fp, out, f_out, epi, s);
-        else
+        } else {
             run_aggregate(p, f_out, ci, nullptr, t + fp, 2 * fp, out, f_out, epi, s);
+        }
     }
     if (own.get()) TG_HIP(hipStreamSynchronize(s));
 }

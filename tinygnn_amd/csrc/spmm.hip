@@ -285,6 +285,15 @@ __device__ __forceinline__ float apply_act(float x, int act, int post, int exact
     return x;
 }
 
+// The self term's vector at column fo of row `row` (row-major or
+// tile-major; a vector never crosses a 32-column tile).
+__device__ __forceinline__ const float* self_row(const AggEpilogue& epi, int row, int64_t fo) {
+    return epi.self_tile_stride > 0
+               ? epi.self + (fo >> 5) * epi.self_tile_stride + static_cast<int64_t>(row) * 32 +
+                     (fo & 31)
+               : epi.self + static_cast<int64_t>(row) * epi.ld_self + fo;
+}
+
 // add_prev: x is the sum of this pass only, to be added to the row's value
 // stored by the earlier column-block passes (split rows); an unsplit row's
 // pass starts its chain from that value instead (see agg_chunk_kernel).
@@ -324,7 +333,7 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
         for (int k = 0; k < VEC; ++k) {
             if (fo + k >= f) break;
             float v = x[k];
-            if (epi.self) v += epi.self[static_cast<int64_t>(row) * epi.ld_self + fo + k];
+            if (epi.self) v += self_row(epi, row, fo)[k];
             if (epi.bias) v += epi.bias[fo + k];
             c[static_cast<int64_t>(row) * ldc + fo + k] = apply_act(v, epi.act, epi.post, epi.exact_exp);
         }
@@ -332,7 +341,7 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
     }
     if (epi.self) {
         float t[VEC];
-        load_vec<VEC>(epi.self + static_cast<int64_t>(row) * epi.ld_self + fo, t);
+        load_vec<VEC>(self_row(epi, row, fo), t);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) x[k] += t[k];
     }
@@ -378,7 +387,7 @@ __device__ __forceinline__ float shfl_f(float v, int src, int width) {
 }
 
 template <int VEC, int LPR, int VPL, int MODE>
-__global__ __launch_bounds__(256) void agg_chunk_kernel(
+__global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
     const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, float* __restrict__ partials, int64_t ldp, int64_t f,
@@ -452,7 +461,11 @@ __global__ __launch_bounds__(256) void agg_chunk_kernel(
     // the host keeps the pitch in bytes below 2^32).
     const char* bl[VPL];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) bl[v] = reinterpret_cast<const char*>(B + fl[v]);
+    for (int v = 0; v < VPL; ++v)
+        bl[v] = reinterpret_cast<const char*>(
+            epi.b_tile_stride > 0 ? B + static_cast<int64_t>(blockIdx.y) * epi.b_tile_stride +
+                                        (fl[v] - fbase)
+                                  : B + fl[v]);
     const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
     int ncl[CPL];
     float nwl[CPL];
@@ -631,9 +644,14 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
                    const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
                    hipStream_t s, int tile_cols, const AggGat* gat) {
     if (p.m == 0 || f == 0) return;
-    require(ldb >= f && ldc >= f, "aggregate: leading dimension smaller than f");
+    const bool tiled_b = epi.b_tile_stride > 0;
+    require(!tiled_b || (tile_cols == 32 && ldb == 32),
+            "aggregate: a tile-major B needs 32-column tiles of pitch 32");
+    require((tiled_b || ldb >= f) && ldc >= f, "aggregate: leading dimension smaller than f");
     require(ldb < (int64_t(1) << 30), "aggregate: B's leading dimension must be < 2^30");
-    require(epi.self == nullptr || epi.ld_self >= f, "aggregate: self ld smaller than f");
+    require(epi.self == nullptr || (epi.self_tile_stride > 0 ? epi.ld_self == 32
+                                                              : epi.ld_self >= f),
+            "aggregate: self ld smaller than f");
     if (p.n_split > 0)
         require(f <= p.max_f,
                 "aggregate: feature width " + std::to_string(f) +
@@ -641,7 +659,7 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
     // Loads use the widest access the rows of B allow (a padded leading
     // dimension lets the last vector of a row run into the padding); stores
     // and the epilogue operands are vectors only when they are aligned too.
-    const int vec = pick_load_vec(f, ldb, B);
+    const int vec = tiled_b ? pick_vec(32, {epi.b_tile_stride}, {B}) : pick_load_vec(f, ldb, B);
     AggEpilogue e = epi;
     e.vec_io = pick_vec(f, {ldc, epi.self ? epi.ld_self : vec}, {C, epi.self, epi.bias}) >= vec;
     require(tile_cols == 0 || tile_cols == 32, "aggregate: tile_cols must be 0 or 32");
