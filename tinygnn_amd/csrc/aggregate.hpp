@@ -44,23 +44,13 @@ struct AggEpilogue {
     int64_t b_tile_stride = 0;
     // self's layout: > 0 = tile-major as B (ld_self = 32); 0 = row-major
     int64_t self_tile_stride = 0;
+    // edge weights in planes of one column group each (GAT: one per head):
+    // the lane group's tile takes plane (first column / w_head_cols), at
+    // val + plane * w_head_stride (tiles never straddle two groups)
+    int64_t w_head_stride = 0;
+    int w_head_cols = 1;
 };
 
-// Per-edge weights of a GAT layer (instead of CSR values):
-//   w_ij = exp(LeakyReLU(src[i, h] + dst[j, h]) - rmax[i, h])
-// for the head h = (first column of the lane group's tile) / f; the caller
-// guarantees that no tile straddles two heads.  exact: the reference's
-// alpha_ij = exp_rn(e_ij - max_i) * rinv[i, h] (layers.cpp:1076-1090).
-struct AggGat {
-    const float* src = nullptr;   // [n x heads]
-    const float* dst = nullptr;   // [n x heads]
-    const float* rmax = nullptr;  // [n x heads]: each row's maximum score
-    const float* rinv = nullptr;  // [n x heads]: 1 / the row's sum (exact only)
-    int heads = 1;
-    int f = 1;                    // columns per head
-    float slope = 0.2f;
-    int exact = 0;
-};
 
 // out[row, :] = epilogue( sum over row nonzeros of w * B[col, :] ), where w is
 // val[nz] (fma, in nonzero order) or, when val is null, 1 (plain add); with
@@ -71,12 +61,9 @@ struct AggGat {
 // in grid order, so the workgroups resident at a time gather one line per
 // row of B from one or two tiles (the column-blocked passes size their
 // blocks for that).
-//
-// gat (optional) replaces val by the per-edge attention weights above.
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
-                   const AggEpilogue& epi, hipStream_t s, int tile_cols = 0,
-                   const AggGat* gat = nullptr);
+                   const AggEpilogue& epi, hipStream_t s, int tile_cols = 0);
 
 // Column-blocked form of a CSR structure for aggregations whose gathered
 // matrix is larger than an XCD's L2: the columns (source nodes) are cut into
@@ -118,8 +105,11 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
 // plans that split no row, the result is bit-identical to the unblocked
 // in-order sums; rows split into chunks are summed from per-chunk partials.
 // epi.max is not supported.
+//
+// weights (optional): per-entry weights in blocked entry order instead of the
+// structure's values (with epi.w_head_stride, one plane per column group).
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
                            float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
-                           const AggGat* gat = nullptr);
+                           const float* weights = nullptr);
 
 }  // namespace tg

@@ -150,12 +150,12 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
                            float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
-                           const AggGat* gat) {
+                           const float* weights) {
     require(!epi.max, "blocked aggregation: max is not supported");
     require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
     if (bk.n == 0 || f == 0) return;
     const int32_t* bci = bk.bci.as<int32_t>();
-    const float* bv = bk.weighted && !gat ? bk.bv.as<float>() : nullptr;
+    const float* bv = weights ? weights : bk.weighted ? bk.bv.as<float>() : nullptr;
     // One launch per block over all 32-column tiles of f (grid.y), blocks
     // in order: the first pass stores every row (zero where the block has no
     // entries), middle passes touch only rows with entries, the last pass
@@ -169,9 +169,12 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         }
         e.acc = first ? 0 : 1;
         e.skip_empty = (!first && !last) ? 1 : 0;
-        e.b_tile_stride = epi.b_tile_stride;  // B's layout, in every pass
+        // the operands' layouts, in every pass
+        e.b_tile_stride = epi.b_tile_stride;
+        e.w_head_stride = epi.w_head_stride;
+        e.w_head_cols = epi.w_head_cols;
         e.exact_exp = epi.exact_exp;
-        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32, gat);
+        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32);
     }
 }
 

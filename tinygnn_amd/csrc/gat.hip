@@ -20,9 +20,10 @@
 //     with its own (max, sum); gat_reduce_kernel merges them in chunk order
 //     (max of maxima, sums rescaled by exp(m_c - M)).
 //   * column-blocked form (large, dense graphs): gat_stats_kernel first
-//     finds each row's max score and 1/sum per head; the blocked passes
-//     (blocked.hip) then aggregate exp(e_ij - max_i) Wh_j block by block and
-//     the last pass scales by 1/sum_i.
+//     finds each row's max score and 1/sum per head, gat_weights_kernel
+//     writes alpha_ij = exp(e_ij - max_i) / sum_i once per entry and head,
+//     and the blocked passes (blocked.hip) aggregate alpha_ij Wh_j block by
+//     block as weighted sums, one weight plane per head.
 #include "aggregate.hpp"
 #include "common.hpp"
 #include "device_utils.hpp"
@@ -673,6 +674,44 @@ __global__ __launch_bounds__(256) void gat_exact_stats_kernel(const int4* __rest
     }
 }
 
+// The attention weights of the column-blocked passes, once per entry and
+// head: alpha_ij = exp(e_ij - max_i) * (1/sum_i) (layers.cpp:1076-1090;
+// exact: exp_rn), e_ij = LeakyReLU(src_i + dst_j), written to plane h at the
+// entry's blocked position (w[h * plane + position]).  One wave per (block,
+// row) segment of the blocked structure (measured faster than a 16-lane
+// group per segment and than one wave per row).
+template <int NH>
+__global__ __launch_bounds__(256) void gat_weights_kernel(
+    const int32_t* __restrict__ brp, const int32_t* __restrict__ bci, int64_t n, int64_t nseg,
+    int heads, const float* __restrict__ src, const float* __restrict__ dst,
+    const float* __restrict__ rmax, const float* __restrict__ rinv, float slope, int exact,
+    float* __restrict__ w, int64_t plane) {
+    const int lane = threadIdx.x & 63;
+    const int64_t seg = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (seg >= nseg) return;  // uniform per wave
+    const int b = brp[seg], e = brp[seg + 1];
+    if (b == e) return;
+    const int64_t row = seg % n;
+    for (int h0 = 0; h0 < heads; h0 += NH) {
+        float si[NH], mi[NH], ri[NH];
+#pragma unroll
+        for (int k = 0; k < NH; ++k) {
+            si[k] = src[row * heads + h0 + k];
+            mi[k] = rmax[row * heads + h0 + k];
+            ri[k] = rinv[row * heads + h0 + k];
+        }
+        for (int i = b + lane; i < e; i += 64) {
+            float d[NH];
+            gat_dst<NH>(dst, heads, h0, bci[i], d);
+#pragma unroll
+            for (int k = 0; k < NH; ++k) {
+                const float x = lrelu(si[k] + d[k], slope) - mi[k];
+                w[static_cast<int64_t>(h0 + k) * plane + i] = (exact ? exp_rn(x) : expf(x)) * ri[k];
+            }
+        }
+    }
+}
+
 // Split rows: the chunks' (max, sum) pairs merged in chunk order, one
 // thread per row and head.
 __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __restrict__ split,
@@ -797,20 +836,21 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
-                           float* rmax, float* rinv, void* work, size_t work_bytes,
-                           hipStream_t s, bool exact) {
+                           float* rmax, float* rinv, float* weights, void* work,
+                           size_t work_bytes, hipStream_t s, bool exact) {
     require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
     require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
+    require(weights != nullptr, "GATLayer: no weight buffer");
     if (n == 0) return;
     const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+    const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
     if (exact) {
         // the reference's operation order: the plan splits no row, the
         // blocked rows are in block order, each pass continues the chains
         require(p.n_split == 0 && bk.in_order,
                 "GATLayer: the exact blocked path needs unsplit, in-order rows");
         if (p.n_chunks > 0) {
-            const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
             if (vec4)
                 gat_exact_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks,
                                                                ci, static_cast<int>(heads), src,
@@ -821,59 +861,48 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
                                                                dst, slope, rmax, rinv);
             TG_LAUNCH_CHECK();
         }
-        AggGat g;
-        g.src = src;
-        g.dst = dst;
-        g.rmax = rmax;
-        g.rinv = rinv;
-        g.heads = static_cast<int>(heads);
-        g.f = static_cast<int>(f);
-        g.slope = slope;
-        g.exact = 1;
-        AggEpilogue epi;
-        epi.bias = bias;
-        epi.act = act;
-        epi.post = post;
-        epi.exact_exp = 1;
-        run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, &g);
-        return;
+    } else {
+        // per-chunk (max, sum) pairs of split rows: the unblocked path's pstats
+        Carver cw(work, work_bytes);
+        float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+        if (p.n_chunks > 0) {
+            if (vec4)
+                gat_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                         static_cast<int>(heads), src, dst, slope,
+                                                         rmax, rinv, pstats);
+            else
+                gat_stats_kernel<1><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                         static_cast<int>(heads), src, dst, slope,
+                                                         rmax, rinv, pstats);
+            TG_LAUNCH_CHECK();
+        }
+        if (p.n_split > 0) {
+            gat_stats_merge_kernel<<<static_cast<unsigned>(ceil_div(p.n_split * heads, 256)), 256,
+                                     0, s>>>(p.split.as<int4>(), p.n_split,
+                                             static_cast<int>(heads), pstats, rmax, rinv);
+            TG_LAUNCH_CHECK();
+        }
     }
-    // per-chunk (max, sum) pairs of split rows: the unblocked path's pstats
-    Carver cw(work, work_bytes);
-    float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
-    if (p.n_chunks > 0) {
-        const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
-        if (vec4)
-            gat_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
-                                                     static_cast<int>(heads), src, dst, slope,
-                                                     rmax, rinv, pstats);
-        else
-            gat_stats_kernel<1><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
-                                                     static_cast<int>(heads), src, dst, slope,
-                                                     rmax, rinv, pstats);
-        TG_LAUNCH_CHECK();
-    }
-    if (p.n_split > 0) {
-        gat_stats_merge_kernel<<<static_cast<unsigned>(ceil_div(p.n_split * heads, 256)), 256, 0,
-                                 s>>>(p.split.as<int4>(), p.n_split, static_cast<int>(heads),
-                                      pstats, rmax, rinv);
-        TG_LAUNCH_CHECK();
-    }
-    AggGat g;
-    g.src = src;
-    g.dst = dst;
-    g.rmax = rmax;
-    g.heads = static_cast<int>(heads);
-    g.f = static_cast<int>(f);
-    g.slope = slope;
+    // the attention weights, once per entry and head, in blocked entry order
+    const int64_t nseg = bk.n_blocks * n;
+    const unsigned wgrid = static_cast<unsigned>(ceil_div(nseg, 4));
+    if (vec4)
+        gat_weights_kernel<4><<<wgrid, 256, 0, s>>>(
+            bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
+            rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
+    else
+        gat_weights_kernel<1><<<wgrid, 256, 0, s>>>(
+            bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
+            rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
+    TG_LAUNCH_CHECK();
     AggEpilogue epi;
     epi.bias = bias;
     epi.act = act;
     epi.post = post;
-    epi.row_scale = rinv;
-    epi.scale_ld = heads;
-    epi.scale_cols = static_cast<int>(f);
-    run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, &g);
+    epi.exact_exp = exact ? 1 : 0;
+    epi.w_head_stride = bk.nnz;
+    epi.w_head_cols = static_cast<int>(f);
+    run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, weights);
 }
 
 }  // namespace tg

@@ -358,15 +358,15 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
     store_vec<VEC>(c + static_cast<int64_t>(row) * ldc + fo, x);
 }
 
-enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2, kAggGat = 3 };
+enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2 };
 
-// One step of a row's reduction: fma with the edge value (SpMM, ops.cpp:
-// 266-287) or the GAT attention weight, a plain add (SAGE mean,
+// One step of a row's reduction: fma with the edge weight (SpMM's value,
+// ops.cpp:266-287, or a GAT attention weight), a plain add (SAGE mean,
 // layers.cpp:604-620), or the element-wise max written as
 // std::max(acc, x) = (acc < x) ? x : acc (layers.cpp:398-417).
 template <int MODE>
 __device__ __forceinline__ float combine(float acc, float x, float w) {
-    if constexpr (MODE == kAggWeighted || MODE == kAggGat) return __builtin_fmaf(w, x, acc);
+    if constexpr (MODE == kAggWeighted) return __builtin_fmaf(w, x, acc);
     if constexpr (MODE == kAggSum) return acc + x;
     return (acc < x) ? x : acc;
 }
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
     const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, float* __restrict__ partials, int64_t ldp, int64_t f,
-    AggEpilogue epi, AggGat gat) {
+    AggEpilogue epi) {
     constexpr int GPB = 256 / LPR;
     constexpr int U = Unroll<VPL>::value;
     constexpr int TILE = LPR * VPL * VEC;
@@ -402,14 +402,9 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int4 ch = chunks[cid];
     if (epi.skip_empty && ch.z == ch.y) return;  // the row keeps its value in C
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
-    // GAT: the tile's head, the row's source score and score maximum
-    int gh = 0;
-    float gsi = 0.0f, gmi = 0.0f, gri = 1.0f;
-    if constexpr (MODE == kAggGat) {
-        gh = static_cast<int>(fbase / gat.f);
-        gsi = gat.src[static_cast<int64_t>(ch.x) * gat.heads + gh];
-        gmi = gat.rmax[static_cast<int64_t>(ch.x) * gat.heads + gh];
-        if (gat.exact) gri = gat.rinv[static_cast<int64_t>(ch.x) * gat.heads + gh];
+    // weights in planes per column group: the tile's group's plane
+    if constexpr (MODE == kAggWeighted) {
+        if (epi.w_head_stride > 0) av += (fbase / epi.w_head_cols) * epi.w_head_stride;
     }
 
     int64_t fo[VPL], fl[VPL];
@@ -486,14 +481,6 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
         for (int j = 0; j < CPL; ++j) {
             cl[j] = ncl[j];
             wl[j] = nwl[j];
-            if constexpr (MODE == kAggGat) {
-                // exp(LeakyReLU(src_i + dst_j) - max_i) (layers.cpp:1056-1109)
-                const int idx = base + l * CPL + j;
-                float x = gsi + gat.dst[static_cast<int64_t>(cl[j]) * gat.heads + gh];
-                x = (x >= 0.0f) ? x : gat.slope * x;
-                const float t = gat.exact ? exp_rn(x - gmi) * gri : expf(x - gmi);
-                wl[j] = idx < e ? t : 0.0f;
-            }
         }
         // U gathers in flight per step; in the chunk's last, partial batch
         // the slots past its end gather row 0 (in bounds: cl is 0 there) and
@@ -508,7 +495,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                 for (int u = 0; u < U; ++u) {
                     col[u] = shfl_i(cl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
                     w[u] = 1.0f;
-                    if constexpr (MODE == kAggWeighted || MODE == kAggGat)
+                    if constexpr (MODE == kAggWeighted)
                         w[u] = shfl_f(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
                 }
                 float bv[U][VPL][VEC];
@@ -600,7 +587,7 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
 template <int VEC, int LPR, int VPL, int MODE>
 void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                 const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
-                const AggEpilogue& epi, const AggGat& gat, hipStream_t s) {
+                const AggEpilogue& epi, hipStream_t s) {
     constexpr int GPB = 256 / LPR;
     float* partials = p.partials.as<float>();
     const int64_t ldp = round_up(f, VEC);  // padded partial rows
@@ -610,7 +597,7 @@ void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const i
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_chunk_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
-            p.chunks.as<int4>(), p.n_chunks, ci, av, B, ldb, C, ldc, partials, ldp, f, epi, gat);
+            p.chunks.as<int4>(), p.n_chunks, ci, av, B, ldb, C, ldc, partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
     if (p.n_split > 0) {
@@ -625,10 +612,10 @@ void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const i
 template <int VEC, int MODE>
 void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                   const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
-                  const AggEpilogue& epi, const AggGat& gat, hipStream_t s) {
+                  const AggEpilogue& epi, hipStream_t s) {
 #define TG_AGG_CASE(LPR_, VPL_)                                                          \
     if (L.lpr == LPR_ && L.vpl == VPL_)                                                  \
-        return launch_agg<VEC, LPR_, VPL_, MODE>(p, L, f, ci, av, B, ldb, C, ldc, epi, gat, s);
+        return launch_agg<VEC, LPR_, VPL_, MODE>(p, L, f, ci, av, B, ldb, C, ldc, epi, s);
     TG_AGG_CASE(4, 1)
     TG_AGG_CASE(8, 1)
     TG_AGG_CASE(16, 1)
@@ -642,7 +629,7 @@ void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const
 
 void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const float* av,
                    const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
-                   hipStream_t s, int tile_cols, const AggGat* gat) {
+                   hipStream_t s, int tile_cols) {
     if (p.m == 0 || f == 0) return;
     const bool tiled_b = epi.b_tile_stride > 0;
     require(!tiled_b || (tile_cols == 32 && ldb == 32),
@@ -670,20 +657,15 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
         L.tile = 32;
         L.n_tiles = static_cast<int>(ceil_div(f, 32));
     }
-    const AggGat ga = gat ? *gat : AggGat{};
-#define TG_AGG_MODE(M_)                                                                 \
-    if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, ga, s);   \
-    if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, ga, s);   \
-    return dispatch_lpr<1, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, ga, s);
-    if (gat) {
-        require(!epi.max && !epi.mean, "aggregate: attention weights take a plain epilogue");
-        require(gat->src && gat->dst && gat->rmax && gat->heads >= 1 && gat->f >= 1,
-                "aggregate: incomplete attention arguments");
-        // every lane group's tile lies inside one head
-        require(gat->heads == 1 || gat->f % L.tile == 0,
-                "aggregate: attention heads must be whole column tiles");
-        TG_AGG_MODE(kAggGat)
-    }
+    // weight planes per column group: every lane group's tile lies in one group
+    require(epi.w_head_stride == 0 ||
+                (av && epi.w_head_cols >= 1 &&
+                 (epi.w_head_cols >= f || epi.w_head_cols % L.tile == 0)),
+            "aggregate: weight planes must cover whole column tiles");
+#define TG_AGG_MODE(M_)                                                                \
+    if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
+    if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
+    return dispatch_lpr<1, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);
     if (epi.max) {
         require(!epi.mean, "aggregate: max and mean are exclusive");
         TG_AGG_MODE(kAggMax)
