@@ -292,10 +292,12 @@ int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);
  *     libm expf is not correctly rounded. */
 enum { TG_PRECISION_FAST = 0, TG_PRECISION_EXACT = 1 };
 int tg_model_set_precision(tg_model_t model, int precision);
-/* Column blocking of the model's GCN, SAGE-mean and GAT aggregations (fast
- * precision, TG_FORWARD_CACHED calls; GAT layers with concatenated or single
- * heads of whole 32-column tiles; no counterpart in the reference, which has
- * one CPU loop per row).  rows_per_block > 0 cuts the adjacency's columns into blocks of
+/* Column blocking of the model's GCN, SAGE-mean and GAT aggregations
+ * (TG_FORWARD_CACHED calls; GAT layers with concatenated or single heads of
+ * whole 32-column tiles; in exact precision only for adjacencies whose rows
+ * are in column order, where the blocked sums keep the reference's order
+ * bit for bit; no counterpart in the reference, which has one CPU loop per
+ * row).  rows_per_block > 0 cuts the adjacency's columns into blocks of
  * that many source nodes (at least n/64) and aggregates block by block, so
  * each pass gathers from a slice of the feature matrix that stays in L2;
  * 0 disables it; -1 (the default) uses 28672 when the graph holds at least
