@@ -401,9 +401,10 @@ class Model:
         lib.check(lib.tg_model_set_precision(self.h, precision))
 
     def set_blocking(self, rows_per_block: int = -1) -> None:
-        """Column blocking of the GCN / SAGE-mean / GAT aggregations in fast
-        precision: rows_per_block source nodes per block, 0 = off, -1 = the
-        default (28672 rows on graphs dense enough to pay)."""
+        """Column blocking of the GCN / SAGE-mean / GAT aggregations of cached
+        forwards (exact precision: only for rows in column order, keeping the
+        reference's summation order): rows_per_block source nodes per block,
+        0 = off, -1 = the default (28672 rows on graphs dense enough to pay)."""
         lib.check(lib.tg_model_set_blocking(self.h, rows_per_block))
 
     def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):
