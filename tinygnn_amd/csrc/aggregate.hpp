@@ -93,10 +93,11 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    hipStream_t s, int64_t chunk = 0);
 
 // Rows per block for an n-node structure with nnz entries: `requested` > 0
-// is taken as given, 0 disables blocking, < 0 picks the default (28672
-// rows: 3.5 MB of one 128-byte tile line per row, inside a 4 MB L2) when the
-// passes pay for their extra output traffic (a mean of at least 8 entries
-// per row and block).  Returns 0 when the structure should not be blocked.
+// is taken as given, 0 disables blocking, < 0 picks the default (equal
+// blocks of at most 38912 rows: about 4.75 MB of one tile's 128-byte lines)
+// when the passes pay for their extra output traffic (a mean of at least 8
+// entries per row and block).  Returns 0 when the structure should not be
+// blocked.
 int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
 
 // The same aggregation as run_aggregate over the unblocked structure (same

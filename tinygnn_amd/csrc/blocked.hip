@@ -26,10 +26,13 @@ namespace tg {
 namespace {
 
 constexpr int kMaxBlocks = 64;   // one lane of a wave per column block
-// 28672 rows x one 128-byte line per row and tile = 3.5 MB, inside the 4 MB
-// L2 of an XCD (measured at 233K nodes / 114.6M entries: 16384 and 40960
-// rows per block are both slower)
-constexpr int64_t kDefaultBlockRows = 28672;
+// Target rows per block, rounded down to equal blocks (n / ceil(n / target)):
+// 38912 rows x 128 bytes = 4.75 MB of one tile's gathered lines.  Measured
+// at 233K nodes / 114.6M entries with tile-major gathers: six equal blocks
+// (38,828 rows) 11.13 / 10.06 / 15.18 ms (GCN / SAGE / GAT); seven or eight
+// equal blocks within 1%; blocks of 16,384 or 20,480 rows 4-12% slower; nine
+// blocks of 28,672 with a 3,589-row tail 3% slower.
+constexpr int64_t kDefaultBlockRows = 38912;
 
 __device__ __forceinline__ int lanes_below(uint64_t m) {
     return static_cast<int>(__builtin_amdgcn_mbcnt_hi(
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void block_split_kernel(
 
 int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz) {
     if (requested == 0 || n <= 0) return 0;
-    int64_t r = requested > 0 ? requested : kDefaultBlockRows;
+    int64_t r = requested > 0 ? requested : ceil_div(n, ceil_div(n, kDefaultBlockRows));
     r = std::max<int64_t>(r, ceil_div(n, kMaxBlocks));
     const int64_t nb = ceil_div(n, r);
     if (nb < 2) return 0;
