@@ -362,3 +362,42 @@ def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
     for _ in range(2):
         got = m.forward(da, _t(gpu, x)).cpu().numpy()
         np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+
+
+@pytest.mark.parametrize("precision", ["fast", "exact"])
+def test_blocked_mixed_stack(gpu, restate, precision):
+    """A stack that shares one blocked A + I between GCN (values) and GAT
+    (attention-weight planes), plus SAGE-mean over blocked A, forced to 40
+    blocks: within the fast tolerance of the oracle, and in exact precision
+    bit-identical to the unblocked exact forward (GCN / SAGE layers keep the
+    reference's order; GAT matches the unblocked exact kernel)."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(44)
+    n = 2500
+    a = random_csr(rng, n, n, avg_deg=35, max_deg=2200, empty_frac=0.03)
+    a.val[:] = np.abs(a.val) + 0.01
+    spec = [dict(type="gat", **{"in": 12}, out=32, heads=2, concat=True, slope=0.2, act=0,
+                 post=2),
+            dict(type="gcn", **{"in": 64}, out=40, act=1, post=0),
+            dict(type="sage", **{"in": 40}, out=33, agg=0, act=1, post=0),
+            dict(type="gat", **{"in": 33}, out=7, heads=1, concat=True, slope=0.2, act=0,
+                 post=0)]
+    w = synth.model_weights(spec, seed=12)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
+    x = rng.standard_normal((n, 12)).astype(np.float32)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = {}
+    for blocking in (0, 63):
+        m = tg.Model.from_spec(spec, w)
+        if precision == "exact":
+            m.set_precision(tg.PRECISION_EXACT)
+        m.set_blocking(blocking)
+        outs[blocking] = m.forward(da, _t(gpu, x)).cpu().numpy()
+    want = restate.model_forward(spec, w, a, x)
+    assert_close(outs[63], want, what=f"{precision} blocked stack")
+    if precision == "exact":
+        np.testing.assert_array_equal(bits(outs[63]), bits(outs[0]))
+    else:
+        assert (bits(outs[63]) != bits(outs[0])).any(), "blocking had no effect"
