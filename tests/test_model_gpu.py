@@ -190,15 +190,18 @@ def test_zero_weights_default(gpu):
 
 @pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
                                   "sage_concat", "sage_transform_first", "sage_split_rows",
-                                  "gat", "gat_split_rows", "gat_negative_slope"])
+                                  "gat", "gat_split_rows", "gat_negative_slope",
+                                  "gat_wide_heads"])
 def test_blocked_aggregation(gpu, restate, case):
     """Column-blocked GCN / SAGE-mean / GAT aggregation (forced on small
     graphs with few rows per block): against the oracle at the
     fast-precision tolerance, deterministic from call to call, and equal to
     the unblocked path within the same tolerance.  Covers wide layers (300
-    columns: ten tiles), a narrow last layer, three 32-column GAT heads,
-    empty rows, unsorted rows and rows of more than one plan chunk inside a
-    block."""
+    columns: ten tiles; A + I passes in 64-column lane groups, SAGE's in
+    32-column ones), a narrow last layer, three 32-column GAT heads (kept in
+    32-column groups), two 64-column heads (one weight plane per 64-column
+    group), empty rows, unsorted rows and rows of more than one plan chunk
+    inside a block."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(31)
     split = case.endswith("split_rows")
@@ -213,6 +216,8 @@ def test_blocked_aggregation(gpu, restate, case):
         # 1/sqrt(deg) blows up the normalised weights and the cancellation
         a.val[:] = np.abs(a.val) + 0.01
         spec = synth.spec_gcn(48, 300, 7)
+    elif case == "gat_wide_heads":  # heads of 64 columns: one weight plane per 64-column group
+        spec = synth.spec_gat(48, 64, 2, 7)
     elif case.startswith("gat"):
         spec = synth.spec_gat(48, 32, 3, 7)
         if case == "gat_negative_slope":  # LeakyReLU not monotone: per-entry score maxima
@@ -326,7 +331,8 @@ def test_blocking_across_modes(gpu):
 
 
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),
-                                               ("gcn", False), ("sage", False), ("gat", False)])
+                                               ("gat64", True), ("gcn", False), ("sage", False),
+                                               ("gat", False)])
 def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
     """PRECISION_EXACT with forced column blocking: with sorted rows each pass
     continues the rows' fma / add chains in nonzero order, so GCN and SAGE
@@ -342,14 +348,14 @@ def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
                    sorted_cols=sorted_cols)
     x = rng.standard_normal((n, 70)).astype(np.float32)
     spec = {"gcn": synth.spec_gcn(70, 96, 41), "sage": synth.spec_sage(70, 96, 41),
-            "gat": synth.spec_gat(70, 32, 3, 41)}[model]
+            "gat": synth.spec_gat(70, 32, 3, 41), "gat64": synth.spec_gat(70, 64, 2, 41)}[model]
     w = synth.model_weights(spec, seed=4)
     for k in w:
         if k.endswith("bias"):
             w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
     want = restate.model_forward(spec, w, a, x)
     da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
-    if model == "gat":
+    if model.startswith("gat"):
         m0 = tg.Model.from_spec(spec, w)
         m0.set_precision(tg.PRECISION_EXACT)
         m0.set_blocking(0)

@@ -404,8 +404,9 @@ class Model:
         """Column blocking of the GCN / SAGE-mean / GAT aggregations of cached
         forwards (exact precision: only for rows in column order, keeping the
         reference's summation order): rows_per_block source nodes per block,
-        0 = off, -1 = the default (equal blocks of at most 38912 rows, on
-        graphs dense enough to pay)."""
+        0 = off, -1 = the default (equal blocks of at most 23552 rows for
+        A + I, the GCN and GAT passes, and 38912 for A, SAGE's mean passes,
+        on graphs dense enough to pay)."""
         lib.check(lib.tg_model_set_blocking(self.h, rows_per_block))
 
     def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):

@@ -56,11 +56,12 @@ struct AggEpilogue {
 // val[nz] (fma, in nonzero order) or, when val is null, 1 (plain add); with
 // epi.max the element-wise maximum of B[col, :] over the row instead.
 //
-// tile_cols = 0 picks the lane layout from f.  tile_cols = 32 makes every
-// lane group cover one 32-float (one cache line) column tile, tiles running
-// in grid order, so the workgroups resident at a time gather one line per
-// row of B from one or two tiles (the column-blocked passes size their
-// blocks for that).
+// tile_cols = 0 picks the lane layout from f.  tile_cols = 32 or 64 makes
+// every lane group cover one column group of that many floats (one or two
+// 128-byte lines per gathered row; with a tile-major B the two lines come
+// from two adjacent tiles), groups running in grid order, so the workgroups
+// resident at a time gather from the rows of one or two groups (the
+// column-blocked passes size their blocks for that).
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
                    const AggEpilogue& epi, hipStream_t s, int tile_cols = 0);
@@ -74,6 +75,8 @@ void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind
 // tile) stay in L2; passes add into out in block order (deterministic).
 struct BlockedCSR {
     int64_t n = 0, nnz = 0, rows_per_block = 0, n_blocks = 0;
+    // columns per lane group in the passes (32 or 64, see resolve_block_rows)
+    int group_cols = 32;
     const int32_t* rp = nullptr;  // row_ptr of the source structure (full row degrees)
     bool weighted = false;
     // every row's entries fall in non-decreasing blocks (e.g. sorted
@@ -92,13 +95,14 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
                    hipStream_t s, int64_t chunk = 0);
 
-// Rows per block for an n-node structure with nnz entries: `requested` > 0
-// is taken as given, 0 disables blocking, < 0 picks the default (equal
-// blocks of at most 38912 rows: about 4.75 MB of one tile's 128-byte lines)
-// when the passes pay for their extra output traffic (a mean of at least 8
-// entries per row and block).  Returns 0 when the structure should not be
-// blocked.
-int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz);
+// Rows per block for an n-node structure with nnz entries whose passes use
+// lane groups of group_cols columns: `requested` > 0 is taken as given, 0
+// disables blocking, < 0 picks the default (equal blocks of at most 38912
+// rows for 32-column groups, 23552 for 64-column ones: 4.75 / 5.75 MB of the
+// gathered lines) when the passes pay for their extra output traffic (a
+// mean of at least 8 entries per row and block).  Returns 0 when the
+// structure should not be blocked.
+int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_cols = 32);
 
 // The same aggregation as run_aggregate over the unblocked structure (same
 // epilogue; weights from the blocked values when bk is weighted), computed

@@ -26,13 +26,20 @@ namespace tg {
 namespace {
 
 constexpr int kMaxBlocks = 64;   // one lane of a wave per column block
-// Target rows per block, rounded down to equal blocks (n / ceil(n / target)):
-// 38912 rows x 128 bytes = 4.75 MB of one tile's gathered lines.  Measured
-// at 233K nodes / 114.6M entries with tile-major gathers: six equal blocks
-// (38,828 rows) 11.13 / 10.06 / 15.18 ms (GCN / SAGE / GAT); seven or eight
-// equal blocks within 1%; blocks of 16,384 or 20,480 rows 4-12% slower; nine
-// blocks of 28,672 with a 3,589-row tail 3% slower.
-constexpr int64_t kDefaultBlockRows = 38912;
+// Target rows per block, rounded down to equal blocks (n / ceil(n / target)).
+// Measured at 233K nodes / 114.6M entries with tile-major gathers:
+// * 32-column lane groups: 38912 rows x 128 bytes = 4.75 MB of one tile's
+//   gathered lines; six equal blocks (38,828 rows) 11.13 / 10.06 / 15.18 ms
+//   (GCN / SAGE / GAT); seven or eight equal blocks within 1%; blocks of
+//   16,384 or 20,480 rows 4-12% slower.
+// * 64-column lane groups read each block's indices once per two tiles (the
+//   index stream, not the gathered bytes, bounds a pass) and gather two
+//   lines per row, so they take smaller blocks: ten blocks of 23,297 rows
+//   10.59 / 10.31 / 14.68 ms; eleven or twelve blocks within 1%; eight 6%
+//   and six 16% slower.  SAGE's mean passes (no value stream) keep
+//   32-column groups.
+constexpr int64_t kDefaultBlockRows32 = 38912;
+constexpr int64_t kDefaultBlockRows64 = 23552;
 
 __device__ __forceinline__ int lanes_below(uint64_t m) {
     return static_cast<int>(__builtin_amdgcn_mbcnt_hi(
@@ -87,9 +94,10 @@ __global__ __launch_bounds__(256) void block_split_kernel(
 
 }  // namespace
 
-int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz) {
+int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_cols) {
     if (requested == 0 || n <= 0) return 0;
-    int64_t r = requested > 0 ? requested : ceil_div(n, ceil_div(n, kDefaultBlockRows));
+    const int64_t target = group_cols == 64 ? kDefaultBlockRows64 : kDefaultBlockRows32;
+    int64_t r = requested > 0 ? requested : ceil_div(n, ceil_div(n, target));
     r = std::max<int64_t>(r, ceil_div(n, kMaxBlocks));
     const int64_t nb = ceil_div(n, r);
     if (nb < 2) return 0;
@@ -159,10 +167,15 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
     if (bk.n == 0 || f == 0) return;
     const int32_t* bci = bk.bci.as<int32_t>();
     const float* bv = weights ? weights : bk.weighted ? bk.bv.as<float>() : nullptr;
-    // One launch per block over all 32-column tiles of f (grid.y), blocks
-    // in order: the first pass stores every row (zero where the block has no
+    // One launch per block over all column groups of f (grid.y), blocks in
+    // order: the first pass stores every row (zero where the block has no
     // entries), middle passes touch only rows with entries, the last pass
-    // adds and applies the epilogue to every row.
+    // adds and applies the epilogue to every row.  64-column groups only
+    // where a group has two tiles' worth of columns and lies in one weight
+    // plane.
+    const bool wide = bk.group_cols == 64 && f > 32 &&
+                      (epi.w_head_stride == 0 || epi.w_head_cols >= f || epi.w_head_cols % 64 == 0);
+    const int group_cols = wide ? 64 : 32;
     for (int64_t blk = 0; blk < bk.n_blocks; ++blk) {
         const bool first = blk == 0, last = blk + 1 == bk.n_blocks;
         AggEpilogue e;
@@ -177,7 +190,7 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         e.w_head_stride = epi.w_head_stride;
         e.w_head_cols = epi.w_head_cols;
         e.exact_exp = epi.exact_exp;
-        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, 32);
+        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, group_cols);
     }
 }
 

@@ -236,18 +236,21 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const bool exact = m.precision == TG_PRECISION_EXACT;
     const int64_t maxf = m.max_wide();
     const int64_t chunk = exact ? (int64_t(1) << 24) : 0;
-    // A + I: GCN's normalised values, or the structure alone for GAT
-    const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n);
+    // A + I: GCN's normalised values, or the structure alone for GAT (weighted
+    // passes: 64-column lane groups); A: SAGE's mean (32-column groups)
+    const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, 64);
     if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s, chunk);
+        m.blk_sl->group_cols = 64;
         if (exact && !m.blk_sl->in_order) m.blk_sl.reset();
     }
-    const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz);
+    const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz, 32);
     if (m.need_raw_mean() && r_raw > 0) {
         m.blk_raw = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s, chunk);
+        m.blk_raw->group_cols = 32;
         if (exact && !m.blk_raw->in_order) m.blk_raw.reset();
     }
 }

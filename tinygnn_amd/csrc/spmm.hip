@@ -453,13 +453,14 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int e = ch.z;
     // Gather address = the lane's base (B + its column offset) + col * row
     // pitch in bytes: one 32 x 32 -> 64-bit multiply-add per gather (col >= 0;
-    // the host keeps the pitch in bytes below 2^32).
+    // the host keeps the pitch in bytes below 2^32).  A tile-major B puts
+    // column c in tile c / 32 at offset c % 32 (a 64-column group spans two
+    // tiles).
     const char* bl[VPL];
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
         bl[v] = reinterpret_cast<const char*>(
-            epi.b_tile_stride > 0 ? B + static_cast<int64_t>(blockIdx.y) * epi.b_tile_stride +
-                                        (fl[v] - fbase)
+            epi.b_tile_stride > 0 ? B + (fl[v] >> 5) * epi.b_tile_stride + (fl[v] & 31)
                                   : B + fl[v]);
     const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
     int ncl[CPL];
@@ -632,8 +633,8 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
                    hipStream_t s, int tile_cols) {
     if (p.m == 0 || f == 0) return;
     const bool tiled_b = epi.b_tile_stride > 0;
-    require(!tiled_b || (tile_cols == 32 && ldb == 32),
-            "aggregate: a tile-major B needs 32-column tiles of pitch 32");
+    require(!tiled_b || ((tile_cols == 32 || tile_cols == 64) && ldb == 32),
+            "aggregate: a tile-major B needs 32- or 64-column groups and tiles of pitch 32");
     require((tiled_b || ldb >= f) && ldc >= f, "aggregate: leading dimension smaller than f");
     require(ldb < (int64_t(1) << 30), "aggregate: B's leading dimension must be < 2^30");
     require(epi.self == nullptr || (epi.self_tile_stride > 0 ? epi.ld_self == 32
@@ -649,13 +650,14 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
     const int vec = tiled_b ? pick_vec(32, {epi.b_tile_stride}, {B}) : pick_load_vec(f, ldb, B);
     AggEpilogue e = epi;
     e.vec_io = pick_vec(f, {ldc, epi.self ? epi.ld_self : vec}, {C, epi.self, epi.bias}) >= vec;
-    require(tile_cols == 0 || tile_cols == 32, "aggregate: tile_cols must be 0 or 32");
+    require(tile_cols == 0 || tile_cols == 32 || tile_cols == 64,
+            "aggregate: tile_cols must be 0, 32 or 64");
     LaneLayout L = choose_layout(f, vec);
-    if (tile_cols == 32) {
-        L.lpr = 32 / vec;
+    if (tile_cols > 0) {
+        L.lpr = tile_cols / vec;
         L.vpl = 1;
-        L.tile = 32;
-        L.n_tiles = static_cast<int>(ceil_div(f, 32));
+        L.tile = tile_cols;
+        L.n_tiles = static_cast<int>(ceil_div(f, tile_cols));
     }
     // weight planes per column group: every lane group's tile lies in one group
     require(epi.w_head_stride == 0 ||
