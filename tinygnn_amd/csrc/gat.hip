@@ -677,36 +677,50 @@ __global__ __launch_bounds__(256) void gat_exact_stats_kernel(const int4* __rest
 // The attention weights of the column-blocked passes, once per entry and
 // head: alpha_ij = exp(e_ij - max_i) * (1/sum_i) (layers.cpp:1076-1090;
 // exact: exp_rn), e_ij = LeakyReLU(src_i + dst_j), written to plane h at the
-// entry's blocked position (w[h * plane + position]).  One wave per (block,
-// row) segment of the blocked structure (measured faster than a 16-lane
-// group per segment and than one wave per row).
-template <int NH>
+// entry's blocked position (w[h * plane + position]).  One wave per SEGS
+// consecutive (block, row) segments of the blocked structure: their entries
+// are one contiguous range, walked 64 at a time; an entry's segment is the
+// number of the range's inner boundaries at or below it, and its row's
+// statistics come from L1.  (One wave per segment, 16-lane groups per
+// segment and one wave per row all measured slower: a segment holds about
+// 50 entries at config E, too few to hide a wave's dependent loads.)
+template <int NH, int SEGS>
 __global__ __launch_bounds__(256) void gat_weights_kernel(
     const int32_t* __restrict__ brp, const int32_t* __restrict__ bci, int64_t n, int64_t nseg,
     int heads, const float* __restrict__ src, const float* __restrict__ dst,
     const float* __restrict__ rmax, const float* __restrict__ rinv, float slope, int exact,
     float* __restrict__ w, int64_t plane) {
     const int lane = threadIdx.x & 63;
-    const int64_t seg = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (seg >= nseg) return;  // uniform per wave
-    const int b = brp[seg], e = brp[seg + 1];
-    if (b == e) return;
-    const int64_t row = seg % n;
-    for (int h0 = 0; h0 < heads; h0 += NH) {
-        float si[NH], mi[NH], ri[NH];
+    const int64_t s0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * SEGS;
+    if (s0 >= nseg) return;  // uniform per wave
+    const int ns = static_cast<int>(nseg - s0 < SEGS ? nseg - s0 : SEGS);
+    // the ns + 1 boundaries, one per lane, then wave-uniform
+    const int bl = lane <= ns ? brp[s0 + lane] : 0;
+    int bnd[SEGS + 1];
 #pragma unroll
-        for (int k = 0; k < NH; ++k) {
-            si[k] = src[row * heads + h0 + k];
-            mi[k] = rmax[row * heads + h0 + k];
-            ri[k] = rinv[row * heads + h0 + k];
-        }
+    for (int k = 0; k <= SEGS; ++k) bnd[k] = __shfl(bl, k <= ns ? k : ns);
+    const int b = bnd[0], e = bnd[ns];
+    if (b == e) return;
+    const int64_t row0 = s0 % n;
+    for (int h0 = 0; h0 < heads; h0 += NH) {
         for (int i = b + lane; i < e; i += 64) {
-            float d[NH];
+            int k = 0;
+#pragma unroll
+            for (int t = 1; t < SEGS; ++t) k += (t < ns && i >= bnd[t]) ? 1 : 0;
+            int64_t row = row0 + k;
+            while (row >= n) row -= n;  // the group ran into the next block(s)
+            float si[NH], mi[NH], ri[NH], d[NH];
+#pragma unroll
+            for (int q = 0; q < NH; ++q) {
+                si[q] = src[row * heads + h0 + q];
+                mi[q] = rmax[row * heads + h0 + q];
+                ri[q] = rinv[row * heads + h0 + q];
+            }
             gat_dst<NH>(dst, heads, h0, bci[i], d);
 #pragma unroll
-            for (int k = 0; k < NH; ++k) {
-                const float x = lrelu(si[k] + d[k], slope) - mi[k];
-                w[static_cast<int64_t>(h0 + k) * plane + i] = (exact ? exp_rn(x) : expf(x)) * ri[k];
+            for (int q = 0; q < NH; ++q) {
+                const float x = lrelu(si[q] + d[q], slope) - mi[q];
+                w[static_cast<int64_t>(h0 + q) * plane + i] = (exact ? exp_rn(x) : expf(x)) * ri[q];
             }
         }
     }
@@ -884,14 +898,15 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
         }
     }
     // the attention weights, once per entry and head, in blocked entry order
+    constexpr int kSegs = 8;  // (block, row) segments per wave
     const int64_t nseg = bk.n_blocks * n;
-    const unsigned wgrid = static_cast<unsigned>(ceil_div(nseg, 4));
+    const unsigned wgrid = static_cast<unsigned>(ceil_div(nseg, 4 * kSegs));
     if (vec4)
-        gat_weights_kernel<4><<<wgrid, 256, 0, s>>>(
+        gat_weights_kernel<4, kSegs><<<wgrid, 256, 0, s>>>(
             bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
             rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
     else
-        gat_weights_kernel<1><<<wgrid, 256, 0, s>>>(
+        gat_weights_kernel<1, kSegs><<<wgrid, 256, 0, s>>>(
             bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
             rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
     TG_LAUNCH_CHECK();
