@@ -512,9 +512,10 @@ __device__ __forceinline__ void gat_dst(const float* __restrict__ dst, int heads
     }
 }
 
-// One wave per plan chunk (at most `chunk` entries of one row), heads in
-// groups of NH (4: heads in fours with 16-byte aligned dst; else 1), one
-// sweep over the chunk: each lane takes four entries at a time, computes
+// One group of GL lanes per plan chunk (at most `chunk` entries of one
+// row; GL = 64: a wave, 16 or 32: several chunks per wave), heads in groups
+// of NH (4: heads in fours with 16-byte aligned dst; else 1), one sweep
+// over the chunk: each lane takes four entries at a time, computes
 // their scores e_ij = LeakyReLU(src_i + dst_j), raises its running max to
 // the batch's maximum (rescaling its running sum once per batch) and adds
 // exp(e - max) for the batch -- one L2 request per entry and head group,
@@ -524,7 +525,7 @@ __device__ __forceinline__ void gat_dst(const float* __restrict__ dst, int heads
 // reference's zero sum gives a zero row before the bias); a split row's
 // chunk writes its (max, sum) pair to its partial slot for
 // gat_stats_merge_kernel.
-template <int NH>
+template <int NH, int GL>
 __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__ chunks,
                                                         int64_t n_chunks,
                                                         const int32_t* __restrict__ ci,
@@ -534,9 +535,9 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
                                                         float slope, float* __restrict__ rmax,
                                                         float* __restrict__ rinv,
                                                         float* __restrict__ pstats) {
-    const int lane = threadIdx.x & 63;
-    const int64_t cid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (cid >= n_chunks) return;  // uniform per wave
+    const int lane = threadIdx.x % GL;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * (256 / GL) + threadIdx.x / GL;
+    if (cid >= n_chunks) return;  // uniform per group
     const int4 ch = chunks[cid];
     const int64_t row = ch.x;
     constexpr int UN = 4;
@@ -548,12 +549,12 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
             m[k] = -INFINITY;
             sm[k] = 0.0f;
         }
-        for (int i0 = ch.y; i0 < ch.z; i0 += 64 * UN) {
+        for (int i0 = ch.y; i0 < ch.z; i0 += GL * UN) {
             float x[UN][NH];
             bool ok[UN];
 #pragma unroll
             for (int u = 0; u < UN; ++u) {
-                const int i = i0 + u * 64 + lane;
+                const int i = i0 + u * GL + lane;
                 ok[u] = i < ch.z;
                 gat_dst<NH>(dst, heads, h0, ok[u] ? ci[i] : 0, x[u]);
             }
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
             }
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
+        for (int off = GL / 2; off >= 1; off >>= 1) {
 #pragma unroll
             for (int k = 0; k < NH; ++k)
                 softmax_merge(m[k], sm[k], __shfl_xor(m[k], off), __shfl_xor(sm[k], off));
@@ -880,14 +881,18 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
         Carver cw(work, work_bytes);
         float* pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
         if (p.n_chunks > 0) {
+            // two chunks per wave (config-E GAT forward: 64 lanes per chunk
+            // 14.24 ms, 32 lanes 14.14 ms, 16 lanes 14.17 ms)
+            constexpr int kGL = 32;
+            const unsigned sgrid = static_cast<unsigned>(ceil_div(p.n_chunks, 256 / kGL));
             if (vec4)
-                gat_stats_kernel<4><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
-                                                         static_cast<int>(heads), src, dst, slope,
-                                                         rmax, rinv, pstats);
+                gat_stats_kernel<4, kGL><<<sgrid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                              static_cast<int>(heads), src, dst,
+                                                              slope, rmax, rinv, pstats);
             else
-                gat_stats_kernel<1><<<grid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
-                                                         static_cast<int>(heads), src, dst, slope,
-                                                         rmax, rinv, pstats);
+                gat_stats_kernel<1, kGL><<<sgrid, 256, 0, s>>>(p.chunks.as<int4>(), p.n_chunks, ci,
+                                                              static_cast<int>(heads), src, dst,
+                                                              slope, rmax, rinv, pstats);
             TG_LAUNCH_CHECK();
         }
         if (p.n_split > 0) {
