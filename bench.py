@@ -49,6 +49,36 @@ DEFAULT_SEED = 2101
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "spmm_configD_pmc.md")
 
 
+def measure_copy(torch, reps: int = 10):
+    """Achievable HBM bandwidth of a plain stream on this box, beside the
+    8 TB/s peak: a 1 GiB device-to-device copy (1 GiB read + 1 GiB written),
+    HIP events on the current stream, median of `reps` copies after 3
+    warm-ups."""
+    x = torch.ones(1 << 28, device="cuda:0")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        y.copy_(x)
+        e1.record()
+        ts.append((e0, e1))
+    torch.cuda.synchronize()
+    ms = float(np.median([a.elapsed_time(b) for a, b in ts]))
+    nbytes = 2 * x.numel() * 4
+    del x, y
+    torch.cuda.empty_cache()
+    print(f"[bench] device copy of 1 GiB: {ms:.3f} ms, {nbytes / ms / 1e6:.0f} GB/s",
+          file=sys.stderr)
+    return {"gbs": round(nbytes / ms / 1e6, 1), "ms": round(ms, 4), "bytes": nbytes,
+            "kernel": "torch copy_ of 1 GiB (read + write)",
+            "note": "a read + write stream; the SpMM pass reads almost only, and part of its "
+                    "B gathers hit the MALL / L2, so its algorithmic rate can exceed this"}
+
+
 def measured_traffic(f: int, seed: int):
     """HBM bytes per SpMM launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (copy-kernel calibrated), for the default workload
@@ -494,6 +524,7 @@ def main():
 
     r = None if args.no_spmm else run_spmm_d(args, torch, tg)
     torch.cuda.empty_cache()
+    copy = measure_copy(torch)
     if args.calib_copy:
         xc = torch.ones(1 << 28, device="cuda:0")  # 1 GiB read, 1 GiB written
         yc = torch.empty_like(xc)
@@ -528,6 +559,8 @@ def main():
                                f"(power-law 2.1, max deg {r['max_deg']}), F={args.f}",
                    "m": r["m"], "nnz": r["nnz"], "f": args.f},
         "pct_hbm_peak": round(100.0 * head["gbs"] / HBM_PEAK_GBS, 2),
+        # achievable bandwidth of a plain copy on this box, beside the peak
+        "hbm_copy": copy,
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
