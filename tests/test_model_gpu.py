@@ -251,6 +251,39 @@ def test_blocked_aggregation(gpu, restate, case):
     assert (bits(outs[rows_per_block]) != bits(outs[0])).any(), "blocking had no effect"
 
 
+@pytest.mark.parametrize("precision", ["fast", "exact"])
+def test_blocked_gat_tiny_graph(gpu, restate, precision):
+    """Blocking forced on a 5-node graph (one or two source nodes per block):
+    a wavefront of the attention-weight kernel walks more consecutive
+    (block, row) segments than there are rows, wrapping across several
+    blocks.  Fast: within tolerance of the oracle and of the unblocked path;
+    exact: bit-identical to the unblocked exact forward."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(51)
+    n = 5
+    src = np.array([0, 0, 1, 2, 2, 3, 4, 4, 4, 1], np.int32)
+    dst = np.array([1, 3, 2, 0, 4, 3, 0, 1, 2, 1], np.int32)
+    a = restate.edge_list_to_csr(src, dst, n)
+    spec = synth.spec_gat(6, 64, 2, 3)
+    w = synth.model_weights(spec, seed=9)
+    x = rng.standard_normal((n, 6)).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = {}
+    for blocking in (0, 1, 2):
+        m = tg.Model.from_spec(spec, w)
+        if precision == "exact":
+            m.set_precision(tg.PRECISION_EXACT)
+        m.set_blocking(blocking)
+        outs[blocking] = m.forward(da, _t(gpu, x)).cpu().numpy()
+        assert_close(outs[blocking], want, what=f"{precision} blocking={blocking}")
+    for blocking in (1, 2):
+        if precision == "exact":
+            np.testing.assert_array_equal(bits(outs[blocking]), bits(outs[0]))
+        else:
+            assert_close(outs[blocking], outs[0], what=f"blocking={blocking} vs unblocked")
+
+
 def test_blocked_gat_fallback(gpu, restate):
     """GAT layers whose heads are not whole 32-column tiles, or whose heads
     are averaged, keep the unblocked kernel under blocking (bit-identical to
