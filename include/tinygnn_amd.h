@@ -293,7 +293,7 @@ int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);
 enum { TG_PRECISION_FAST = 0, TG_PRECISION_EXACT = 1 };
 int tg_model_set_precision(tg_model_t model, int precision);
 /* Column blocking of the model's GCN, SAGE-mean and GAT aggregations
- * (TG_FORWARD_CACHED calls; GAT layers with concatenated or single heads of
+ * (both forward modes; GAT layers with concatenated or single heads of
  * whole 32-column tiles; in exact precision only for adjacencies whose rows
  * are in column order, where the blocked sums keep the reference's order
  * bit for bit; no counterpart in the reference, which has one CPU loop per

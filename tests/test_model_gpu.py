@@ -330,10 +330,10 @@ def test_blocking_setting(gpu):
 
 
 def test_blocking_across_modes(gpu):
-    """Reference-mode forwards never block; a cached forward after one adds
-    the blocked copy to the reused state, and a later reference-mode call
-    drops it again: each result equals a fresh model's in that mode, bit for
-    bit."""
+    """Both forward modes block.  With one setting, reference-mode forwards
+    (preprocessing, plans and the blocked copy rebuilt in place on every
+    call) and cached ones give the same bits, call after call and in any
+    order; a new setting takes effect on the next call in either mode."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(21)
     n = 2000
@@ -351,16 +351,18 @@ def test_blocking_across_modes(gpu):
 
     unblocked, blocked = fresh(0, tg.FORWARD_CACHED), fresh(100, tg.FORWARD_CACHED)
     assert (unblocked != blocked).any()
+    np.testing.assert_array_equal(fresh(100, tg.FORWARD_REFERENCE), blocked)
+    np.testing.assert_array_equal(fresh(0, tg.FORWARD_REFERENCE), unblocked)
     m = tg.Model.from_spec(spec, w)
     m.set_blocking(100)
-    seq = [(tg.FORWARD_REFERENCE, unblocked), (tg.FORWARD_CACHED, blocked),
-           (tg.FORWARD_CACHED, blocked), (tg.FORWARD_REFERENCE, unblocked),
-           (tg.FORWARD_CACHED, blocked)]
-    for i, (mode, want) in enumerate(seq):
+    ref, cached = tg.FORWARD_REFERENCE, tg.FORWARD_CACHED
+    seq = [(ref, 100, blocked), (cached, 100, blocked), (ref, 100, blocked), (ref, 100, blocked),
+           (cached, 100, blocked), (cached, 0, unblocked), (ref, 0, unblocked),
+           (ref, 100, blocked), (cached, 100, blocked)]
+    for i, (mode, blocking, want) in enumerate(seq):
+        m.set_blocking(blocking)
         got = bits(m.forward(da, x, mode=mode).cpu().numpy())
-        np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode}")
-    m.set_blocking(0)  # a new setting rebuilds the blocked state on the next cached call
-    np.testing.assert_array_equal(bits(m.forward(da, x).cpu().numpy()), unblocked)
+        np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode} blocking {blocking}")
 
 
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),

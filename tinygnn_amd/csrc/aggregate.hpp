@@ -86,11 +86,13 @@ struct BlockedCSR {
     DeviceBuffer brp;  // int32 [n_blocks * n + 1]
     DeviceBuffer bci;  // int32 [nnz]
     DeviceBuffer bv;   // float [nnz] (weighted structures)
+    DeviceBuffer scratch;  // the build's temporaries
     std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
 };
 
 // Blocks with at most 64 column blocks; v may be null (structure only);
-// chunk: the per-block plans' chunk size (0 = default).
+// chunk: the per-block plans' chunk size (0 = default).  Rebuilding into the
+// same object reuses its buffers and plans (they only grow).
 void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
                    hipStream_t s, int64_t chunk = 0);

@@ -120,17 +120,16 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     bk.n_blocks = nb;
     bk.rp = rp;
     bk.weighted = v != nullptr;
-    bk.brp.resize(static_cast<size_t>(nb * n + 1) * sizeof(int32_t));
-    bk.bci.resize(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(int32_t));
-    if (v) bk.bv.resize(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
-    else bk.bv.resize(0);
+    bk.brp.reserve(static_cast<size_t>(nb * n + 1) * sizeof(int32_t));
+    bk.bci.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(int32_t));
+    if (v) bk.bv.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
 
     Carver cv(nullptr, 0);
     cv.take<int32_t>(nb * n);
     cv.take<int64_t>(scan_temp_elems(nb * n));
     cv.take<int32_t>(1);
-    DeviceBuffer tmp(cv.bytes());
-    Carver c(tmp.get(), tmp.size());
+    bk.scratch.reserve(cv.bytes());
+    Carver c(bk.scratch.get(), bk.scratch.size());
     int32_t* cnt = c.take<int32_t>(nb * n);
     int64_t* scan_tmp = c.take<int64_t>(scan_temp_elems(nb * n));
     int32_t* disorder = c.take<int32_t>(1);
@@ -149,13 +148,12 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     TG_LAUNCH_CHECK();
     int32_t h_disorder = 1;
     TG_HIP(hipMemcpyAsync(&h_disorder, disorder, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-    bk.plans.clear();
+    bk.plans.resize(static_cast<size_t>(nb));
     for (int64_t b = 0; b < nb; ++b) {
-        auto p = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*p, n, nnz, brp + b * n, max_f, chunk, s);  // synchronises s
-        bk.plans.push_back(std::move(p));
+        if (!bk.plans[b]) bk.plans[b] = std::make_unique<tg_spmm_plan_s>();
+        build_plan(*bk.plans[b], n, nnz, brp + b * n, max_f, chunk, s);  // synchronises s
     }
-    TG_HIP(hipStreamSynchronize(s));  // h_disorder, and tmp's last readers
+    TG_HIP(hipStreamSynchronize(s));  // h_disorder
     bk.in_order = h_disorder == 0;
 }
 

@@ -162,8 +162,8 @@ void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* 
     cv.take<int32_t>(kPlanBins);
     cv.take<int64_t>(4);
     cv.take<int64_t>(scan_temp_elems(m));
-    DeviceBuffer tmp(cv.bytes());
-    Carver c(tmp.get(), tmp.size());
+    p.scratch.reserve(cv.bytes());
+    Carver c(p.scratch.get(), p.scratch.size());
     int32_t* split_cnt = c.take<int32_t>(m);
     int32_t* is_split = c.take<int32_t>(m);
     int32_t* slot_base = c.take<int32_t>(m + 1);
@@ -189,18 +189,16 @@ void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* 
     p.n_split = host_tot[1];
     p.n_partials = host_tot[2];
 
-    p.chunks.resize(static_cast<size_t>(p.n_chunks) * sizeof(int4));
-    p.split.resize(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
+    p.chunks.reserve(static_cast<size_t>(std::max<int64_t>(p.n_chunks, 1)) * sizeof(int4));
+    p.split.reserve(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
     // partial rows are padded to a multiple of 4 floats (128-bit access)
     if (p.n_partials > 0 && max_f > 0)
-        p.partials.resize(static_cast<size_t>(p.n_partials) *
-                          static_cast<size_t>(round_up(max_f, 4)) * sizeof(float));
+        p.partials.reserve(static_cast<size_t>(p.n_partials) *
+                           static_cast<size_t>(round_up(max_f, 4)) * sizeof(float));
     plan_scatter_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), slot_base,
                                              split_pos, bin_cursor, p.chunks.as<int4>(),
                                              p.split.as<int4>());
     TG_LAUNCH_CHECK();
-    // `tmp` is released at scope exit; make sure the scatter has consumed it.
-    TG_HIP(hipStreamSynchronize(s));
 }
 
 LaneLayout choose_layout(int64_t f, int vec) {

@@ -29,6 +29,7 @@ struct tg_spmm_plan_s {
     tg::DeviceBuffer chunks;            // int4 {row, begin, end, slot (-1 = direct)}
     tg::DeviceBuffer split;             // int4 {row, first slot, n chunks, degree}
     tg::DeviceBuffer partials;          // float [n_partials x max_f]
+    tg::DeviceBuffer scratch;           // the build's temporaries (kept for rebuilds)
 };
 
 namespace tg {
@@ -36,7 +37,9 @@ namespace tg {
 constexpr int kPlanBins = 64;
 constexpr int64_t kDefaultChunk = 1024;
 
-// Builds the plan (allocates, synchronises `s` once).
+// Builds the plan (synchronises `s` once, for the chunk count).  Buffers only
+// grow: rebuilding a plan object for a structure of the same size allocates
+// nothing.
 void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
                 int64_t max_f, int64_t chunk, hipStream_t s);
 
