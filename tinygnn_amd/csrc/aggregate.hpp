@@ -87,6 +87,7 @@ struct BlockedCSR {
     DeviceBuffer bci;  // int32 [nnz]
     DeviceBuffer bv;   // float [nnz] (weighted structures)
     DeviceBuffer scratch;  // the build's temporaries
+    PinnedBuffer host;     // the build's device-to-host results (plan totals, disorder)
     std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
 };
 

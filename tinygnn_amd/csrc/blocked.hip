@@ -146,15 +146,19 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                                                   static_cast<int>(nb), brp, bk.bci.as<int32_t>(),
                                                   v ? bk.bv.as<float>() : nullptr, nullptr);
     TG_LAUNCH_CHECK();
-    int32_t h_disorder = 1;
-    TG_HIP(hipMemcpyAsync(&h_disorder, disorder, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    // one plan per block, all counted before one synchronisation, then
+    // scattered; the disorder flag comes back with the plans' totals
+    bk.host.reserve(static_cast<size_t>(4 * nb + 1) * sizeof(int64_t));
+    int64_t* host = bk.host.as<int64_t>();
+    TG_HIP(hipMemcpyAsync(host + 4 * nb, disorder, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     bk.plans.resize(static_cast<size_t>(nb));
     for (int64_t b = 0; b < nb; ++b) {
         if (!bk.plans[b]) bk.plans[b] = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*bk.plans[b], n, nnz, brp + b * n, max_f, chunk, s);  // synchronises s
+        build_plan_count(*bk.plans[b], n, nnz, brp + b * n, max_f, chunk, s, host + 4 * b);
     }
-    TG_HIP(hipStreamSynchronize(s));  // h_disorder
-    bk.in_order = h_disorder == 0;
+    TG_HIP(hipStreamSynchronize(s));
+    for (int64_t b = 0; b < nb; ++b) build_plan_finish(*bk.plans[b], host + 4 * b, s);
+    bk.in_order = *reinterpret_cast<const int32_t*>(host + 4 * nb) == 0;
 }
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,

@@ -40,6 +40,25 @@ void DeviceBuffer::reset() {
     n_ = 0;
 }
 
+void PinnedBuffer::reserve(size_t bytes) {
+    if (bytes <= n_) return;
+    reset();
+    hipError_t e = hipHostMalloc(&p_, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        p_ = nullptr;
+        (void)hipGetLastError();
+        throw AllocError("hipHostMalloc of " + std::to_string(bytes) + " bytes failed: " +
+                         hipGetErrorString(e));
+    }
+    n_ = bytes;
+}
+
+void PinnedBuffer::reset() {
+    if (p_) (void)hipHostFree(p_);
+    p_ = nullptr;
+    n_ = 0;
+}
+
 // ---------------------------------------------------------------------------
 // Exclusive scan of int32 counts (tiles of 1024 = 256 threads x 4 items).
 // ---------------------------------------------------------------------------

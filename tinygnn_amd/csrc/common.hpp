@@ -123,6 +123,24 @@ private:
     size_t n_ = 0;
 };
 
+// RAII pinned host allocation (hipHostMalloc): small device-to-host results
+// that the host reads after a stream synchronisation, so that the copies
+// themselves stay asynchronous.
+class PinnedBuffer {
+public:
+    PinnedBuffer() = default;
+    ~PinnedBuffer() { reset(); }
+    PinnedBuffer(const PinnedBuffer&) = delete;
+    PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+    void reserve(size_t bytes);
+    void reset();
+    template <typename T> T* as() const { return static_cast<T*>(p_); }
+
+private:
+    void* p_ = nullptr;
+    size_t n_ = 0;
+};
+
 // Small fill kernels (used instead of hipMemset*Async so that library calls
 // can be captured into HIP graphs).
 void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s);

@@ -307,8 +307,8 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     m.key_nnz = nnz;
     // column blocking in both modes: with the reference's per-call
     // preprocessing (config E) GCN / SAGE / GAT took 22.4 / 21.5 / 23.4 ms
-    // unblocked and 15.3 / 12.2 / 17.7 ms blocked with everything rebuilt in
-    // place
+    // unblocked and 14.8 / 12.0 / 17.3 ms blocked with everything rebuilt in
+    // place (the block plans counted before one synchronisation)
     prepare_blocked(m, n, nnz, rp, ci, s);
 }
 

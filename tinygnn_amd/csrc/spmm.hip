@@ -132,8 +132,44 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
 
 }  // namespace
 
-void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
-                int64_t max_f, int64_t chunk, hipStream_t s) {
+namespace {
+
+// The plan build's temporaries, carved from the plan's scratch in the same
+// layout by both phases: split_cnt[m], is_split[m], slot_base[m+1],
+// split_pos[m+1], bin_count[64], bin_cursor[64], totals[4], scan temp.
+struct PlanTemps {
+    int32_t *split_cnt, *is_split, *slot_base, *split_pos, *bin_count, *bin_cursor;
+    int64_t *totals, *scan_tmp;
+};
+
+PlanTemps carve_plan_temps(tg_spmm_plan_s& p, int64_t m) {
+    Carver cv(nullptr, 0);
+    cv.take<int32_t>(m);
+    cv.take<int32_t>(m);
+    cv.take<int32_t>(m + 1);
+    cv.take<int32_t>(m + 1);
+    cv.take<int32_t>(kPlanBins);
+    cv.take<int32_t>(kPlanBins);
+    cv.take<int64_t>(4);
+    cv.take<int64_t>(scan_temp_elems(m));
+    p.scratch.reserve(cv.bytes());
+    Carver c(p.scratch.get(), p.scratch.size());
+    PlanTemps t;
+    t.split_cnt = c.take<int32_t>(m);
+    t.is_split = c.take<int32_t>(m);
+    t.slot_base = c.take<int32_t>(m + 1);
+    t.split_pos = c.take<int32_t>(m + 1);
+    t.bin_count = c.take<int32_t>(kPlanBins);
+    t.bin_cursor = c.take<int32_t>(kPlanBins);
+    t.totals = c.take<int64_t>(4);
+    t.scan_tmp = c.take<int64_t>(scan_temp_elems(m));
+    return t;
+}
+
+}  // namespace
+
+void build_plan_count(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                      int64_t max_f, int64_t chunk, hipStream_t s, int64_t* host_totals) {
     require(m >= 0, "spmm plan: m must be >= 0");
     require(m < (int64_t(1) << 31), "spmm plan: m must be < 2^31");
     require(nnz_bound >= 0 && nnz_bound < (int64_t(1) << 31),
@@ -148,57 +184,49 @@ void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* 
     p.chunk = chunk;
     p.row_ptr = row_ptr;
     p.n_chunks = p.n_split = p.n_partials = 0;
+    host_totals[0] = host_totals[1] = host_totals[2] = 0;
     if (m == 0) return;
     require(row_ptr != nullptr, "spmm plan: row_ptr is null");
-
-    // temporaries: split_cnt[m], is_split[m], slot_base[m+1], split_pos[m+1],
-    // bin_count[64], bin_cursor[64], totals[3], scan temp
-    Carver cv(nullptr, 0);
-    cv.take<int32_t>(m);
-    cv.take<int32_t>(m);
-    cv.take<int32_t>(m + 1);
-    cv.take<int32_t>(m + 1);
-    cv.take<int32_t>(kPlanBins);
-    cv.take<int32_t>(kPlanBins);
-    cv.take<int64_t>(4);
-    cv.take<int64_t>(scan_temp_elems(m));
-    p.scratch.reserve(cv.bytes());
-    Carver c(p.scratch.get(), p.scratch.size());
-    int32_t* split_cnt = c.take<int32_t>(m);
-    int32_t* is_split = c.take<int32_t>(m);
-    int32_t* slot_base = c.take<int32_t>(m + 1);
-    int32_t* split_pos = c.take<int32_t>(m + 1);
-    int32_t* bin_count = c.take<int32_t>(kPlanBins);
-    int32_t* bin_cursor = c.take<int32_t>(kPlanBins);
-    int64_t* totals = c.take<int64_t>(4);
-    int64_t* scan_tmp = c.take<int64_t>(scan_temp_elems(m));
-
-    fill_i32(bin_count, kPlanBins, 0, s);
+    const PlanTemps t = carve_plan_temps(p, m);
+    fill_i32(t.bin_count, kPlanBins, 0, s);
     const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
-    plan_count_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), split_cnt,
-                                           is_split, bin_count);
+    plan_count_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), t.split_cnt,
+                                           t.is_split, t.bin_count);
     TG_LAUNCH_CHECK();
-    exclusive_scan_i32(split_cnt, slot_base, m, scan_tmp, s);
-    exclusive_scan_i32(is_split, split_pos, m, scan_tmp, s);
-    plan_bins_kernel<<<1, 64, 0, s>>>(bin_count, bin_cursor, slot_base, split_pos, m, totals);
+    exclusive_scan_i32(t.split_cnt, t.slot_base, m, t.scan_tmp, s);
+    exclusive_scan_i32(t.is_split, t.split_pos, m, t.scan_tmp, s);
+    plan_bins_kernel<<<1, 64, 0, s>>>(t.bin_count, t.bin_cursor, t.slot_base, t.split_pos, m,
+                                      t.totals);
     TG_LAUNCH_CHECK();
-    int64_t host_tot[3];
-    TG_HIP(hipMemcpyAsync(host_tot, totals, sizeof(host_tot), hipMemcpyDeviceToHost, s));
-    TG_HIP(hipStreamSynchronize(s));
-    p.n_chunks = host_tot[0];
-    p.n_split = host_tot[1];
-    p.n_partials = host_tot[2];
+    TG_HIP(hipMemcpyAsync(host_totals, t.totals, 3 * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+}
 
+void build_plan_finish(tg_spmm_plan_s& p, const int64_t* host_totals, hipStream_t s) {
+    p.n_chunks = host_totals[0];
+    p.n_split = host_totals[1];
+    p.n_partials = host_totals[2];
+    if (p.m == 0) return;
+    const PlanTemps t = carve_plan_temps(p, p.m);
     p.chunks.reserve(static_cast<size_t>(std::max<int64_t>(p.n_chunks, 1)) * sizeof(int4));
     p.split.reserve(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
     // partial rows are padded to a multiple of 4 floats (128-bit access)
-    if (p.n_partials > 0 && max_f > 0)
+    if (p.n_partials > 0 && p.max_f > 0)
         p.partials.reserve(static_cast<size_t>(p.n_partials) *
-                           static_cast<size_t>(round_up(max_f, 4)) * sizeof(float));
-    plan_scatter_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), slot_base,
-                                             split_pos, bin_cursor, p.chunks.as<int4>(),
-                                             p.split.as<int4>());
+                           static_cast<size_t>(round_up(p.max_f, 4)) * sizeof(float));
+    const unsigned nblk = static_cast<unsigned>(ceil_div(p.m, 256));
+    plan_scatter_kernel<<<nblk, 256, 0, s>>>(p.row_ptr, p.m, static_cast<int>(p.chunk),
+                                             t.slot_base, t.split_pos, t.bin_cursor,
+                                             p.chunks.as<int4>(), p.split.as<int4>());
     TG_LAUNCH_CHECK();
+}
+
+void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                int64_t max_f, int64_t chunk, hipStream_t s) {
+    p.host_totals.reserve(4 * sizeof(int64_t));
+    int64_t* tot = p.host_totals.as<int64_t>();
+    build_plan_count(p, m, nnz_bound, row_ptr, max_f, chunk, s, tot);
+    if (m > 0) TG_HIP(hipStreamSynchronize(s));
+    build_plan_finish(p, tot, s);
 }
 
 LaneLayout choose_layout(int64_t f, int vec) {

@@ -30,6 +30,7 @@ struct tg_spmm_plan_s {
     tg::DeviceBuffer split;             // int4 {row, first slot, n chunks, degree}
     tg::DeviceBuffer partials;          // float [n_partials x max_f]
     tg::DeviceBuffer scratch;           // the build's temporaries (kept for rebuilds)
+    tg::PinnedBuffer host_totals;       // the count phase's totals, read by the host
 };
 
 namespace tg {
@@ -42,6 +43,15 @@ constexpr int64_t kDefaultChunk = 1024;
 // nothing.
 void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
                 int64_t max_f, int64_t chunk, hipStream_t s);
+
+// The same build in two phases, so that several plans share one
+// synchronisation: build_plan_count enqueues the counting and the copy of
+// the three totals to host_totals (pinned host memory, 3 int64); once `s`
+// has synchronised, build_plan_finish sizes the plan and enqueues the
+// scatter.
+void build_plan_count(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
+                      int64_t max_f, int64_t chunk, hipStream_t s, int64_t* host_totals);
+void build_plan_finish(tg_spmm_plan_s& p, const int64_t* host_totals, hipStream_t s);
 
 // Lane layout for an aggregation of width f: each lane owns VPL (= 1)
 // vectors of VEC consecutive floats, LPR lanes own one row's feature tile,
