@@ -47,18 +47,30 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
 }
 
-// One wave per row.  The row is walked in 64-entry batches in order; for
+// c / d for 0 <= c < 2^31 and 0 < d < 2^31, d fixed per launch: through the
+// double reciprocal (exact to one unit for these ranges) and one correction
+// each way, in place of a 32-bit integer division sequence.
+__device__ __forceinline__ int div_by(int c, int d, double inv_d) {
+    int q = static_cast<int>(static_cast<double>(c) * inv_d);
+    q -= (static_cast<int64_t>(q) * d > c) ? 1 : 0;
+    q += (static_cast<int64_t>(q + 1) * d <= c) ? 1 : 0;
+    return q;
+}
+
+// One wave per row.  The row is walked in 64-entry batches in order (the
+// next batch's entries are loaded while the current one is placed); for
 // each block b the wave ballots the entries of the batch that fall in b, so
 // an entry's rank among the row's entries of its block is the count of
 // earlier batches plus the ballot bits below its lane (a stable partition).
 // Lane b keeps block b's running count (COUNT: written to cnt[b*n + row]) or
 // running output position (SCATTER: starting at brp[b*n + row]).
 // COUNT also flags (*disorder = 1) a row whose entries step back to an
-// earlier block.
+// earlier block (the previous entry's block comes from the lane below, or
+// from the previous batch's last lane).
 template <bool SCATTER>
 __global__ __launch_bounds__(256) void block_split_kernel(
     const int32_t* __restrict__ rp, const int32_t* __restrict__ ci,
-    const float* __restrict__ v, int64_t n, int rows_per_block, int nb,
+    const float* __restrict__ v, int64_t n, int rows_per_block, double inv_rows, int nb,
     int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv,
     int32_t* __restrict__ disorder) {
     const int lane = threadIdx.x & 63;
@@ -67,14 +79,27 @@ __global__ __launch_bounds__(256) void block_split_kernel(
     const int s = rp[row], e = rp[row + 1];
     int run = 0;
     if (SCATTER && lane < nb) run = cnt_or_brp[static_cast<int64_t>(lane) * n + row];
+    int cn = s + lane < e ? ci[s + lane] : 0;
+    float vn = 0.0f;
+    if (SCATTER && bv) vn = s + lane < e ? v[s + lane] : 0.0f;
+    int prev_last = -1;  // the block of the previous batch's last entry
     for (int i = s; i < e; i += 64) {
         const int idx = i + lane;
         const bool valid = idx < e;
-        const int c = valid ? ci[idx] : 0;
-        const int blk = valid ? c / rows_per_block : -1;
+        const int c = cn;
+        const float val = vn;
+        if (i + 64 < e) {  // uniform: prefetch the next batch
+            const int nidx = idx + 64;
+            cn = nidx < e ? ci[nidx] : 0;
+            if (SCATTER && bv) vn = nidx < e ? v[nidx] : 0.0f;
+        }
+        const int blk = valid ? div_by(c, rows_per_block, inv_rows) : -1;
         if (!SCATTER) {
-            const bool back = valid && idx > s && ci[idx - 1] / rows_per_block > blk;
+            const int below = __shfl_up(blk, 1);
+            const int pb = lane == 0 ? prev_last : below;
+            const bool back = valid && pb > blk;
             if (__ballot(back) != 0 && lane == 0) atomicOr(disorder, 1);
+            prev_last = __shfl(blk, 63);  // a full batch continues; the last one ends the row
         }
         int pos = 0;
         for (int b = 0; b < nb; ++b) {
@@ -86,7 +111,7 @@ __global__ __launch_bounds__(256) void block_split_kernel(
         }
         if (SCATTER && valid) {
             bci[pos] = c;
-            if (bv) bv[pos] = v[idx];
+            if (bv) bv[pos] = val;
         }
     }
     if (!SCATTER && lane < nb) cnt_or_brp[static_cast<int64_t>(lane) * n + row] = run;
@@ -136,14 +161,16 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
 
     fill_i32(disorder, 1, 0, s);
     const unsigned grid = static_cast<unsigned>(ceil_div(n, 4));
+    const double inv_rows = 1.0 / static_cast<double>(rows_per_block);
     block_split_kernel<false><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
-                                                   static_cast<int>(nb), cnt, nullptr, nullptr,
-                                                   disorder);
+                                                   inv_rows, static_cast<int>(nb), cnt, nullptr,
+                                                   nullptr, disorder);
     TG_LAUNCH_CHECK();
     int32_t* brp = bk.brp.as<int32_t>();
     exclusive_scan_i32(cnt, brp, nb * n, scan_tmp, s);
     block_split_kernel<true><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
-                                                  static_cast<int>(nb), brp, bk.bci.as<int32_t>(),
+                                                  inv_rows, static_cast<int>(nb), brp,
+                                                  bk.bci.as<int32_t>(),
                                                   v ? bk.bv.as<float>() : nullptr, nullptr);
     TG_LAUNCH_CHECK();
     // one plan per block, all counted before one synchronisation, then

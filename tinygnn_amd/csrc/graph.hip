@@ -487,9 +487,109 @@ __device__ __forceinline__ void copy_span(const int32_t* __restrict__ col_ind,
     }
 }
 
+// 16-byte vectors: the aligned output granules of the copy, and its input
+// reads, which start wherever the output granule's first input falls (dword
+// aligned only).
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4_dw __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f32x4_dw __attribute__((ext_vector_type(4), aligned(4)));
+
+// Row i of A + I written in output order: output entry t (0 <= t < len,
+// len = row length + 1 when the diagonal is inserted at `ins` >= 0) is the
+// diagonal when t == ins, else input entry b + t - (ins >= 0 && t > ins).
+// Lanes take 16-byte aligned granules of 4 output entries (col_out and
+// val_out 16-byte aligned), kCopyUnroll per step.  A granule inside the row
+// and clear of the inserted diagonal reads its 4 inputs as one vector per
+// array and stores one aligned vector per array; the row's first and last
+// granules (shared with the neighbouring rows) and the diagonal's go entry
+// by entry.  Values: x = v (+1 on the diagonal), with NORM (x * dis_i) *
+// dis[col]; the inserted diagonal is x = 1.
+template <bool NORM, int LANES>
+__device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ col_ind,
+                                                  const float* __restrict__ val, int b, int e,
+                                                  int lane, int32_t i, int ins, int ob,
+                                                  float dis_i, const float* __restrict__ dis,
+                                                  int32_t* __restrict__ col_out,
+                                                  float* __restrict__ val_out) {
+    const int len = (e - b) + (ins >= 0 ? 1 : 0);
+    const int end = ob + len;
+    constexpr int kStep = LANES * 4;
+    for (int o0 = (ob & ~3) + lane * 4; o0 < end; o0 += kStep * kCopyUnroll) {
+        i32x4 c[kCopyUnroll];
+        f32x4 v[kCopyUnroll];
+        f32x4 dj[kCopyUnroll];
+        bool fast[kCopyUnroll];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+            const int o = o0 + u * kStep;
+            const int t = o - ob;
+            fast[u] = o < end && t >= 0 && t + 4 <= len && !(ins >= t && ins < t + 4);
+            if (fast[u]) {
+                const int s0 = b + t - ((ins >= 0 && t > ins) ? 1 : 0);
+                c[u] = *reinterpret_cast<const i32x4_dw*>(col_ind + s0);
+                v[u] = *reinterpret_cast<const f32x4_dw*>(val + s0);
+            } else if (o < end) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int tk = t + k;
+                    // entries outside the row (not stored) and the inserted
+                    // diagonal read as (i, 0): x = 0 + 1 on the diagonal
+                    int32_t ck = i;
+                    float vk = 0.0f;
+                    if (tk >= 0 && tk < len && tk != ins) {
+                        const int src = b + tk - ((ins >= 0 && tk > ins) ? 1 : 0);
+                        ck = col_ind[src];
+                        vk = val[src];
+                    }
+                    c[u][k] = ck;
+                    v[u][k] = vk;
+                }
+            }
+        }
+        if constexpr (NORM) {
+#pragma unroll
+            for (int u = 0; u < kCopyUnroll; ++u) {
+                if (o0 + u * kStep < end) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) dj[u][k] = dis[c[u][k]];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+            const int o = o0 + u * kStep;
+            if (o >= end) continue;
+            f32x4 x;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float xk = v[u][k];
+                if (c[u][k] == i) xk = xk + 1.0f;
+                if constexpr (NORM) xk = (xk * dis_i) * dj[u][k];
+                x[k] = xk;
+            }
+            if (fast[u]) {
+                *reinterpret_cast<i32x4*>(col_out + o) = c[u];
+                *reinterpret_cast<f32x4*>(val_out + o) = x;
+            } else {
+                const int t = o - ob;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (t + k >= 0 && t + k < len) {
+                        col_out[o + k] = c[u][k];
+                        val_out[o + k] = x[k];
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Copies A into A + I: out position of input entry t of row i is
 // row_ptr_out[i] + t (+1 past the inserted diagonal).  With NORM the values
-// are scaled: ((v) * dis_i) * dis_j.  Reads VEC entries per lane and step.
+// are scaled: ((v) * dis_i) * dis_j.  VEC = 4: aligned output granules
+// (copy_row_granules; col_out and val_out 16-byte aligned); VEC = 1: one
+// entry per lane and step.
 template <bool NORM, int VEC>
 __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ col_ind,
@@ -506,6 +606,11 @@ __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     const int ob = row_ptr_out[row];
     float dis_i = 1.0f;
     if constexpr (NORM) dis_i = dis[row];
+    if constexpr (VEC == 4) {
+        copy_row_granules<NORM, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out,
+                                        val_out);
+        return;
+    }
     copy_span<NORM, VEC, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out, val_out);
     if (g == 0 && ins >= 0) {
         float x = 1.0f;
@@ -641,6 +746,11 @@ __global__ __launch_bounds__(kLongBlock) void self_loop_copy_long_kernel(
         const int ob = row_ptr_out[i];
         float dis_i = 1.0f;
         if constexpr (NORM) dis_i = dis[i];
+        if constexpr (VEC == 4) {
+            copy_row_granules<NORM, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x),
+                                                i, ins, ob, dis_i, dis, col_out, val_out);
+            continue;
+        }
         copy_span<NORM, VEC, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x), i, ins,
                                          ob, dis_i, dis, col_out, val_out);
         if (threadIdx.x == 0 && ins >= 0) {
@@ -848,13 +958,15 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
             row_ptr, col_ind, val, long_list, long_count, first_ins, new_len, nullptr, nullptr);
     TG_LAUNCH_CHECK();
     exclusive_scan_i32(new_len, row_ptr_out, n, scan, s);
-    if (norm && v4)
+    // the copy writes 128-bit granules when both outputs are 16-byte aligned
+    const bool o4 = (reinterpret_cast<uintptr_t>(col_out) | reinterpret_cast<uintptr_t>(val_out)) % 16 == 0;
+    if (norm && o4)
         self_loop_copy_kernel<true, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
                                                               row_ptr_out, dis, col_out, val_out);
     else if (norm)
         self_loop_copy_kernel<true, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
                                                               row_ptr_out, dis, col_out, val_out);
-    else if (v4)
+    else if (o4)
         self_loop_copy_kernel<false, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n,
                                                                first_ins, row_ptr_out, nullptr,
                                                                col_out, val_out);
@@ -863,7 +975,7 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
                                                                first_ins, row_ptr_out, nullptr,
                                                                col_out, val_out);
     TG_LAUNCH_CHECK();
-    if (norm && v4)
+    if (norm && o4)
         self_loop_copy_long_kernel<true, 4><<<long_grid, kLongBlock, 0, s>>>(
             row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
             val_out);
@@ -871,7 +983,7 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
         self_loop_copy_long_kernel<true, 1><<<long_grid, kLongBlock, 0, s>>>(
             row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
             val_out);
-    else if (v4)
+    else if (o4)
         self_loop_copy_long_kernel<false, 4><<<long_grid, kLongBlock, 0, s>>>(
             row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, nullptr,
             col_out, val_out);
