@@ -190,6 +190,57 @@ def test_self_loops_long_rows(gpu, restate, weights):
     np.testing.assert_array_equal(bits(got.val.cpu().numpy()), bits(want.val))
 
 
+@pytest.mark.parametrize("in_off,out_off", [(0, 1), (1, 0), (1, 1), (0, 2), (3, 0)])
+def test_self_loops_pointer_alignment(gpu, restate, in_off, out_off):
+    """col_ind / val inputs and outputs starting 4-12 bytes past a 16-byte
+    boundary (C-ABI callers may pass any element-aligned pointer): the
+    128-bit read and aligned-granule copy paths and the entry-wise ones give
+    the same bits."""
+    import tinygnn_amd as tg
+    torch = gpu
+    rng = np.random.default_rng(23)
+    n = 700
+    a = random_csr(rng, n, n, avg_deg=12, max_deg=3000, empty_frac=0.1)
+    rows = np.repeat(np.arange(n), np.diff(a.row_ptr))
+    diag = rng.choice(n, size=n // 3, replace=False)
+    g = restate.edge_list_to_csr(np.concatenate([rows, diag]).astype(np.int32),
+                                 np.concatenate([a.col_ind, diag]).astype(np.int32), n)
+    g.val[:] = (rng.random(g.nnz) * 2 + 0.01).astype(np.float32)
+    assert np.diff(g.row_ptr).max() > 2048  # the workgroup-per-row kernels too
+
+    def placed(x, off):  # x's values in a device buffer, starting off elements in
+        buf = torch.zeros(x.size + off + 4, dtype=torch.from_numpy(x[:1]).dtype).cuda()
+        buf[off:off + x.size] = torch.from_numpy(x).cuda()
+        return buf, buf.data_ptr() + off * x.itemsize
+
+    rp = torch.from_numpy(g.row_ptr).cuda()
+    ci_buf, ci_p = placed(g.col_ind, in_off)
+    v_buf, v_p = placed(g.val, in_off)
+    cap = g.nnz + n
+    for norm in (False, True):
+        want = restate.gcn_norm(g) if norm else restate.add_self_loops(g)
+        rp_o = torch.empty(n + 1, dtype=torch.int32).cuda()
+        co_buf, co_p = placed(np.zeros(cap, np.int32), out_off)
+        vo_buf, vo_p = placed(np.zeros(cap, np.float32), out_off)
+        if norm:
+            st = tg.lib.tg_gcn_norm(n, g.nnz, rp.data_ptr(), ci_p, v_p, rp_o.data_ptr(), co_p,
+                                    vo_p, None, None, None, 0, None)
+        else:
+            st = tg.lib.tg_add_self_loops(n, g.nnz, rp.data_ptr(), ci_p, v_p, rp_o.data_ptr(),
+                                          co_p, vo_p, None, 0, None)
+        tg.lib.check(st)
+        torch.cuda.synchronize()
+        nnz = want.row_ptr[-1]
+        np.testing.assert_array_equal(rp_o.cpu().numpy(), want.row_ptr)
+        ci_o = co_buf.cpu().numpy()[out_off:out_off + nnz]
+        v_o = vo_buf.cpu().numpy()[out_off:out_off + nnz]
+        np.testing.assert_array_equal(ci_o, want.col_ind)
+        np.testing.assert_array_equal(bits(v_o), bits(want.val))
+        # nothing written outside the outputs
+        assert not co_buf.cpu().numpy()[:out_off].any()
+        assert not co_buf.cpu().numpy()[out_off + nnz:].any()
+
+
 def test_gcn_norm_degree_sweep(gpu, restate):
     """1/sqrt(deg) correctly rounded for every integer degree 1..4096 (star-like
     rows of unit weights): the device sqrt and divide must round exactly as
