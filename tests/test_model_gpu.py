@@ -365,6 +365,56 @@ def test_blocking_across_modes(gpu):
         np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode} blocking {blocking}")
 
 
+@pytest.mark.parametrize("diagonal", [False, True])
+def test_blocked_gcn_unit_weights(gpu, restate, diagonal):
+    """GCN over an edge list's CSR (every value 1, no diagonal): in fast
+    precision the blocked aggregation is factored (D^-1/2 applied in the
+    GEMM's and the aggregation's stores, passes without values).  Within the
+    fast tolerance of the oracle, deterministic, the same bits in both
+    forward modes, and within tolerance of the unblocked (unfactored) path.
+    One diagonal entry in A (A + I then holds a 2) keeps the weighted blocked
+    passes, with the same guarantees; so does exact precision (bit-exact)."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(57)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=40, max_deg=2800, empty_frac=0.05)
+    rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
+    keep = rows != a.col_ind
+    src, dst = rows[keep], a.col_ind[keep].astype(np.int32)
+    if diagonal:
+        src = np.append(src, np.int32(17))
+        dst = np.append(dst, np.int32(17))
+    g = restate.edge_list_to_csr(src, dst, n)
+    assert (g.val == 1.0).all()
+    spec = synth.spec_gcn(48, 300, 7)
+    w = synth.model_weights(spec, seed=5)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
+    x = rng.standard_normal((n, 48)).astype(np.float32)
+    want = restate.model_forward(spec, w, g, x)
+    da = tg.DeviceCSR.from_numpy(n, n, g.row_ptr, g.col_ind, g.val)
+    xt = _t(gpu, x)
+    outs = {}
+    for blocking in (100, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(blocking)
+        got = m.forward(da, xt).cpu().numpy()
+        for mode in (tg.FORWARD_CACHED, tg.FORWARD_REFERENCE, tg.FORWARD_CACHED):
+            again = m.forward(da, xt, mode=mode).cpu().numpy()
+            np.testing.assert_array_equal(bits(got), bits(again), err_msg=f"mode {mode}")
+        assert_close(got, want, what=f"gcn unit weights blocking={blocking}")
+        outs[blocking] = got
+    assert_close(outs[100], outs[0], what="blocked vs unblocked")
+    if not diagonal:  # the factored sums round differently from the unblocked ones
+        assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
+    m = tg.Model.from_spec(spec, w)
+    m.set_precision(tg.PRECISION_EXACT)
+    m.set_blocking(100)
+    got = m.forward(da, xt).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+
+
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),
                                                ("gat64", True), ("gcn", False), ("sage", False),
                                                ("gat", False)])

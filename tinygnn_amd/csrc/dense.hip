@@ -38,6 +38,12 @@ __device__ __forceinline__ float epi_apply(float x, const float* __restrict__ bi
     return x;
 }
 
+// Output element (m, n): the row factor, then bias and activation.
+__device__ __forceinline__ float epi_out(const GemmArgs& g, float x, int64_t m, int64_t n) {
+    if (g.row_scale) x = x * g.row_scale[m];
+    return epi_apply(x, g.bias, n, g.epi);
+}
+
 // ---------------------------------------------------------------------------
 // In-order GEMM (bit-exact)
 // ---------------------------------------------------------------------------
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int64_t gn = n0 + tx * TN + j;
-            if (gn < N) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+            if (gn < N) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j], gm, gn);
         }
     }
 }
@@ -265,7 +271,7 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int64_t gn = n0 + tx * 8 + j;
-            if (gn < N) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j], g.bias, gn, g.epi);
+            if (gn < N) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j], gm, gn);
         }
     }
 }
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int64_t gm = m0 + wm + i * 16 + 4 * q + rr;
-                if (gm < M) g.c[c_index(g, gm, gn)] = epi_apply(acc[i][j][rr], g.bias, gn, g.epi);
+                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
             }
         }
 }

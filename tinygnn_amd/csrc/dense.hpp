@@ -36,6 +36,8 @@ struct GemmArgs {
     int64_t ldc = 0;
     const float* bias = nullptr;
     int epi = 0;
+    // per-row factor: C[m, :] = epilogue(row_scale[m] * (A B)[m, :]) (null: none)
+    const float* row_scale = nullptr;
     int64_t tail_from = -1;  // in-order dual only; -1 = no tail columns, else a multiple of 8
     // C's layout: 0 = row-major (ldc); > 0 = tile-major, column n of row m at
     // c[(n / 32) * c_tile_stride + m * 32 + n % 32] (ldc = 32): the layout the

@@ -20,6 +20,12 @@
 //     one pass per block of source nodes, so the gathered rows of a pass
 //     stay in L2; each pass continues the rows' sums, which keeps exact
 //     precision's in-order sums when the rows are in block order;
+//   * in fast precision, when every value of A + I is exactly 1 (A's values
+//     all 1 and no diagonal in A, as an edge list's CSR), a blocked GCN
+//     aggregation is factored: A_norm (HW) = D^-1/2 (A + I) (D^-1/2 HW),
+//     the D^-1/2 on the right applied in the GEMM's store and the one on the
+//     left in the aggregation's, so the passes read the column indices alone
+//     (no values): the same sum, rounded differently;
 //   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
 //     while the adjacency pointers and sizes are unchanged;
 //     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
@@ -92,6 +98,12 @@ struct tg_model_s {
     const float* key_v = nullptr;
     int64_t key_n = -1, key_nnz = -1;
     DeviceBuffer sl_rp, sl_ci, sl_v;  // A + I (normalised values when GCN is present)
+    DeviceBuffer dis;                 // gcn_norm's 1/sqrt(deg) (GCN present)
+    // fast precision, GCN present: every value of A + I is 1 (the blocked
+    // GCN aggregation is factored, its blocked copy carries no values)
+    bool unit_sl = false;
+    DeviceBuffer flag;
+    tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
     // column-blocked copies for the large aggregations (fast precision):
     // A_norm for GCN, A's structure for SAGE-mean
@@ -126,6 +138,21 @@ struct tg_model_s {
 
 namespace tg {
 namespace {
+
+// *flag = 0 if some value of A is not exactly 1, or if A has a diagonal
+// entry (then A + I has fewer than nnz + n entries); *flag is 1 before.
+__global__ __launch_bounds__(256) void unit_values_kernel(const float* __restrict__ v,
+                                                          int64_t nnz,
+                                                          const int32_t* __restrict__ sl_rp,
+                                                          int64_t n, int32_t* __restrict__ flag) {
+    bool bad = false;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nnz;
+         i += stride)
+        bad |= v[i] != 1.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0) bad |= sl_rp[n] != nnz + n;
+    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) *flag = 0;  // one store per wave
+}
 
 int64_t add_layer(tg_model_s& m, Layer&& l) {
     const char* name = l.type == LType::GCN ? "GCNLayer" : l.type == LType::SAGE ? "SAGELayer"
@@ -237,11 +264,13 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const int64_t chunk = exact ? (int64_t(1) << 24) : 0;
     // A + I: GCN's normalised values, or the structure alone for GAT (weighted
     // passes: 64-column lane groups); A: SAGE's mean (32-column groups)
+    // (a factored GCN aggregation reads no values either)
     const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, 64);
     if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                      m.need_norm() ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s, chunk);
+                      m.need_norm() && !m.unit_sl ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s,
+                      chunk);
         m.blk_sl->group_cols = 64;
         if (exact && !m.blk_sl->in_order) m.blk_sl.reset();
     } else {
@@ -287,16 +316,33 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         m.sl_ci.reserve((nnz + n) * sizeof(int32_t));
         m.sl_v.reserve((nnz + n) * sizeof(float));
         m.work.reserve(self_loops_workspace(n));
-        if (m.need_norm())
+        if (m.need_norm()) {
+            m.dis.reserve(n * sizeof(float));
             gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                     m.sl_v.as<float>(), nullptr, nullptr, m.work.get(), m.work.size(), s);
-        else
+                     m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(), m.work.size(),
+                     s);
+        } else {
             add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                            m.sl_v.as<float>(), m.work.get(), m.work.size(), s);
+        }
         if (!m.plan_sl) m.plan_sl = std::make_unique<tg_spmm_plan_s>();
         build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, chunk, s);
     } else {
         m.plan_sl.reset();
+    }
+    m.unit_sl = false;
+    if (m.need_norm() && m.precision != TG_PRECISION_EXACT) {
+        m.flag.reserve(sizeof(int32_t));
+        m.flag_host.reserve(sizeof(int32_t));
+        fill_i32(m.flag.as<int32_t>(), 1, 1, s);
+        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 256), 1), 4096);
+        unit_values_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+            v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
+        TG_LAUNCH_CHECK();
+        TG_HIP(hipMemcpyAsync(m.flag_host.as<int32_t>(), m.flag.as<int32_t>(), sizeof(int32_t),
+                              hipMemcpyDeviceToHost, s));
+        TG_HIP(hipStreamSynchronize(s));
+        m.unit_sl = *m.flag_host.as<int32_t>() == 1;
     }
     m.have_cache = true;
     m.built_precision = m.precision;
@@ -380,6 +426,9 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             // (blocked: tile-major, each 32-column tile one slab of n rows)
             float* hw = m.tmp.as<float>();
             const bool tiled = m.blk_sl != nullptr;
+            // factored (unit A + I, blocked): D^-1/2 in the GEMM's and the
+            // aggregation's stores, an unweighted blocked copy
+            const bool factored = tiled && m.unit_sl;
             const int64_t ldhw = tiled ? 32 : gather_pitch(l.out);
             GemmArgs g;
             g.m = n;
@@ -392,8 +441,14 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             g.c = hw;
             g.ldc = ldhw;
             g.c_tile_stride = tiled ? n * 32 : 0;
+            if (factored) g.row_scale = m.dis.as<float>();
             gemm(g, algo, s);
             AggEpilogue epi;
+            if (factored) {
+                epi.row_scale = m.dis.as<float>();
+                epi.scale_ld = 1;
+                epi.scale_cols = static_cast<int>(l.out);
+            }
             epi.bias = l.bias ? l.b.as<float>() : nullptr;
             epi.act = l.act;
             epi.post = l.post;
