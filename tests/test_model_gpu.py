@@ -365,15 +365,17 @@ def test_blocking_across_modes(gpu):
         np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode} blocking {blocking}")
 
 
-@pytest.mark.parametrize("diagonal", [False, True])
-def test_blocked_gcn_unit_weights(gpu, restate, diagonal):
+@pytest.mark.parametrize("variant", ["unit", "diagonal", "last_weight"])
+def test_blocked_gcn_unit_weights(gpu, restate, variant):
     """GCN over an edge list's CSR (every value 1, no diagonal): in fast
     precision the blocked aggregation is factored (D^-1/2 applied in the
     GEMM's and the aggregation's stores, passes without values).  Within the
     fast tolerance of the oracle, deterministic, the same bits in both
     forward modes, and within tolerance of the unblocked (unfactored) path.
-    One diagonal entry in A (A + I then holds a 2) keeps the weighted blocked
-    passes, with the same guarantees; so does exact precision (bit-exact)."""
+    One diagonal entry in A (A + I then holds a 2), or a last value of 2
+    (past the check's 128-bit reads: nnz % 4 != 0), keeps the weighted
+    blocked passes, with the same guarantees; so does exact precision
+    (bit-exact)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(57)
     n = 3000
@@ -381,11 +383,16 @@ def test_blocked_gcn_unit_weights(gpu, restate, diagonal):
     rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
     keep = rows != a.col_ind
     src, dst = rows[keep], a.col_ind[keep].astype(np.int32)
-    if diagonal:
+    if variant == "diagonal":
         src = np.append(src, np.int32(17))
         dst = np.append(dst, np.int32(17))
+    if variant == "last_weight" and src.size % 4 == 0:
+        src, dst = src[:-1], dst[:-1]
     g = restate.edge_list_to_csr(src, dst, n)
     assert (g.val == 1.0).all()
+    if variant == "last_weight":
+        assert g.nnz % 4 != 0
+        g.val[-1] = 2.0
     spec = synth.spec_gcn(48, 300, 7)
     w = synth.model_weights(spec, seed=5)
     for k in w:
@@ -406,7 +413,7 @@ def test_blocked_gcn_unit_weights(gpu, restate, diagonal):
         assert_close(got, want, what=f"gcn unit weights blocking={blocking}")
         outs[blocking] = got
     assert_close(outs[100], outs[0], what="blocked vs unblocked")
-    if not diagonal:  # the factored sums round differently from the unblocked ones
+    if variant == "unit":  # the factored sums round differently from the unblocked ones
         assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
     m = tg.Model.from_spec(spec, w)
     m.set_precision(tg.PRECISION_EXACT)

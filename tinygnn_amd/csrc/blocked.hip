@@ -58,31 +58,39 @@ __device__ __forceinline__ int div_by(int c, int d, double inv_d) {
 }
 
 // One wave per row.  The row is walked in 64-entry batches in order (the
-// next batch's entries are loaded while the current one is placed); for
-// each block b the wave ballots the entries of the batch that fall in b, so
-// an entry's rank among the row's entries of its block is the count of
-// earlier batches plus the ballot bits below its lane (a stable partition).
-// Lane b keeps block b's running count (COUNT: written to cnt[b*n + row]) or
-// running output position (SCATTER: starting at brp[b*n + row]).
-// COUNT also flags (*disorder = 1) a row whose entries step back to an
-// earlier block (the previous entry's block comes from the lane below, or
-// from the previous batch's last lane).
+// next batch's entries are loaded while the current one is placed).  The
+// wave keeps one slot per block in LDS: COUNT, the block's entries so far
+// (written to cnt[b*n + row] at the end); SCATTER, the block's next output
+// position (starting at brp[b*n + row]).  A batch splits into runs of equal
+// block (lane order); a run's entries take consecutive positions.
+//   * COUNT: each run's last lane adds the run's length to its block's slot.
+//     A row whose entries step back to an earlier block (the previous
+//     entry's block comes from the lane below, or from the previous batch's
+//     last lane) sets *disorder = 1.
+//   * SCATTER, batch in block order (the common case: sorted rows): every
+//     block has at most one run, so an entry's position is its block's slot
+//     plus its rank in the run, and the run's last lane moves the slot past
+//     the run.  Otherwise, per block b present in the batch, the entries of b
+//     are ranked by the ballot bits below their lane (a stable partition).
 template <bool SCATTER>
 __global__ __launch_bounds__(256) void block_split_kernel(
     const int32_t* __restrict__ rp, const int32_t* __restrict__ ci,
     const float* __restrict__ v, int64_t n, int rows_per_block, double inv_rows, int nb,
     int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv,
     int32_t* __restrict__ disorder) {
+    __shared__ int32_t slots[4][64];
     const int lane = threadIdx.x & 63;
+    int32_t* slot = slots[threadIdx.x >> 6];
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (row >= n) return;  // uniform per wave
+    if (row >= n) return;  // uniform per wave (no workgroup barrier below)
     const int s = rp[row], e = rp[row + 1];
-    int run = 0;
-    if (SCATTER && lane < nb) run = cnt_or_brp[static_cast<int64_t>(lane) * n + row];
+    if (lane < nb) slot[lane] = SCATTER ? cnt_or_brp[static_cast<int64_t>(lane) * n + row] : 0;
+    __builtin_amdgcn_wave_barrier();
     int cn = s + lane < e ? ci[s + lane] : 0;
     float vn = 0.0f;
     if (SCATTER && bv) vn = s + lane < e ? v[s + lane] : 0.0f;
     int prev_last = -1;  // the block of the previous batch's last entry
+    bool back_seen = false;
     for (int i = s; i < e; i += 64) {
         const int idx = i + lane;
         const bool valid = idx < e;
@@ -94,27 +102,49 @@ __global__ __launch_bounds__(256) void block_split_kernel(
             if (SCATTER && bv) vn = nidx < e ? v[nidx] : 0.0f;
         }
         const int blk = valid ? div_by(c, rows_per_block, inv_rows) : -1;
+        const int below = __shfl_up(blk, 1);
+        const int above = __shfl_down(blk, 1);
+        const int pb = lane == 0 ? prev_last : below;
+        const bool in_order = __ballot(valid && pb > blk) == 0;
+        prev_last = __shfl(blk, 63);  // a full batch continues; the last one ends the row
+        // runs: a start where the block changes from the lane below, an end
+        // where it changes to the lane above (invalid lanes hold -1)
+        const uint64_t starts = __ballot(valid && (lane == 0 || below != blk));
+        const bool run_end = valid && (lane == 63 || above != blk);
+        const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+        const int rank = lane - (63 - __clzll(starts & upto));  // valid lanes only
         if (!SCATTER) {
-            const int below = __shfl_up(blk, 1);
-            const int pb = lane == 0 ? prev_last : below;
-            const bool back = valid && pb > blk;
-            if (__ballot(back) != 0 && lane == 0) atomicOr(disorder, 1);
-            prev_last = __shfl(blk, 63);  // a full batch continues; the last one ends the row
+            back_seen |= !in_order;
+            if (run_end) atomicAdd(&slot[blk], rank + 1);
+            continue;
         }
         int pos = 0;
-        for (int b = 0; b < nb; ++b) {
-            const uint64_t m = __ballot(blk == b);
-            if (m == 0) continue;  // uniform: the ballot is the wave's
-            const int base = __shfl(run, b);
-            if (blk == b) pos = base + lanes_below(m);
-            if (lane == b) run += __popcll(m);
+        if (in_order) {
+            if (valid) pos = slot[blk] + rank;
+            __builtin_amdgcn_wave_barrier();
+            if (run_end) slot[blk] = pos + 1;
+        } else {
+            for (int b = 0; b < nb; ++b) {
+                const uint64_t m = __ballot(blk == b);
+                if (m == 0) continue;  // uniform: the ballot is the wave's
+                const int base = slot[b];
+                __builtin_amdgcn_wave_barrier();
+                if (blk == b) pos = base + lanes_below(m);
+                if (lane == b) slot[b] = base + __popcll(m);
+                __builtin_amdgcn_wave_barrier();
+            }
         }
-        if (SCATTER && valid) {
+        __builtin_amdgcn_wave_barrier();
+        if (valid) {
             bci[pos] = c;
             if (bv) bv[pos] = val;
         }
     }
-    if (!SCATTER && lane < nb) cnt_or_brp[static_cast<int64_t>(lane) * n + row] = run;
+    if (!SCATTER) {
+        if (back_seen && lane == 0) atomicOr(disorder, 1);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < nb) cnt_or_brp[static_cast<int64_t>(lane) * n + row] = slot[lane];
+    }
 }
 
 }  // namespace

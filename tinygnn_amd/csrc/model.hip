@@ -141,16 +141,28 @@ namespace {
 
 // *flag = 0 if some value of A is not exactly 1, or if A has a diagonal
 // entry (then A + I has fewer than nnz + n entries); *flag is 1 before.
+// VEC = 4: 128-bit reads (v 16-byte aligned), the last nnz % 4 values on
+// the first thread.
+template <int VEC>
 __global__ __launch_bounds__(256) void unit_values_kernel(const float* __restrict__ v,
                                                           int64_t nnz,
                                                           const int32_t* __restrict__ sl_rp,
                                                           int64_t n, int32_t* __restrict__ flag) {
     bool bad = false;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nnz;
-         i += stride)
-        bad |= v[i] != 1.0f;
-    if (blockIdx.x == 0 && threadIdx.x == 0) bad |= sl_rp[n] != nnz + n;
+    const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if constexpr (VEC == 4) {
+        const float4* v4 = reinterpret_cast<const float4*>(v);
+        for (int64_t i = tid; i < nnz / 4; i += stride) {
+            const float4 x = v4[i];
+            bad |= (x.x != 1.0f) | (x.y != 1.0f) | (x.z != 1.0f) | (x.w != 1.0f);
+        }
+        if (tid == 0)
+            for (int64_t i = nnz / 4 * 4; i < nnz; ++i) bad |= v[i] != 1.0f;
+    } else {
+        for (int64_t i = tid; i < nnz; i += stride) bad |= v[i] != 1.0f;
+    }
+    if (tid == 0) bad |= sl_rp[n] != nnz + n;
     if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) *flag = 0;  // one store per wave
 }
 
@@ -335,9 +347,13 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         m.flag.reserve(sizeof(int32_t));
         m.flag_host.reserve(sizeof(int32_t));
         fill_i32(m.flag.as<int32_t>(), 1, 1, s);
-        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 256), 1), 4096);
-        unit_values_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(
-            v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
+        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 1024), 1), 4096);
+        if (reinterpret_cast<uintptr_t>(v) % 16 == 0)
+            unit_values_kernel<4><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+                v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
+        else
+            unit_values_kernel<1><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+                v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
         TG_LAUNCH_CHECK();
         TG_HIP(hipMemcpyAsync(m.flag_host.as<int32_t>(), m.flag.as<int32_t>(), sizeof(int32_t),
                               hipMemcpyDeviceToHost, s));
