@@ -549,14 +549,28 @@ __global__ __launch_bounds__(256) void gat_stats_kernel(const int4* __restrict__
             m[k] = -INFINITY;
             sm[k] = 0.0f;
         }
+        // the next batch's column indices are loaded behind this batch's
+        // dst gathers
+        int cn[UN];
+#pragma unroll
+        for (int u = 0; u < UN; ++u) {
+            const int i = ch.y + u * GL + lane;
+            cn[u] = i < ch.z ? ci[i] : 0;
+        }
         for (int i0 = ch.y; i0 < ch.z; i0 += GL * UN) {
             float x[UN][NH];
             bool ok[UN];
 #pragma unroll
             for (int u = 0; u < UN; ++u) {
-                const int i = i0 + u * GL + lane;
-                ok[u] = i < ch.z;
-                gat_dst<NH>(dst, heads, h0, ok[u] ? ci[i] : 0, x[u]);
+                ok[u] = i0 + u * GL + lane < ch.z;
+                gat_dst<NH>(dst, heads, h0, cn[u], x[u]);
+            }
+            if (i0 + GL * UN < ch.z) {  // uniform per group
+#pragma unroll
+                for (int u = 0; u < UN; ++u) {
+                    const int i = i0 + GL * UN + u * GL + lane;
+                    cn[u] = i < ch.z ? ci[i] : 0;
+                }
             }
 #pragma unroll
             for (int k = 0; k < NH; ++k) {
