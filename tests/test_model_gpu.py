@@ -365,7 +365,7 @@ def test_blocking_across_modes(gpu):
         np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode} blocking {blocking}")
 
 
-@pytest.mark.parametrize("variant", ["unit", "diagonal", "last_weight"])
+@pytest.mark.parametrize("variant", ["unit", "diagonal", "last_weight", "unit_gat_stack"])
 def test_blocked_gcn_unit_weights(gpu, restate, variant):
     """GCN over an edge list's CSR (every value 1, no diagonal): in fast
     precision the blocked aggregation is factored (D^-1/2 applied in the
@@ -375,7 +375,8 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     One diagonal entry in A (A + I then holds a 2), or a last value of 2
     (past the check's 128-bit reads: nnz % 4 != 0), keeps the weighted
     blocked passes, with the same guarantees; so does exact precision
-    (bit-exact)."""
+    (bit-exact).  A GAT layer before the GCN shares the blocked A + I (its
+    weighted passes in 64-column groups, the factored GCN's too)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(57)
     n = 3000
@@ -394,6 +395,10 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
         assert g.nnz % 4 != 0
         g.val[-1] = 2.0
     spec = synth.spec_gcn(48, 300, 7)
+    if variant == "unit_gat_stack":
+        spec = [dict(type="gat", **{"in": 48}, out=64, heads=2, concat=True, slope=0.2, act=0,
+                     post=2),
+                dict(type="gcn", **{"in": 128}, out=7, act=0, post=0)]
     w = synth.model_weights(spec, seed=5)
     for k in w:
         if k.endswith("bias"):
@@ -415,11 +420,16 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     assert_close(outs[100], outs[0], what="blocked vs unblocked")
     if variant == "unit":  # the factored sums round differently from the unblocked ones
         assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
-    m = tg.Model.from_spec(spec, w)
-    m.set_precision(tg.PRECISION_EXACT)
-    m.set_blocking(100)
-    got = m.forward(da, xt).cpu().numpy()
-    np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+    exact = {}
+    for blocking in (100, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_precision(tg.PRECISION_EXACT)
+        m.set_blocking(blocking)
+        exact[blocking] = m.forward(da, xt).cpu().numpy()
+    # GCN alone: the reference's bytes; after a GAT layer: the unblocked exact path's
+    np.testing.assert_array_equal(exact[100].view(np.int32), exact[0].view(np.int32))
+    if variant != "unit_gat_stack":
+        np.testing.assert_array_equal(exact[100].view(np.int32), want.view(np.int32))
 
 
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),

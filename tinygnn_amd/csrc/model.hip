@@ -276,14 +276,18 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const int64_t chunk = exact ? (int64_t(1) << 24) : 0;
     // A + I: GCN's normalised values, or the structure alone for GAT (weighted
     // passes: 64-column lane groups); A: SAGE's mean (32-column groups)
-    // (a factored GCN aggregation reads no values either)
-    const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, 64);
+    // (a factored GCN aggregation reads no values either).  Passes without a
+    // value stream run in 32-column groups, as SAGE's (config-E GCN, factored:
+    // 64-column groups at 10 blocks 9.64 ms, 32-column groups at 6 blocks
+    // 9.36 ms); a GAT layer's weighted passes keep 64-column groups.
+    const int gc_sl = (m.unit_sl && !m.need_sl()) ? 32 : 64;
+    const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, gc_sl);
     if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() && !m.unit_sl ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s,
                       chunk);
-        m.blk_sl->group_cols = 64;
+        m.blk_sl->group_cols = gc_sl;
         if (exact && !m.blk_sl->in_order) m.blk_sl.reset();
     } else {
         m.blk_sl.reset();
