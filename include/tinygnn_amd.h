@@ -301,10 +301,13 @@ int tg_model_set_precision(tg_model_t model, int precision);
  * that many source nodes (at least n/64) and aggregates block by block, so
  * each pass gathers from a slice of the feature matrix that stays in L2;
  * 0 disables it; -1 (the default) uses equal blocks of at most 23552 rows for
- * A + I (GCN, GAT: passes of 64-column lane groups) and 38912 rows for A
- * (SAGE mean: 32-column groups) when the graph holds at least 8 entries per
- * row and block.  The blocked copy of the adjacency is built with the other
- * cached preprocessing (one more copy of col_ind / val). */
+ * weighted passes over A + I (GAT, and GCN in exact precision or on
+ * weighted graphs: 64-column lane groups) and 38912 rows for passes without
+ * values (SAGE mean over A; fast GCN over an A + I whose values are all 1:
+ * 32-column groups) when the graph holds at least 8 entries per row and
+ * block.  The blocked copy of the adjacency is built with the other
+ * preprocessing of the forward (one more copy of col_ind, and of val for
+ * weighted passes). */
 int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block);
 int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
                      const int32_t* row_ptr, const int32_t* col_ind, const float* val,

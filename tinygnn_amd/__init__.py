@@ -401,12 +401,13 @@ class Model:
         lib.check(lib.tg_model_set_precision(self.h, precision))
 
     def set_blocking(self, rows_per_block: int = -1) -> None:
-        """Column blocking of the GCN / SAGE-mean / GAT aggregations of cached
-        forwards (exact precision: only for rows in column order, keeping the
-        reference's summation order): rows_per_block source nodes per block,
-        0 = off, -1 = the default (equal blocks of at most 23552 rows for
-        A + I, the GCN and GAT passes, and 38912 for A, SAGE's mean passes,
-        on graphs dense enough to pay)."""
+        """Column blocking of the GCN / SAGE-mean / GAT aggregations (both
+        forward modes; exact precision: only for rows in column order, keeping
+        the reference's summation order): rows_per_block source nodes per
+        block, 0 = off, -1 = the default (equal blocks of at most 23552 rows
+        for weighted passes over A + I -- GAT, exact or weighted GCN -- and
+        38912 for passes without values -- SAGE's mean over A, fast GCN over a
+        unit-valued A + I -- on graphs dense enough to pay)."""
         lib.check(lib.tg_model_set_blocking(self.h, rows_per_block))
 
     def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):

@@ -36,8 +36,8 @@ constexpr int kMaxBlocks = 64;   // one lane of a wave per column block
 //   index stream, not the gathered bytes, bounds a pass) and gather two
 //   lines per row, so they take smaller blocks: ten blocks of 23,297 rows
 //   10.59 / 10.31 / 14.68 ms; eleven or twelve blocks within 1%; eight 6%
-//   and six 16% slower.  SAGE's mean passes (no value stream) keep
-//   32-column groups.
+//   and six 16% slower.  Passes without a value stream (SAGE's mean, the
+//   factored GCN) keep 32-column groups.
 constexpr int64_t kDefaultBlockRows32 = 38912;
 constexpr int64_t kDefaultBlockRows64 = 23552;
 
