@@ -420,6 +420,13 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     assert_close(outs[100], outs[0], what="blocked vs unblocked")
     if variant == "unit":  # the factored sums round differently from the unblocked ones
         assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
+    # a new blocking setting between cached calls (the factored path keeps no
+    # normalised values; turning blocking off must bring them back)
+    m = tg.Model.from_spec(spec, w)
+    for blocking in (100, 0, 100, 0):
+        m.set_blocking(blocking)
+        got = m.forward(da, xt).cpu().numpy()
+        np.testing.assert_array_equal(bits(got), bits(outs[blocking]), err_msg=f"{blocking}")
     exact = {}
     for blocking in (100, 0):
         m = tg.Model.from_spec(spec, w)

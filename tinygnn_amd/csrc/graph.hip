@@ -434,6 +434,7 @@ __global__ __launch_bounds__(256) void self_loop_info_kernel(
 // inserted diagonal at `ins`), scaled when NORM.  `lanes` threads share the
 // row (this one is `lane`); each keeps kCopyUnroll granules of VEC entries in
 // flight, so the loads of four steps (and then their dis[c] gathers) overlap.
+// A null val_out copies the structure alone (val is then not read).
 constexpr int kCopyUnroll = 4;
 template <bool NORM, int VEC, int LANES>
 __device__ __forceinline__ void copy_span(const int32_t* __restrict__ col_ind,
@@ -442,18 +443,19 @@ __device__ __forceinline__ void copy_span(const int32_t* __restrict__ col_ind,
                                           const float* __restrict__ dis,
                                           int32_t* __restrict__ col_out,
                                           float* __restrict__ val_out) {
+    const bool vals = val_out != nullptr;  // null: the structure alone
     const int start = VEC == 4 ? (b & ~3) : b;
     constexpr int kStep = LANES * VEC;
     for (int q0 = start + lane * VEC; q0 < e; q0 += kStep * kCopyUnroll) {
         int32_t c[kCopyUnroll][VEC];
-        float v[kCopyUnroll][VEC];
+        float v[kCopyUnroll][VEC] = {};
         float dj[kCopyUnroll][VEC];
 #pragma unroll
         for (int u = 0; u < kCopyUnroll; ++u) {
             const int q = q0 + u * kStep;
             if (q < e) {
                 load_vec<VEC>(col_ind, q, c[u]);
-                load_vec<VEC>(val, q, v[u]);
+                if (vals) load_vec<VEC>(val, q, v[u]);
             }
         }
 #pragma unroll
@@ -481,7 +483,7 @@ __device__ __forceinline__ void copy_span(const int32_t* __restrict__ col_ind,
                 if constexpr (NORM) x = (x * dis_i) * dj[u][k];
                 const int o = ob + t + ((ins >= 0 && t >= ins) ? 1 : 0);
                 col_out[o] = c[u][k];
-                val_out[o] = x;
+                if (vals) val_out[o] = x;
             }
         }
     }
@@ -504,7 +506,8 @@ typedef float f32x4_dw __attribute__((ext_vector_type(4), aligned(4)));
 // array and stores one aligned vector per array; the row's first and last
 // granules (shared with the neighbouring rows) and the diagonal's go entry
 // by entry.  Values: x = v (+1 on the diagonal), with NORM (x * dis_i) *
-// dis[col]; the inserted diagonal is x = 1.
+// dis[col]; the inserted diagonal is x = 1.  A null val_out copies the
+// structure alone (val is then not read).
 template <bool NORM, int LANES>
 __device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ col_ind,
                                                   const float* __restrict__ val, int b, int e,
@@ -512,12 +515,13 @@ __device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ co
                                                   float dis_i, const float* __restrict__ dis,
                                                   int32_t* __restrict__ col_out,
                                                   float* __restrict__ val_out) {
+    const bool vals = val_out != nullptr;  // null: the structure alone
     const int len = (e - b) + (ins >= 0 ? 1 : 0);
     const int end = ob + len;
     constexpr int kStep = LANES * 4;
     for (int o0 = (ob & ~3) + lane * 4; o0 < end; o0 += kStep * kCopyUnroll) {
         i32x4 c[kCopyUnroll];
-        f32x4 v[kCopyUnroll];
+        f32x4 v[kCopyUnroll] = {};
         f32x4 dj[kCopyUnroll];
         bool fast[kCopyUnroll];
 #pragma unroll
@@ -528,7 +532,7 @@ __device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ co
             if (fast[u]) {
                 const int s0 = b + t - ((ins >= 0 && t > ins) ? 1 : 0);
                 c[u] = *reinterpret_cast<const i32x4_dw*>(col_ind + s0);
-                v[u] = *reinterpret_cast<const f32x4_dw*>(val + s0);
+                if (vals) v[u] = *reinterpret_cast<const f32x4_dw*>(val + s0);
             } else if (o < end) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
@@ -540,7 +544,7 @@ __device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ co
                     if (tk >= 0 && tk < len && tk != ins) {
                         const int src = b + tk - ((ins >= 0 && tk > ins) ? 1 : 0);
                         ck = col_ind[src];
-                        vk = val[src];
+                        if (vals) vk = val[src];
                     }
                     c[u][k] = ck;
                     v[u][k] = vk;
@@ -570,14 +574,14 @@ __device__ __forceinline__ void copy_row_granules(const int32_t* __restrict__ co
             }
             if (fast[u]) {
                 *reinterpret_cast<i32x4*>(col_out + o) = c[u];
-                *reinterpret_cast<f32x4*>(val_out + o) = x;
+                if (vals) *reinterpret_cast<f32x4*>(val_out + o) = x;
             } else {
                 const int t = o - ob;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (t + k >= 0 && t + k < len) {
                         col_out[o + k] = c[u][k];
-                        val_out[o + k] = x[k];
+                        if (vals) val_out[o + k] = x[k];
                     }
                 }
             }
@@ -609,14 +613,15 @@ __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     if constexpr (VEC == 4) {
         copy_row_granules<NORM, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out,
                                         val_out);
-        return;
-    }
-    copy_span<NORM, VEC, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out, val_out);
-    if (g == 0 && ins >= 0) {
-        float x = 1.0f;
-        if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
-        col_out[ob + ins] = i;
-        val_out[ob + ins] = x;
+    } else {
+        copy_span<NORM, VEC, kGroup>(col_ind, val, b, e, g, i, ins, ob, dis_i, dis, col_out,
+                                     val_out);
+        if (g == 0 && ins >= 0) {
+            float x = 1.0f;
+            if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
+            col_out[ob + ins] = i;
+            if (val_out) val_out[ob + ins] = x;
+        }
     }
 }
 
@@ -749,15 +754,15 @@ __global__ __launch_bounds__(kLongBlock) void self_loop_copy_long_kernel(
         if constexpr (VEC == 4) {
             copy_row_granules<NORM, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x),
                                                 i, ins, ob, dis_i, dis, col_out, val_out);
-            continue;
-        }
-        copy_span<NORM, VEC, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x), i, ins,
-                                         ob, dis_i, dis, col_out, val_out);
-        if (threadIdx.x == 0 && ins >= 0) {
-            float x = 1.0f;
-            if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
-            col_out[ob + ins] = i;
-            val_out[ob + ins] = x;
+        } else {
+            copy_span<NORM, VEC, kLongBlock>(col_ind, val, b, e, static_cast<int>(threadIdx.x), i,
+                                             ins, ob, dis_i, dis, col_out, val_out);
+            if (threadIdx.x == 0 && ins >= 0) {
+                float x = 1.0f;
+                if constexpr (NORM) x = (1.0f * dis_i) * dis_i;
+                col_out[ob + ins] = i;
+                if (val_out) val_out[ob + ins] = x;
+            }
         }
     }
 }
@@ -884,10 +889,12 @@ void require_square(int64_t n, const char* fn) {
 }
 
 // Shared by add_self_loops and gcn_norm.
+// values = false: row_ptr_out and col_out only (val_out is ignored; with
+// norm, deg_out / dis_out are still computed).
 void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
                      const int32_t* col_ind, const float* val, int32_t* row_ptr_out,
                      int32_t* col_out, float* val_out, float* deg_out, float* dis_out,
-                     void* workspace, size_t ws_bytes, hipStream_t s) {
+                     void* workspace, size_t ws_bytes, hipStream_t s, bool values) {
     const char* fn = norm ? "gcn_norm" : "add_self_loops";
     require_square(n, fn);
     require(nnz >= 0 && nnz + n < (int64_t(1) << 31),
@@ -897,7 +904,9 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
         TG_LAUNCH_CHECK();
         return;
     }
-    require(row_ptr && row_ptr_out && col_out && val_out, std::string(fn) + ": null pointer");
+    if (!values) val_out = nullptr;
+    require(row_ptr && row_ptr_out && col_out && (val_out || !values),
+            std::string(fn) + ": null pointer");
     require(nnz == 0 || (col_ind && val), std::string(fn) + ": null pointer");
     Carver probe(nullptr, 0);
     probe.take<int32_t>(n);
@@ -960,10 +969,12 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
     exclusive_scan_i32(new_len, row_ptr_out, n, scan, s);
     // the copy writes 128-bit granules when both outputs are 16-byte aligned
     const bool o4 = (reinterpret_cast<uintptr_t>(col_out) | reinterpret_cast<uintptr_t>(val_out)) % 16 == 0;
-    if (norm && o4)
+    // the structure alone needs no scaling: copied as add_self_loops' structure
+    const bool scale = norm && values;
+    if (scale && o4)
         self_loop_copy_kernel<true, 4><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
                                                               row_ptr_out, dis, col_out, val_out);
-    else if (norm)
+    else if (scale)
         self_loop_copy_kernel<true, 1><<<blocks, 256, 0, s>>>(row_ptr, col_ind, val, n, first_ins,
                                                               row_ptr_out, dis, col_out, val_out);
     else if (o4)
@@ -975,11 +986,11 @@ void self_loops_impl(bool norm, int64_t n, int64_t nnz, const int32_t* row_ptr,
                                                                first_ins, row_ptr_out, nullptr,
                                                                col_out, val_out);
     TG_LAUNCH_CHECK();
-    if (norm && o4)
+    if (scale && o4)
         self_loop_copy_long_kernel<true, 4><<<long_grid, kLongBlock, 0, s>>>(
             row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
             val_out);
-    else if (norm)
+    else if (scale)
         self_loop_copy_long_kernel<true, 1><<<long_grid, kLongBlock, 0, s>>>(
             row_ptr, col_ind, val, long_list, long_count, first_ins, row_ptr_out, dis, col_out,
             val_out);
@@ -1118,16 +1129,17 @@ void csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz, const int32_t* ro
 
 void add_self_loops(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
                     const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
-                    void* ws, size_t ws_bytes, hipStream_t s) {
+                    void* ws, size_t ws_bytes, hipStream_t s, bool values) {
     self_loops_impl(false, n, nnz, row_ptr, col_ind, val, row_ptr_out, col_out, val_out, nullptr,
-                    nullptr, ws, ws_bytes, s);
+                    nullptr, ws, ws_bytes, s, values);
 }
 
 void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
               const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
-              float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s) {
+              float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s,
+              bool values) {
     self_loops_impl(true, n, nnz, row_ptr, col_ind, val, row_ptr_out, col_out, val_out, deg_out,
-                    dis_out, ws, ws_bytes, s);
+                    dis_out, ws, ws_bytes, s, values);
 }
 
 size_t self_loops_workspace(int64_t n) { return self_loops_ws(n); }
@@ -1178,7 +1190,8 @@ int tg_add_self_loops(int64_t n, int64_t nnz, const int32_t* row_ptr, const int3
                       tg_stream_t stream) {
     return tg::guard([&] {
         tg::add_self_loops(n, nnz, row_ptr, col_ind, val, row_ptr_out, col_ind_out, val_out,
-                           workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                           workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                           true);
     });
 }
 
@@ -1188,7 +1201,8 @@ int tg_gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* c
                 tg_stream_t stream) {
     return tg::guard([&] {
         tg::gcn_norm(n, nnz, row_ptr, col_ind, val, row_ptr_out, col_ind_out, val_out, deg_out,
-                     dis_out, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                     dis_out, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                     true);
     });
 }
 

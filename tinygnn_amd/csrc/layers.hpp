@@ -24,12 +24,15 @@ void edge_list_to_csr(int64_t n_nodes, int64_t n_edges, const int32_t* src, cons
 size_t edge_list_to_csr_ws(int64_t n_nodes);
 void csr_validate(int64_t n_rows, int64_t n_cols, int64_t nnz, const int32_t* row_ptr,
                   const int32_t* col_ind, hipStream_t s);
+// values = false: the structure of A + I alone (row_ptr_out, col_out; val_out
+// is ignored), and for gcn_norm deg_out / dis_out.
 void add_self_loops(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
                     const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
-                    void* ws, size_t ws_bytes, hipStream_t s);
+                    void* ws, size_t ws_bytes, hipStream_t s, bool values = true);
 void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col_ind,
               const float* val, int32_t* row_ptr_out, int32_t* col_out, float* val_out,
-              float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s);
+              float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s,
+              bool values = true);
 size_t self_loops_workspace(int64_t n);
 
 // sage.hip

@@ -102,6 +102,9 @@ struct tg_model_s {
     // fast precision, GCN present: every value of A + I is 1 (the blocked
     // GCN aggregation is factored, its blocked copy carries no values)
     bool unit_sl = false;
+    // sl_v holds A + I's values (GCN present, unless only the factored
+    // blocked path reads A + I)
+    bool sl_values = false;
     DeviceBuffer flag;
     tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
@@ -139,15 +142,13 @@ struct tg_model_s {
 namespace tg {
 namespace {
 
-// *flag = 0 if some value of A is not exactly 1, or if A has a diagonal
-// entry (then A + I has fewer than nnz + n entries); *flag is 1 before.
+// *flag = 0 if some value of A is not exactly 1 (*flag is 1 before).
 // VEC = 4: 128-bit reads (v 16-byte aligned), the last nnz % 4 values on
 // the first thread.
 template <int VEC>
 __global__ __launch_bounds__(256) void unit_values_kernel(const float* __restrict__ v,
                                                           int64_t nnz,
-                                                          const int32_t* __restrict__ sl_rp,
-                                                          int64_t n, int32_t* __restrict__ flag) {
+                                                          int32_t* __restrict__ flag) {
     bool bad = false;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -162,7 +163,6 @@ __global__ __launch_bounds__(256) void unit_values_kernel(const float* __restric
     } else {
         for (int64_t i = tid; i < nnz; i += stride) bad |= v[i] != 1.0f;
     }
-    if (tid == 0) bad |= sl_rp[n] != nnz + n;
     if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) *flag = 0;  // one store per wave
 }
 
@@ -307,7 +307,10 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
                       m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision;
-    if (mode == TG_FORWARD_CACHED && same) {
+    // a new blocking setting keeps the cached state, unless A + I's values
+    // were skipped for the factored path (an unblocked GCN needs them)
+    const bool values_ok = m.sl_values || !m.need_norm();
+    if (mode == TG_FORWARD_CACHED && same && (values_ok || m.built_block_rows == m.block_rows)) {
         // a cached call after a reference-mode one (or a new blocking
         // setting) adds the blocked copies to the state it reuses
         if (m.built_block_rows != m.block_rows) prepare_blocked(m, n, nnz, rp, ci, s);
@@ -326,43 +329,69 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     } else {
         m.plan_raw.reset();
     }
+    m.unit_sl = false;
+    m.sl_values = false;
     if (m.need_norm() || m.need_sl()) {
         require(nnz + n < (int64_t(1) << 31), "Model::forward: nnz + n must be < 2^31");
         m.sl_rp.reserve((n + 1) * sizeof(int32_t));
         m.sl_ci.reserve((nnz + n) * sizeof(int32_t));
         m.sl_v.reserve((nnz + n) * sizeof(float));
         m.work.reserve(self_loops_workspace(n));
+        m.flag.reserve(sizeof(int32_t));
+        m.flag_host.reserve(2 * sizeof(int32_t));
+        int32_t* host = m.flag_host.as<int32_t>();
+        // fast precision: all of A's values exactly 1?  Then, with no
+        // diagonal in A, every value of A + I is 1 and a blocked GCN
+        // aggregation is factored (it reads no values)
+        bool unit_v = false;
+        if (m.need_norm() && m.precision != TG_PRECISION_EXACT) {
+            fill_i32(m.flag.as<int32_t>(), 1, 1, s);
+            const int64_t blocks =
+                std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 1024), 1), 4096);
+            if (reinterpret_cast<uintptr_t>(v) % 16 == 0)
+                unit_values_kernel<4><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+                    v, nnz, m.flag.as<int32_t>());
+            else
+                unit_values_kernel<1><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+                    v, nnz, m.flag.as<int32_t>());
+            TG_LAUNCH_CHECK();
+            TG_HIP(hipMemcpyAsync(host, m.flag.as<int32_t>(), sizeof(int32_t),
+                                  hipMemcpyDeviceToHost, s));
+            TG_HIP(hipStreamSynchronize(s));
+            unit_v = host[0] == 1;
+        }
+        // A + I's values: GAT reads the structure alone; GCN needs the
+        // normalised values unless its aggregation will run factored (the
+        // blocking prepare_blocked resolves for a unit A + I)
+        const int gc_unit = m.need_sl() ? 64 : 32;
+        const bool will_block = resolve_block_rows(m.block_rows, n, nnz + n, gc_unit) > 0;
+        m.sl_values = m.need_norm() && !(unit_v && will_block);
         if (m.need_norm()) {
             m.dis.reserve(n * sizeof(float));
             gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                      m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(), m.work.size(),
-                     s);
+                     s, m.sl_values);
         } else {
             add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                           m.sl_v.as<float>(), m.work.get(), m.work.size(), s);
+                           m.sl_v.as<float>(), m.work.get(), m.work.size(), s, false);
+        }
+        if (unit_v) {
+            // no diagonal in A: A + I has nnz + n entries
+            TG_HIP(hipMemcpyAsync(host + 1, m.sl_rp.as<int32_t>() + n, sizeof(int32_t),
+                                  hipMemcpyDeviceToHost, s));
+            TG_HIP(hipStreamSynchronize(s));
+            m.unit_sl = host[1] == nnz + n;
+            if (!m.unit_sl && !m.sl_values) {  // a diagonal of A: A + I holds a 2
+                m.sl_values = true;
+                gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                         m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(),
+                         m.work.size(), s, true);
+            }
         }
         if (!m.plan_sl) m.plan_sl = std::make_unique<tg_spmm_plan_s>();
         build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, chunk, s);
     } else {
         m.plan_sl.reset();
-    }
-    m.unit_sl = false;
-    if (m.need_norm() && m.precision != TG_PRECISION_EXACT) {
-        m.flag.reserve(sizeof(int32_t));
-        m.flag_host.reserve(sizeof(int32_t));
-        fill_i32(m.flag.as<int32_t>(), 1, 1, s);
-        const int64_t blocks = std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 1024), 1), 4096);
-        if (reinterpret_cast<uintptr_t>(v) % 16 == 0)
-            unit_values_kernel<4><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
-                v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
-        else
-            unit_values_kernel<1><<<static_cast<unsigned>(blocks), 256, 0, s>>>(
-                v, nnz, m.sl_rp.as<int32_t>(), n, m.flag.as<int32_t>());
-        TG_LAUNCH_CHECK();
-        TG_HIP(hipMemcpyAsync(m.flag_host.as<int32_t>(), m.flag.as<int32_t>(), sizeof(int32_t),
-                              hipMemcpyDeviceToHost, s));
-        TG_HIP(hipStreamSynchronize(s));
-        m.unit_sl = *m.flag_host.as<int32_t>() == 1;
     }
     m.have_cache = true;
     m.built_precision = m.precision;
