@@ -108,6 +108,7 @@ struct tg_model_s {
     DeviceBuffer flag;
     tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
+    bool plan_sl_built = false;  // plan_sl holds A + I's row plan (ensure_plan_sl)
     // column-blocked copies for the large aggregations (fast precision):
     // A_norm for GCN, A's structure for SAGE-mean
     std::unique_ptr<tg::BlockedCSR> blk_sl, blk_raw;
@@ -303,6 +304,18 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     }
 }
 
+// A + I's unblocked row plan, where something reads it: GAT (its statistics
+// run over the plan's chunks) and an unblocked GCN aggregation.  A blocked
+// GCN runs on the block plans alone (config-E reference-semantics GCN: one
+// plan build and its synchronisation fewer per call).
+void ensure_plan_sl(tg_model_s& m, int64_t n, int64_t nnz, hipStream_t s) {
+    const bool needed = m.need_sl() || (m.need_norm() && !m.blk_sl);
+    if (!needed || m.plan_sl_built) return;
+    const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
+    build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.max_wide(), chunk, s);
+    m.plan_sl_built = true;
+}
+
 void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
@@ -313,7 +326,10 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     if (mode == TG_FORWARD_CACHED && same && (values_ok || m.built_block_rows == m.block_rows)) {
         // a cached call after a reference-mode one (or a new blocking
         // setting) adds the blocked copies to the state it reuses
-        if (m.built_block_rows != m.block_rows) prepare_blocked(m, n, nnz, rp, ci, s);
+        if (m.built_block_rows != m.block_rows) {
+            prepare_blocked(m, n, nnz, rp, ci, s);
+            if (m.need_norm() || m.need_sl()) ensure_plan_sl(m, n, nnz, s);
+        }
         return;
     }
     m.have_cache = false;
@@ -388,8 +404,9 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                          m.work.size(), s, true);
             }
         }
+        // A + I's row plan is built by ensure_plan_sl, once the blocking is known
         if (!m.plan_sl) m.plan_sl = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), maxf, chunk, s);
+        m.plan_sl_built = false;
     } else {
         m.plan_sl.reset();
     }
@@ -405,6 +422,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     // unblocked and 14.8 / 12.0 / 17.3 ms blocked with everything rebuilt in
     // place (the block plans counted before one synchronisation)
     prepare_blocked(m, n, nnz, rp, ci, s);
+    if (m.need_norm() || m.need_sl()) ensure_plan_sl(m, n, nnz, s);
 }
 
 void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int32_t* ci,
