@@ -420,6 +420,16 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     assert_close(outs[100], outs[0], what="blocked vs unblocked")
     if variant == "unit":  # the factored sums round differently from the unblocked ones
         assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
+    # the values at an address off 16-byte alignment (the unit check's
+    # entry-wise reads): the same decision, the same bits
+    vbuf = gpu.zeros(g.nnz + 1, dtype=gpu.float32, device="cuda")
+    vbuf[1:] = da.val
+    da_off = tg.DeviceCSR(n, n, da.row_ptr, da.col_ind, vbuf[1:])
+    assert da_off.val.data_ptr() % 16 != 0
+    m = tg.Model.from_spec(spec, w)
+    m.set_blocking(100)
+    got = m.forward(da_off, xt).cpu().numpy()
+    np.testing.assert_array_equal(bits(got), bits(outs[100]), err_msg="unaligned values")
     # a new blocking setting between cached calls (the factored path keeps no
     # normalised values; turning blocking off must bring them back)
     m = tg.Model.from_spec(spec, w)
