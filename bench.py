@@ -126,21 +126,12 @@ class StreamTimer:
 
 
 def build_graph_gpu(torch, tg, n, n_edges, seed, dev):
-    """Seeded power-law edge list (degrees on the host, destinations and a
-    random edge order drawn on the GPU), then the device CSR build
-    (edge_list_to_csr).  Returns the device CSR and the build time in ms."""
+    """Seeded power-law edge list drawn on the GPU (synth.powerlaw_edges_device),
+    then the device CSR build (edge_list_to_csr).  Returns the device CSR and
+    the build time in ms."""
     from tinygnn_amd import synth
 
-    deg = synth.powerlaw_degrees(n, n_edges, alpha=2.1, dmax=20000, seed=seed)
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed + 1)
-    src = torch.repeat_interleave(torch.arange(n, dtype=torch.int32, device=dev),
-                                  torch.from_numpy(deg.astype(np.int64)).to(dev))
-    dst = torch.randint(0, n - 1, (n_edges,), generator=g, device=dev, dtype=torch.int32)
-    dst += (dst >= src).to(torch.int32)  # no self-loops in the raw graph
-    perm = torch.randperm(n_edges, generator=g, device=dev)
-    src, dst = src[perm].contiguous(), dst[perm].contiguous()
-    del perm
+    src, dst = synth.powerlaw_edges_device(torch, n, n_edges, seed, dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     a = tg.edge_list_to_csr(src, dst, n)

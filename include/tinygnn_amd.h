@@ -255,9 +255,18 @@ int tg_gat_aggregate(tg_spmm_plan_t plan, int64_t n, int64_t heads, int64_t f,
  *   tg_model_forward      <- Model::forward (:359-439).  adjacency: raw CSR
  *     (no self-loops) on the device; x: [n x f_in] device features; out:
  *     [n x out_cols] device.  mode TG_FORWARD_REFERENCE recomputes gcn_norm /
- *     add_self_loops on every call as the reference does; TG_FORWARD_CACHED
- *     reuses them (and the SpMM plans) while the adjacency pointers and
- *     sizes are unchanged.  The model owns its intermediate buffers.
+ *     add_self_loops on every call as the reference does (src/model.cpp:
+ *     373-381); TG_FORWARD_CACHED reuses them (and the SpMM plans and
+ *     blocked copies) while the adjacency pointers, sizes, the precision and
+ *     the layer list are unchanged.  The cache cannot see the adjacency's
+ *     contents: a caller that edits row_ptr / col_ind / val in place, or
+ *     frees them and passes new arrays that may land at the same addresses,
+ *     must call tg_model_invalidate first (or pass TG_FORWARD_REFERENCE,
+ *     which also refreshes the cache).  The C++ API (tinygnn::Model) and the
+ *     Python front end do this from the tensors' versions.  The model owns
+ *     its intermediate buffers.
+ *   tg_model_invalidate   forgets the cached adjacency state (no counterpart
+ *     in the reference, which keeps none); the next forward recomputes it.
  * ------------------------------------------------------------------------ */
 typedef struct tg_model_s* tg_model_t;
 enum { TG_FORWARD_REFERENCE = 0, TG_FORWARD_CACHED = 1 };
@@ -313,6 +322,7 @@ int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
                      const int32_t* row_ptr, const int32_t* col_ind, const float* val,
                      int64_t f_in, const float* x, float* out, int mode,
                      tg_stream_t stream);
+int tg_model_invalidate(tg_model_t model);
 
 /* ------------------------------------------------------------------------
  * CSV ingestion -- replaces GraphLoader::parse_edges / parse_features and

@@ -88,6 +88,7 @@ class _Restate:
             "or_add_self_loops": (None, [_i64, _p, _p, _p, _p, _p, _p]),
             "or_gcn_norm": (None, [_i64, _p, _p, _p, _p, _p, _p, _p, _p]),
             "or_spmm": (None, [_i64, _i64, _p, _p, _p, _p, _p]),
+            "or_spmm_rows_f64": (None, [_i64, _p, _i64, _p, _p, _p, _p, _p, _p]),
             "or_matmul": (None, [_i64, _i64, _i64, _p, _p, _p]),
             "or_relu": (None, [_i64, _p]),
             "or_leaky_relu": (None, [_i64, _p, _f32]),
@@ -197,6 +198,18 @@ class _Restate:
         self.L.or_spmm(a.n_rows, f, _ptr(a.row_ptr), _ptr(a.col_ind), _ptr(a.val),
                        _ptr(b), _ptr(c))
         return c
+
+    def spmm_rows_f64(self, a: CSR, b, rows):
+        """Checker (not a restatement): float64 ``(exact, absum)`` of the
+        product's rows ``rows``: sum of val*B[col] and of |val*B[col]|."""
+        b = _f(b)
+        rows = _i(rows)
+        f = b.shape[1]
+        exact = np.zeros((rows.shape[0], f), np.float64)
+        absum = np.zeros_like(exact)
+        self.L.or_spmm_rows_f64(rows.shape[0], _ptr(rows), f, _ptr(a.row_ptr), _ptr(a.col_ind),
+                                _ptr(a.val), _ptr(b), _ptr(exact), _ptr(absum))
+        return exact, absum
 
     def matmul(self, a, b) -> np.ndarray:
         a, b = _f(a), _f(b)
@@ -551,6 +564,18 @@ class _Reference:
         ta, tb = self.csr(a), self.dense(b)
         self._check(self.L.ref_spmm(ta.h, tb.h, _ptr(out)))
         return out
+
+    def spmm_rows_f64(self, a: CSR, b, rows):
+        """Checker (not a restatement): float64 ``(exact, absum)`` of the
+        product's rows ``rows``: sum of val*B[col] and of |val*B[col]|."""
+        b = _f(b)
+        rows = _i(rows)
+        f = b.shape[1]
+        exact = np.zeros((rows.shape[0], f), np.float64)
+        absum = np.zeros_like(exact)
+        self.L.or_spmm_rows_f64(rows.shape[0], _ptr(rows), f, _ptr(a.row_ptr), _ptr(a.col_ind),
+                                _ptr(a.val), _ptr(b), _ptr(exact), _ptr(absum))
+        return exact, absum
 
     def matmul(self, a, b) -> np.ndarray:
         a, b = _f(a), _f(b)

@@ -220,6 +220,35 @@ void or_spmm(int64_t m, int64_t f, const int32_t* rp, const int32_t* ci,
 }
 
 /* ------------------------------------------------------------------------
+ * Checker, not a restatement: the exact-in-double product of selected rows,
+ * exact[r] = sum val * B[col] and absum[r] = sum |val * B[col]| over row
+ * rows[r]'s nonzeros, in float64.  Each term is exact in double (a product
+ * of two floats), so |fl32 sum - exact| <= k 2^-24 absum (+ the float64
+ * rounding, far smaller) bounds any float32 summation order of k roundings:
+ * the bound that regrouped (split-row) sums are held to.
+ * ------------------------------------------------------------------------ */
+void or_spmm_rows_f64(int64_t n_sel, const int32_t* rows, int64_t f, const int32_t* rp,
+                      const int32_t* ci, const float* av, const float* b, double* exact,
+                      double* absum) {
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t r = 0; r < n_sel; ++r) {
+        const int64_t i = rows[r];
+        double* e = exact + r * f;
+        double* s = absum + r * f;
+        for (int64_t j = 0; j < f; ++j) e[j] = s[j] = 0.0;
+        for (int32_t nz = rp[i]; nz < rp[i + 1]; ++nz) {
+            const double a = av[nz];
+            const float* brow = b + (int64_t)ci[nz] * f;
+            for (int64_t j = 0; j < f; ++j) {
+                const double t = a * (double)brow[j];
+                e[j] += t;
+                s[j] += fabs(t);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------
  * ops.cpp:70-162  matmul, (i,k,j) order, C[i,j] = fma(A[i,k], B[k,j], C)
  * with k ascending from 0 and C starting at 0 (:106, :120-159).
  * ------------------------------------------------------------------------ */

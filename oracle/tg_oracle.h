@@ -52,6 +52,10 @@ void or_gcn_norm(int64_t n, const int32_t* rp, const int32_t* ci,
 /* ops.cpp:198-297 -- C[M x F] = A_csr[M x K] * B[K x F]. */
 void or_spmm(int64_t m, int64_t f, const int32_t* rp, const int32_t* ci,
              const float* av, const float* b, float* c);
+/* checker: float64 products of selected rows and their sums of |terms| */
+void or_spmm_rows_f64(int64_t n_sel, const int32_t* rows, int64_t f, const int32_t* rp,
+                      const int32_t* ci, const float* av, const float* b, double* exact,
+                      double* absum);
 
 /* ops.cpp:70-162 -- C[M x N] = A[M x K] * B[K x N], (i,k,j) order. */
 void or_matmul(int64_t m, int64_t k, int64_t n, const float* a,

@@ -242,6 +242,41 @@ static void test_model() {
     Tensor ref3 = l1.forward(gcn_norm(A), l0.forward(gcn_norm(A), X));
     CHECK(out3.data() == ref3.data());
     CHECK(out3.data() != out.data());
+    // layers added after a forward, on the same adjacency at the same
+    // version: the derived state must follow the new layer list (A's row
+    // plan for SAGE, A + I for GAT); the reference's forward keeps no state,
+    // so this order is legal there (model.cpp:359-439)
+    CHECK(m.add_sage_layer(3, 4) == 2);
+    CHECK(m.add_gat_layer(4, 2) == 3);
+    std::vector<float> wn(12), ws(12), b2(4), w3(8);
+    for (size_t i = 0; i < wn.size(); ++i) wn[i] = std::sin(0.3f * i + 0.1f);
+    for (size_t i = 0; i < ws.size(); ++i) ws[i] = std::cos(0.2f * i) * 0.7f;
+    for (size_t i = 0; i < b2.size(); ++i) b2[i] = 0.05f * i - 0.1f;
+    for (size_t i = 0; i < w3.size(); ++i) w3[i] = std::sin(0.5f * i) * 0.6f;
+    wf.tensors["layer2.weight_neigh"] = Tensor::dense(3, 4, wn);
+    wf.tensors["layer2.weight_self"] = Tensor::dense(3, 4, ws);
+    wf.tensors["layer2.bias"] = Tensor::dense(1, 4, b2);
+    wf.tensors["layer3.head0.weight"] = Tensor::dense(4, 2, w3);
+    wf.tensors["layer3.head0.attn_left"] = Tensor::dense(1, 2, {0.3f, -0.4f});
+    wf.tensors["layer3.head0.attn_right"] = Tensor::dense(1, 2, {0.2f, 0.1f});
+    wf.tensors["layer3.head0.bias"] = Tensor::dense(1, 2, {0.01f, -0.02f});
+    m.load_weights(wf);
+    Tensor out4 = m.forward(A, X);
+    SAGELayer l2(3, 4);
+    l2.set_weight_neigh(Tensor::dense(3, 4, wn));
+    l2.set_weight_self(Tensor::dense(3, 4, ws));
+    l2.set_bias(Tensor::dense(1, 4, b2));
+    GATLayer l3(4, 2);
+    l3.set_weight(Tensor::dense(4, 2, w3));
+    l3.set_attn_left(Tensor::dense(1, 2, {0.3f, -0.4f}));
+    l3.set_attn_right(Tensor::dense(1, 2, {0.2f, 0.1f}));
+    l3.set_bias(Tensor::dense(1, 2, {0.01f, -0.02f}));
+    Tensor ref4 = l3.forward(add_self_loops(A), l2.forward(A, ref3));
+    CHECK(out4.rows() == 40 && out4.cols() == 2);
+    for (size_t i = 0; i < ref4.data().size(); ++i)
+        CHECK_NEAR(out4.data()[i], ref4.data()[i], 1e-5 + 1e-4 * std::fabs(ref4.data()[i]));
+    Tensor out5 = m.forward(A, X);  // cached again with the four layers
+    CHECK(out5.data() == out4.data());
     // multi-head GAT concat + ELU, then a 1-head GAT
     Model gm;
     gm.add_gat_layer(5, 4, 2, true, 0.2f, true, Activation::None, Model::InterActivation::ELU);

@@ -1,0 +1,222 @@
+"""Full-size parity at the BASELINE configurations D and E (marked gpu, slow).
+
+The inputs are the benchmark's own seeded workloads (``bench.py`` through
+``tinygnn_amd.synth``): the edge lists are drawn on the GPU, copied to the
+host, and built into CSR by the device and by the oracle independently.
+
+Config D -- 1,000,000 nodes, 50,000,000 power-law edges:
+  * ``edge_list_to_csr`` bit-exact (graph_loader.cpp:211-281);
+  * SpMM at F = 32, 128, 512 (ops.cpp:198-297): rows of one plan chunk
+    bit-identical to the oracle's fma chain; rows split into chunks within
+    k 2^-24 sum|terms| of the float64 product (k = roundings per element),
+    the bound the oracle's own sequential sum obeys too.
+
+Config E -- 232,965 nodes, 114,615,892 edges, 602 N(0,1) features:
+  * CSR, ``add_self_loops`` and ``gcn_norm`` (values, deg, 1/sqrt(deg))
+    bit-exact (layers.cpp:71-208);
+  * the raw ``Model::forward`` outputs (model.cpp:359-439, before the caller's
+    log_softmax) of 2-layer GCN, SAGE-mean and GAT (4 x 64 heads, ELU, then
+    1 head), in both forward modes, within |err| <= 1e-5 + 1e-4 |ref|;
+  * exact precision: GCN and SAGE byte-identical to the oracle; GAT within
+    the tolerance; the per-node argmax identical everywhere;
+  * fast precision: the per-node argmax identical except at near-ties, nodes
+    whose two largest reference outputs are closer than the fast path's
+    largest error on that node (their order is decided by rounding).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import bits
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow, pytest.mark.timeout(600)]
+
+D_SEED = 2101          # bench.py DEFAULT_SEED: config D graph, values seed+2, B seed+3
+E_SEED = D_SEED + 10   # bench.py run_forward_e: graph seed, features seed+1, weights seed+10
+TOL_ABS, TOL_REL = 1e-5, 1e-4
+
+
+def say(msg):
+    print(f"[fullsize] {msg}", file=sys.stderr, flush=True)
+
+
+def _graph(gpu, restate, n, n_edges, seed):
+    """(device CSR, oracle CSR) of the benchmark's seeded edge list."""
+    import tinygnn_amd as tg
+    from tinygnn_amd import synth
+    dev = gpu.device("cuda:0")
+    src, dst = synth.powerlaw_edges_device(gpu, n, n_edges, seed, dev)
+    src_h, dst_h = src.cpu().numpy(), dst.cpu().numpy()
+    adj = tg.edge_list_to_csr(src, dst, n)
+    del src, dst
+    a = restate.edge_list_to_csr(src_h, dst_h, n)
+    return adj, a
+
+
+def _assert_csr_equal(dev_csr, a, what):
+    rp, ci, v = dev_csr.to_numpy()
+    np.testing.assert_array_equal(rp, a.row_ptr, err_msg=what + " row_ptr")
+    np.testing.assert_array_equal(ci, a.col_ind, err_msg=what + " col_ind")
+    np.testing.assert_array_equal(bits(v), bits(a.val), err_msg=what + " val")
+
+
+# ---------------------------------------------------------------------------
+# Config D
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def config_d(gpu, restate):
+    """The unit-valued CSR of the 50M-edge list (device, oracle), and the
+    same structure with the benchmark's values, uniform (0, 1] drawn on the
+    device."""
+    import tinygnn_amd as tg
+    from tinygnn_amd import synth
+    say("config D: building the graph")
+    adj, a = _graph(gpu, restate, synth.D_NODES, synth.D_EDGES, D_SEED)
+    dev = gpu.device("cuda:0")
+    gv = gpu.Generator(device=dev)
+    gv.manual_seed(D_SEED + 2)
+    val = 1.0 - gpu.rand(adj.nnz, generator=gv, device=dev)
+    wadj = tg.DeviceCSR(adj.n_rows, adj.n_cols, adj.row_ptr, adj.col_ind, val)
+    wa = type(a)(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, val.cpu().numpy())
+    say(f"config D: nnz {a.nnz}, max degree {int(np.diff(a.row_ptr).max())}")
+    return adj, a, wadj, wa
+
+
+def test_config_d_csr_bitexact(config_d):
+    adj, a, _, _ = config_d
+    _assert_csr_equal(adj, a, "config D edge_list_to_csr")
+
+
+@pytest.mark.parametrize("f", [32, 128, 512])
+def test_config_d_spmm(gpu, restate, config_d, f):
+    import tinygnn_amd as tg
+    from tinygnn_amd import synth
+    _, _, adj, a = config_d
+    dev = gpu.device("cuda:0")
+    m = synth.D_NODES
+    gb = gpu.Generator(device=dev)
+    gb.manual_seed(D_SEED + 3 + f)
+    b = gpu.randn((m, f), generator=gb, device=dev, dtype=gpu.float32)
+    plan = tg.SpmmPlan(adj.row_ptr, m, adj.nnz, f)
+    info = plan.info()
+    got = tg.spmm(adj, b, plan=plan).cpu().numpy()
+    b_h = b.cpu().numpy()
+    del b
+    want = restate.spmm(a, b_h)
+    deg = np.diff(a.row_ptr)
+    # the plan's chunk is 1,024 nonzeros: longer rows are summed from
+    # per-chunk partials (a regrouped sum)
+    split = deg > 1024
+    assert info["n_split_rows"] == int(split.sum())
+    single = ~split
+    np.testing.assert_array_equal(bits(got[single]), bits(want[single]),
+                                  err_msg=f"F={f}: unsplit rows must be bit-identical")
+    rows = np.flatnonzero(split).astype(np.int32)
+    exact, absum = restate.spmm_rows_f64(a, b_h, rows)
+    k = (deg[rows] + np.ceil(deg[rows] / 1024) + 1)[:, None]
+    bound = k * 2.0 ** -24 * absum * 1.01 + 1e-30
+    for name, x in (("gpu", got[rows]), ("oracle", want[rows])):
+        err = np.abs(x.astype(np.float64) - exact)
+        assert (err <= bound).all(), (f"F={f}", name, float((err / bound).max()))
+    d = np.abs(got[rows].astype(np.float64) - want[rows])
+    inside = d <= TOL_ABS + TOL_REL * np.abs(want[rows].astype(np.float64))
+    say(f"config D F={f}: {len(rows)} split rows ({int(deg[rows].sum())} nnz); "
+        f"{inside.mean() * 100:.3f}% of their elements within 1e-5 + 1e-4|ref| of the "
+        f"oracle's sequential sum; max |gpu - f64| / bound "
+        f"{float((np.abs(got[rows] - exact) / bound).max()):.3f}")
+
+
+# ---------------------------------------------------------------------------
+# Config E
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def config_e(gpu, restate):
+    from tinygnn_amd import synth
+    say("config E: building the graph")
+    adj, a = _graph(gpu, restate, synth.E_NODES, synth.E_EDGES, E_SEED)
+    rng = np.random.default_rng(E_SEED + 1)
+    x_h = rng.standard_normal((synth.E_NODES, synth.E_FEATURES), dtype=np.float32)
+    x = gpu.from_numpy(x_h).cuda()
+    say(f"config E: nnz {a.nnz}")
+    return adj, a, x, x_h
+
+
+def test_config_e_preprocessing_bitexact(gpu, restate, config_e):
+    import tinygnn_amd as tg
+    adj, a, _, _ = config_e
+    _assert_csr_equal(adj, a, "config E edge_list_to_csr")
+    _assert_csr_equal(tg.add_self_loops(adj), restate.add_self_loops(a), "add_self_loops")
+    got, gdeg, gdis = tg.gcn_norm(adj, with_degrees=True)
+    want, wdeg, wdis = restate.gcn_norm(a, with_degrees=True)
+    _assert_csr_equal(got, want, "gcn_norm")
+    np.testing.assert_array_equal(bits(gdeg.cpu().numpy()), bits(wdeg), err_msg="deg")
+    np.testing.assert_array_equal(bits(gdis.cpu().numpy()), bits(wdis), err_msg="dis")
+    assert want.nnz == 114_848_857
+
+
+def _spec(name):
+    from tinygnn_amd import synth
+    return {"gcn": synth.spec_gcn(synth.E_FEATURES, 256, synth.E_CLASSES),
+            "sage": synth.spec_sage(synth.E_FEATURES, 256, synth.E_CLASSES),
+            "gat": synth.spec_gat(synth.E_FEATURES, 64, 4, synth.E_CLASSES)}[name]
+
+
+def _within_tolerance(got, want, what):
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    err = np.abs(g - w)
+    bad = err > TOL_ABS + TOL_REL * np.abs(w)
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance, max abs "
+                           f"err {float(err.max()):.3g}")
+    return err
+
+
+def _argmax_check(got, want, err, strict, what):
+    """Per-node argmax equality; with strict=False a node may differ only
+    when the reference's top-2 gap is within that node's largest error."""
+    ga, wa = got.argmax(1), want.argmax(1)
+    diff = np.flatnonzero(ga != wa)
+    top2 = np.sort(want, axis=1)[:, -2:]
+    gap = (top2[:, 1] - top2[:, 0]).astype(np.float64)
+    tie = gap <= 2 * err.max(axis=1)
+    if strict:
+        assert diff.size == 0, f"{what}: argmax differs on {diff.size} nodes"
+    else:
+        assert tie[diff].all(), (f"{what}: argmax differs on {int((~tie[diff]).sum())} nodes "
+                                 f"that are not near-ties")
+    return int(diff.size), int(tie.sum())
+
+
+@pytest.mark.parametrize("model", ["gcn", "sage", "gat"])
+def test_config_e_forward(gpu, restate, config_e, model):
+    import tinygnn_amd as tg
+    from tinygnn_amd import synth
+    adj, a, x, x_h = config_e
+    spec = _spec(model)
+    w = synth.model_weights(spec, seed=E_SEED + 10)
+    say(f"config E {model}: oracle forward")
+    want = restate.model_forward(spec, w, a, x_h)
+    m = tg.Model.from_spec(spec, w)
+    y = gpu.empty((synth.E_NODES, m.output_cols()), device="cuda:0")
+    for mode, mname in ((tg.FORWARD_REFERENCE, "reference semantics"),
+                        (tg.FORWARD_CACHED, "cached")):
+        m.forward(adj, x, mode=mode, out=y)
+        if mode == tg.FORWARD_CACHED:  # the second cached call reuses the state
+            m.forward(adj, x, mode=mode, out=y)
+        got = y.cpu().numpy()
+        what = f"{model} fast, {mname}"
+        err = _within_tolerance(got, want, what)
+        n_diff, n_tie = _argmax_check(got, want, err, strict=False, what=what)
+        say(f"{what}: max abs err {float(err.max()):.3g}, argmax differs on {n_diff} nodes "
+            f"(near-ties {n_tie}), bit-identical "
+            f"{float((bits(got) == bits(want)).mean()) * 100:.2f}%")
+    m.set_precision(tg.PRECISION_EXACT)
+    m.forward(adj, x, mode=tg.FORWARD_CACHED, out=y)
+    got = y.cpu().numpy()
+    what = f"{model} exact"
+    if model in ("gcn", "sage"):
+        np.testing.assert_array_equal(bits(got), bits(want), err_msg=what)
+    err = _within_tolerance(got, want, what)
+    _argmax_check(got, want, err, strict=True, what=what)
+    say(f"{what}: max abs err {float(err.max()):.3g}, bit-identical "
+        f"{float((bits(got) == bits(want)).mean()) * 100:.2f}%")

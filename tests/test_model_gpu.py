@@ -526,3 +526,63 @@ def test_blocked_mixed_stack(gpu, restate, precision):
         np.testing.assert_array_equal(bits(outs[63]), bits(outs[0]))
     else:
         assert (bits(outs[63]) != bits(outs[0])).any(), "blocking had no effect"
+
+
+def test_cached_forward_follows_adjacency(gpu, restate):
+    """FORWARD_CACHED never reuses state derived from another adjacency: after
+    an in-place edit of the values, after new column indices written into the
+    same tensor (the same device addresses), after a write torch does not
+    see followed by invalidate(), and after layers are added to the model.
+    Every forward must equal the oracle's, which recomputes per call as the
+    reference does (model.cpp:373-381)."""
+    import tinygnn_amd as tg
+    from tinygnn_amd import _lib
+    rng = np.random.default_rng(31)
+    n, f = 1500, 24
+    spec = synth.spec_gcn(f, 16, 5)
+    w = synth.model_weights(spec, seed=2)
+    x = rng.standard_normal((n, f)).astype(np.float32)
+    xd = _t(gpu, x)
+    a = random_csr(rng, n, n, avg_deg=12, max_deg=600, weighted=False)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    m = tg.Model.from_spec(spec, w)
+
+    def check(what, spec=spec, w=w):
+        got = m.forward(da, xd, mode=tg.FORWARD_CACHED).cpu().numpy()
+        assert_close(got, restate.model_forward(spec, w, a, x), what=what)
+
+    check("first forward")
+    check("second forward (cached)")
+    # in-place edit of the values through torch (bumps the tensor's version)
+    da.val.mul_(0.5)
+    a.val *= np.float32(0.5)
+    check("after an in-place edit of val")
+    # a different graph of the same size written into the same tensors
+    for i in range(n):
+        s, e = a.row_ptr[i], a.row_ptr[i + 1]
+        a.col_ind[s:e] = np.sort(rng.integers(0, n, e - s)).astype(np.int32)
+    ptr = da.col_ind.data_ptr()
+    da.col_ind.copy_(gpu.from_numpy(a.col_ind))
+    assert da.col_ind.data_ptr() == ptr
+    check("after new column indices at the same address")
+    # a write torch does not track (a C-ABI op on the raw pointer), then
+    # invalidate(): the values go negative, then ReLU zeroes them
+    da.val.neg_()
+    m.forward(da, xd, mode=tg.FORWARD_CACHED)
+    _lib.lib.check(_lib.lib.tg_relu(da.nnz, da.val.data_ptr(), tg.stream_handle()))
+    gpu.cuda.synchronize()
+    a.val[:] = 0.0
+    m.invalidate()
+    check("after a raw write and invalidate()")
+    # layers added after a forward on the same adjacency (A's plan for SAGE,
+    # A + I for GAT were never built for the two-layer GCN)
+    m.add_sage_layer(5, 6)
+    m.add_gat_layer(6, 3, num_heads=2, concat=True)
+    spec2 = spec + [dict(type="sage", **{"in": 5}, out=6, agg=0, act=1, post=0),
+                    dict(type="gat", **{"in": 6}, out=3, heads=2, concat=True, slope=0.2,
+                         act=0, post=0)]
+    a.val[:] = rng.random(a.nnz).astype(np.float32)
+    da.val.copy_(gpu.from_numpy(a.val))
+    w2 = synth.model_weights(spec2, seed=4)
+    m.load_weights(w2)
+    check("after layers were added", spec2, w2)

@@ -172,6 +172,26 @@ def test_math_spmm_matches_dense_product(restate):
     assert (np.abs(got - exact) <= bound).all()
 
 
+def test_checker_spmm_rows_f64(restate):
+    """The full-size tests' float64 checker against per-term brute force on
+    selected rows (duplicate columns with values of either sign included,
+    so sum|terms| differs from |A| @ |B|), and the float32 spmm against the
+    bound it yields."""
+    rng = np.random.default_rng(5)
+    a = random_csr(rng, 80, 30, avg_deg=14, max_deg=60, empty_frac=0.1)
+    b = rng.standard_normal((30, 9)).astype(np.float32)
+    rows = np.array([79, 0, 3, 41, 41, 17], np.int32)
+    exact, absum = restate.spmm_rows_f64(a, b, rows)
+    for k, i in enumerate(rows):
+        s, e = a.row_ptr[i], a.row_ptr[i + 1]
+        terms = a.val[s:e].astype(np.float64)[:, None] * b[a.col_ind[s:e]].astype(np.float64)
+        np.testing.assert_allclose(exact[k], terms.sum(0), rtol=0, atol=1e-12)
+        np.testing.assert_allclose(absum[k], np.abs(terms).sum(0), rtol=0, atol=1e-12)
+    got = restate.spmm(a, b)[rows].astype(np.float64)
+    bound = (np.diff(a.row_ptr)[rows][:, None] + 1) * 2.0 ** -24 * absum + 1e-30
+    assert (np.abs(got - exact) <= bound).all()
+
+
 def test_math_matmul_fp64(restate):
     rng = np.random.default_rng(2)
     a = rng.standard_normal((31, 57)).astype(np.float32)

@@ -410,14 +410,48 @@ class Model:
         unit-valued A + I -- on graphs dense enough to pay)."""
         lib.check(lib.tg_model_set_blocking(self.h, rows_per_block))
 
-    def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_CACHED, out=None, stream=None):
+    def invalidate(self) -> None:
+        """Forgets the cached adjacency state (tg_model_invalidate)."""
+        self._adj_key = None
+        lib.check(lib.tg_model_invalidate(self.h))
+
+    @staticmethod
+    def _adjacency_key(adj: DeviceCSR):
+        return (adj.n_rows, adj.row_ptr, adj.col_ind, adj.val, adj.row_ptr._version,
+                adj.col_ind._version, adj.val._version)
+
+    def _cache_valid(self, key) -> bool:
+        old = getattr(self, "_adj_key", None)
+        if old is None:
+            return False
+        return (old[0] == key[0] and all(a is b for a, b in zip(old[1:4], key[1:4]))
+                and old[4:] == key[4:])
+
+    def forward(self, adj: DeviceCSR, x, mode: int = FORWARD_REFERENCE, out=None, stream=None):
+        """Model::forward (model.cpp:359-439).
+
+        ``mode=FORWARD_REFERENCE`` (the default) recomputes gcn_norm /
+        add_self_loops and the row plans on every call, as the reference
+        does (model.cpp:373-381).  ``mode=FORWARD_CACHED`` reuses them when
+        ``adj`` holds the same ``row_ptr`` / ``col_ind`` / ``val`` tensor
+        objects as the previous forward, at the same torch versions (an
+        in-place edit through torch bumps the version; a new tensor is a
+        different object).  The model keeps references to those three
+        tensors, so their memory cannot be handed to another graph while the
+        cache refers to it.  Writes that torch does not track (through raw
+        device pointers) must be followed by :meth:`invalidate`."""
         torch = _torch()
         if out is None:
             out = torch.empty((adj.n_rows, self.output_cols()), dtype=torch.float32,
                               device=x.device)
+        key = self._adjacency_key(adj)
+        if mode == FORWARD_CACHED and not self._cache_valid(key):
+            lib.check(lib.tg_model_invalidate(self.h))
+        self._adj_key = None
         lib.check(lib.tg_model_forward(self.h, adj.n_rows, adj.nnz, dptr(adj.row_ptr),
                                        adj.col_ind.data_ptr(), adj.val.data_ptr(), x.shape[1],
                                        dptr(x), dptr(out), mode, stream_handle(stream)))
+        self._adj_key = key
         return out
 
     @staticmethod

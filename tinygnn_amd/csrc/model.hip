@@ -27,7 +27,8 @@
 //     left in the aggregation's, so the passes read the column indices alone
 //     (no values): the same sum, rounded differently;
 //   * TG_FORWARD_CACHED keeps the preprocessed adjacency and the row plans
-//     while the adjacency pointers and sizes are unchanged;
+//     while the adjacency pointers, sizes, precision and layer list are
+//     unchanged and tg_model_invalidate has not been called since;
 //     TG_FORWARD_REFERENCE recomputes them on every call, as the reference.
 #include "aggregate.hpp"
 #include "common.hpp"
@@ -90,6 +91,12 @@ struct tg_model_s {
     int built_precision = -1;  // precision the cached plans were built for
     int64_t block_rows = -1;   // column blocking (tg_model_set_blocking)
     int64_t built_block_rows = -2;  // blocking the blocked copies were built for (-2: none)
+
+    // bumped by every add_*_layer: the cached adjacency state (which of
+    // A + I, its values, A's plan and the blocked copies exist, and the
+    // feature width the plans were sized for) depends on the layer list
+    uint64_t layers_gen = 0;
+    uint64_t built_layers_gen = ~uint64_t(0);
 
     // adjacency-derived state
     bool have_cache = false;
@@ -191,6 +198,7 @@ int64_t add_layer(tg_model_s& m, Layer&& l) {
         upload(l.ar, zb);
     }
     m.layers.push_back(std::move(l));
+    ++m.layers_gen;  // the cached adjacency state no longer matches the layers
     return static_cast<int64_t>(m.layers.size()) - 1;
 }
 
@@ -319,7 +327,8 @@ void ensure_plan_sl(tg_model_s& m, int64_t n, int64_t nnz, hipStream_t s) {
 void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                        const int32_t* ci, const float* v, int mode, hipStream_t s) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
-                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision;
+                      m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision &&
+                      m.built_layers_gen == m.layers_gen;
     // a new blocking setting keeps the cached state, unless A + I's values
     // were skipped for the factored path (an unblocked GCN needs them)
     const bool values_ok = m.sl_values || !m.need_norm();
@@ -412,6 +421,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     }
     m.have_cache = true;
     m.built_precision = m.precision;
+    m.built_layers_gen = m.layers_gen;
     m.key_rp = rp;
     m.key_ci = ci;
     m.key_v = v;
@@ -687,6 +697,13 @@ int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block) {
         require(model != nullptr, "model is null");
         require(rows_per_block >= -1, "tg_model_set_blocking: rows_per_block must be >= -1");
         model->block_rows = rows_per_block;
+    });
+}
+
+int tg_model_invalidate(tg_model_t model) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        model->have_cache = false;
     });
 }
 

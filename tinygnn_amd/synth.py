@@ -124,6 +124,27 @@ def cora_synth(seed: int = 2708):
     return src, dst, x
 
 
+def powerlaw_edges_device(torch, n: int, total: int, seed: int, device, alpha: float = 2.1,
+                          dmax: int = 20000):
+    """The benchmark's config-D / config-E edge list, drawn on the GPU:
+    out-degrees from ``powerlaw_degrees(n, total, alpha, dmax, seed)`` (host),
+    destinations uniform over the other nodes and a random edge order from a
+    torch generator on ``device`` seeded with ``seed + 1``.  Returns int32
+    device tensors ``(src, dst)`` of ``total`` entries; deterministic for a
+    given seed and device type."""
+    deg = powerlaw_degrees(n, total, alpha=alpha, dmax=dmax, seed=seed)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed + 1)
+    src = torch.repeat_interleave(torch.arange(n, dtype=torch.int32, device=device),
+                                  torch.from_numpy(deg.astype(np.int64)).to(device))
+    dst = torch.randint(0, n - 1, (total,), generator=g, device=device, dtype=torch.int32)
+    dst += (dst >= src).to(torch.int32)  # no self-loops in the raw graph
+    perm = torch.randperm(total, generator=g, device=device)
+    src, dst = src[perm].contiguous(), dst[perm].contiguous()
+    del perm
+    return src, dst
+
+
 def glorot(rng: np.random.Generator, fan_in: int, fan_out: int, shape=None) -> np.ndarray:
     a = math.sqrt(6.0 / (fan_in + fan_out))
     shape = shape or (fan_in, fan_out)
