@@ -144,6 +144,28 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
             float* c, int64_t ldc, tg_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * SpMM that allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Arguments and
+ * result bits are tg_spmm's (the same plan and kernels), but the plan lives
+ * in a fixed device array of TG_SPMM_NOALLOC_SCRATCH_BYTES per GPU, held
+ * from the first call on that GPU until the process ends, and the call
+ * neither allocates nor synchronises: it only enqueues kernels on `stream`.
+ *   Limit: the plan takes 16(m+1) + 16(m + nnz/1024) + 16 nnz/1025
+ *   + 4 round_up(f, 4) (nnz/1024 + nnz/1025) bytes, about (256-byte aligned
+ *   pieces); larger sizes fail with TG_ERR_INVALID_ARGUMENT before any device
+ *   work.  Config D (10^6 rows, 5 x 10^7 nonzeros) fits for f <= 256.
+ *   Every call on one GPU uses that GPU's one array and leaves its contents
+ *   behind: calls that overlap in time on one GPU (other streams, other
+ *   threads) race, and the caller must serialise them.  row_ptr[m] must
+ *   equal nnz, as for tg_spmm (a larger row_ptr[m] leaves C unwritten).
+ * ------------------------------------------------------------------------ */
+#define TG_SPMM_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+                    const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
+                    float* c, int64_t ldc, tg_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Dense transform -- replaces tinygnn::matmul (src/ops.cpp:70-162,
  * ops.hpp:76): C[m x n] = A[m x k] * B[k x n], with an optional fused
  * epilogue (bias add, then activation) that equals calling add_bias

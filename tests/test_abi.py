@@ -63,3 +63,19 @@ def test_python_front_end_raises_typed_errors():
     with pytest.raises(tg.TgError) as e:
         _lib.lib.check(_lib.TG_ERR_RUNTIME)
     assert e.value.kind == "runtime_error"
+
+
+def test_spmm_noalloc_rejects_oversize_before_device_work():
+    """tg_spmm_noalloc checks the plan's size against its fixed scratch before
+    any device call (so this runs without a GPU): config D's 10^6 x 10^6 /
+    5 x 10^7 matrix fits up to f = 256 and not at f = 257."""
+    L = _lib.lib.load()
+    dummy = C.c_void_p(16)  # never dereferenced: the call fails on the host
+    rc = L.tg_spmm_noalloc(1_000_000, 1_000_000, 257, 50_000_000, dummy, dummy, dummy, dummy,
+                           257, dummy, 257, None)
+    assert rc == _lib.TG_ERR_INVALID_ARGUMENT
+    msg = L.tg_last_error().decode()
+    assert msg.startswith("tg_spmm_noalloc: the plan for m=1000000, nnz=50000000, f=257 needs ")
+    assert "the maximum is 134217728" in msg
+    assert L.tg_spmm_noalloc(-1, 1, 1, 1, dummy, dummy, dummy, dummy, 1, dummy, 1,
+                             None) == _lib.TG_ERR_INVALID_ARGUMENT

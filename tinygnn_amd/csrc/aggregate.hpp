@@ -65,6 +65,10 @@ struct AggEpilogue {
 void run_aggregate(const tg_spmm_plan_s& plan, int64_t f, const int32_t* col_ind,
                    const float* val, const float* b, int64_t ldb, float* c, int64_t ldc,
                    const AggEpilogue& epi, hipStream_t s, int tile_cols = 0);
+// The same over a plan view (a plan in fixed scratch, counts on the device).
+void run_aggregate(const PlanView& plan, int64_t f, const int32_t* col_ind, const float* val,
+                   const float* b, int64_t ldb, float* c, int64_t ldc, const AggEpilogue& epi,
+                   hipStream_t s, int tile_cols = 0);
 
 // Column-blocked form of a CSR structure for aggregations whose gathered
 // matrix is larger than an XCD's L2: the columns (source nodes) are cut into

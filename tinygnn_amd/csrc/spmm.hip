@@ -15,7 +15,9 @@
 #include "spmm_plan.hpp"
 
 #include <algorithm>
+#include <climits>
 #include <memory>
+#include <mutex>
 
 namespace tg {
 
@@ -61,20 +63,27 @@ __global__ __launch_bounds__(256) void plan_count_kernel(const int32_t* __restri
 }
 
 // Turns bin counts into start cursors, longest bin first; writes totals.
+// With caps (a plan built into fixed scratch), totals beyond the capacities
+// (a row_ptr inconsistent with the nnz the caller gave) zero the counts the
+// kernels read, so nothing runs, and set totals[3].
 __global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
                                  int32_t* __restrict__ bin_cursor,
                                  const int32_t* __restrict__ slot_base,
                                  const int32_t* __restrict__ split_pos, int64_t m,
-                                 int64_t* __restrict__ totals) {
+                                 int64_t* __restrict__ totals, int64_t cap_chunks,
+                                 int64_t cap_split, int64_t cap_partials) {
     if (threadIdx.x == 0) {
         int64_t acc = 0;
         for (int b = kPlanBins - 1; b >= 0; --b) {
             bin_cursor[b] = static_cast<int32_t>(acc);
             acc += bin_count[b];
         }
-        totals[0] = acc;                 // chunks
-        totals[1] = split_pos[m];        // split rows
-        totals[2] = slot_base[m];        // partial slots
+        const int64_t n_split = split_pos[m], n_part = slot_base[m];
+        const bool over = acc > cap_chunks || n_split > cap_split || n_part > cap_partials;
+        totals[0] = over ? 0 : acc;      // chunks
+        totals[1] = over ? 0 : n_split;  // split rows
+        totals[2] = n_part;              // partial slots
+        totals[3] = over ? 1 : 0;
     }
 }
 
@@ -85,7 +94,8 @@ __global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
 __global__ __launch_bounds__(256) void plan_scatter_kernel(
     const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
     const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
-    int32_t* __restrict__ bin_cursor, int4* __restrict__ chunks, int4* __restrict__ split) {
+    int32_t* __restrict__ bin_cursor, int4* __restrict__ chunks, int4* __restrict__ split,
+    int64_t cap_chunks, int64_t cap_split) {
     __shared__ int hist[kPlanBins], gbase[kPlanBins];
     for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
@@ -117,17 +127,25 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
     __syncthreads();
     if (r >= m) return;
     const int row = static_cast<int>(r);
+    // the caps only bite for a row_ptr that disagrees with the caller's nnz
+    // (fixed scratch); the plan's count is then zero and nothing reads these
     if (rem < 0) {
-        chunks[gbase[bin_r] + pos_r] = make_int4(row, b, e, -1);
+        const int64_t at = static_cast<int64_t>(gbase[bin_r]) + pos_r;
+        if (at < cap_chunks) chunks[at] = make_int4(row, b, e, -1);
         return;
     }
     const int slot0 = slot_base[r];
     for (int c = 0; c < full; ++c) {
         const int cb = b + c * chunk;
-        chunks[gbase[bin_f] + pos_f + c] = make_int4(row, cb, cb + chunk, slot0 + c);
+        const int64_t at = static_cast<int64_t>(gbase[bin_f]) + pos_f + c;
+        if (at < cap_chunks) chunks[at] = make_int4(row, cb, cb + chunk, slot0 + c);
     }
-    if (rem) chunks[gbase[bin_r] + pos_r] = make_int4(row, b + full * chunk, e, slot0 + full);
-    split[split_pos[r]] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
+    if (rem) {
+        const int64_t at = static_cast<int64_t>(gbase[bin_r]) + pos_r;
+        if (at < cap_chunks) chunks[at] = make_int4(row, b + full * chunk, e, slot0 + full);
+    }
+    if (split_pos[r] < cap_split)
+        split[split_pos[r]] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
 }
 
 }  // namespace
@@ -142,18 +160,7 @@ struct PlanTemps {
     int64_t *totals, *scan_tmp;
 };
 
-PlanTemps carve_plan_temps(tg_spmm_plan_s& p, int64_t m) {
-    Carver cv(nullptr, 0);
-    cv.take<int32_t>(m);
-    cv.take<int32_t>(m);
-    cv.take<int32_t>(m + 1);
-    cv.take<int32_t>(m + 1);
-    cv.take<int32_t>(kPlanBins);
-    cv.take<int32_t>(kPlanBins);
-    cv.take<int64_t>(4);
-    cv.take<int64_t>(scan_temp_elems(m));
-    p.scratch.reserve(cv.bytes());
-    Carver c(p.scratch.get(), p.scratch.size());
+PlanTemps carve_temps(Carver& c, int64_t m) {
     PlanTemps t;
     t.split_cnt = c.take<int32_t>(m);
     t.is_split = c.take<int32_t>(m);
@@ -164,6 +171,14 @@ PlanTemps carve_plan_temps(tg_spmm_plan_s& p, int64_t m) {
     t.totals = c.take<int64_t>(4);
     t.scan_tmp = c.take<int64_t>(scan_temp_elems(m));
     return t;
+}
+
+PlanTemps carve_plan_temps(tg_spmm_plan_s& p, int64_t m) {
+    Carver cv(nullptr, 0);
+    carve_temps(cv, m);
+    p.scratch.reserve(cv.bytes());
+    Carver c(p.scratch.get(), p.scratch.size());
+    return carve_temps(c, m);
 }
 
 }  // namespace
@@ -195,8 +210,9 @@ void build_plan_count(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int
     TG_LAUNCH_CHECK();
     exclusive_scan_i32(t.split_cnt, t.slot_base, m, t.scan_tmp, s);
     exclusive_scan_i32(t.is_split, t.split_pos, m, t.scan_tmp, s);
+    constexpr int64_t kNoCap = INT64_MAX;  // the host sizes the buffers afterwards
     plan_bins_kernel<<<1, 64, 0, s>>>(t.bin_count, t.bin_cursor, t.slot_base, t.split_pos, m,
-                                      t.totals);
+                                      t.totals, kNoCap, kNoCap, kNoCap);
     TG_LAUNCH_CHECK();
     TG_HIP(hipMemcpyAsync(host_totals, t.totals, 3 * sizeof(int64_t), hipMemcpyDeviceToHost, s));
 }
@@ -216,7 +232,8 @@ void build_plan_finish(tg_spmm_plan_s& p, const int64_t* host_totals, hipStream_
     const unsigned nblk = static_cast<unsigned>(ceil_div(p.m, 256));
     plan_scatter_kernel<<<nblk, 256, 0, s>>>(p.row_ptr, p.m, static_cast<int>(p.chunk),
                                              t.slot_base, t.split_pos, t.bin_cursor,
-                                             p.chunks.as<int4>(), p.split.as<int4>());
+                                             p.chunks.as<int4>(), p.split.as<int4>(),
+                                             p.n_chunks, p.n_split);
     TG_LAUNCH_CHECK();
 }
 
@@ -414,7 +431,8 @@ __device__ __forceinline__ float shfl_f(float v, int src, int width) {
 
 template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
-    const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
+    const int4* __restrict__ chunks, int64_t n_chunks, const int64_t* __restrict__ n_chunks_dev,
+    const int32_t* __restrict__ ci,
     const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, float* __restrict__ partials, int64_t ldp, int64_t f,
     AggEpilogue epi) {
@@ -424,7 +442,9 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int g = threadIdx.x / LPR;
     const int l = threadIdx.x % LPR;
     const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
-    if (cid >= n_chunks) return;
+    // a plan in fixed scratch: the grid covers an upper bound, the count is
+    // in device memory
+    if (cid >= (n_chunks_dev ? *n_chunks_dev : n_chunks)) return;
     const int4 ch = chunks[cid];
     if (epi.skip_empty && ch.z == ch.y) return;  // the row keeps its value in C
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
@@ -582,6 +602,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
 template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict__ split,
                                                          int64_t n_split,
+                                                         const int64_t* __restrict__ n_split_dev,
                                                          const float* __restrict__ partials,
                                                          int64_t ldp, float* __restrict__ C,
                                                          int64_t ldc, int64_t f,
@@ -591,7 +612,7 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
     const int g = threadIdx.x / LPR;
     const int l = threadIdx.x % LPR;
     const int64_t sid = static_cast<int64_t>(blockIdx.x) * GPB + g;
-    if (sid >= n_split) return;
+    if (sid >= (n_split_dev ? *n_split_dev : n_split)) return;
     const int4 sp = split[sid];
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
 #pragma unroll
@@ -612,32 +633,32 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
 }
 
 template <int VEC, int LPR, int VPL, int MODE>
-void launch_agg(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
+void launch_agg(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                 const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
                 const AggEpilogue& epi, hipStream_t s) {
     constexpr int GPB = 256 / LPR;
-    float* partials = p.partials.as<float>();
     const int64_t ldp = round_up(f, VEC);  // padded partial rows
+    const int64_t* dc = p.dev_counts;
     if (p.n_chunks > 0) {
         // grid.y = column tile: the workgroups resident at a time (dispatched
         // in x order) gather from one or two tiles of B
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_chunk_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
-            p.chunks.as<int4>(), p.n_chunks, ci, av, B, ldb, C, ldc, partials, ldp, f, epi);
+            p.chunks, p.n_chunks, dc, ci, av, B, ldb, C, ldc, p.partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
     if (p.n_split > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
                   static_cast<unsigned>(L.n_tiles));
-        agg_reduce_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(p.split.as<int4>(), p.n_split,
-                                                             partials, ldp, C, ldc, f, epi);
+        agg_reduce_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
+            p.split, p.n_split, dc ? dc + 1 : nullptr, p.partials, ldp, C, ldc, f, epi);
         TG_LAUNCH_CHECK();
     }
 }
 
 template <int VEC, int MODE>
-void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const int32_t* ci,
+void dispatch_lpr(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                   const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
                   const AggEpilogue& epi, hipStream_t s) {
 #define TG_AGG_CASE(LPR_, VPL_)                                                          \
@@ -655,6 +676,12 @@ void dispatch_lpr(const tg_spmm_plan_s& p, const LaneLayout& L, int64_t f, const
 }  // namespace
 
 void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const float* av,
+                   const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
+                   hipStream_t s, int tile_cols) {
+    run_aggregate(plan_view(p), f, ci, av, B, ldb, C, ldc, epi, s, tile_cols);
+}
+
+void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float* av,
                    const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
                    hipStream_t s, int tile_cols) {
     if (p.m == 0 || f == 0) return;
@@ -705,6 +732,116 @@ void run_aggregate(const tg_spmm_plan_s& p, int64_t f, const int32_t* ci, const 
 #undef TG_AGG_MODE
 }
 
+}  // namespace tg
+
+// ---------------------------------------------------------------------------
+// SpMM without allocation (tg_spmm_noalloc): the plan of one call -- its
+// build temporaries, chunks, split records and partials -- carved from one
+// fixed device array instead of allocated buffers.  The host never reads the
+// plan's counts: the grids cover upper bounds and the kernels read the true
+// counts from the array, so the call only enqueues kernels.
+// ---------------------------------------------------------------------------
+
+// Each GPU holds its own copy from the library's first use on it until the
+// process ends; every call on one GPU shares it (overlapping calls race).
+static __device__ __align__(256) unsigned char scratch[TG_SPMM_NOALLOC_SCRATCH_BYTES];
+
+namespace tg {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The array's device address on the current device.  The array's name in
+// host code is a host-side stand-in, not a device address, so every use
+// goes through the address hipGetSymbolAddress returns, taken once per
+// device with that device current.
+char* noalloc_scratch() {
+    int dev = 0;
+    TG_HIP(hipGetDevice(&dev));
+    require(dev >= 0 && dev < kMaxDevices, "tg_spmm_noalloc: device ordinal out of range");
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        void* p = nullptr;
+        TG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        require(p != nullptr, "tg_spmm_noalloc: no device address for the scratch array");
+        addr[dev] = p;
+    }
+    return static_cast<char*>(addr[dev]);
+}
+
+// Capacities of a plan for m rows and nnz nonzeros in chunks of c:
+// chunks <= m + nnz / c (each row one chunk, plus one per further c
+// entries); split rows hold more than c entries, so there are at most
+// nnz / (c + 1) of them; their partial slots number ceil(deg / c) <= 1 +
+// deg / c each, at most n_split + nnz / c.
+struct NoAllocPlan {
+    int64_t cap_chunks = 0, cap_split = 0, cap_partials = 0;
+    PlanTemps t{};
+    int4* chunks = nullptr;
+    int4* split = nullptr;
+    float* partials = nullptr;
+};
+
+NoAllocPlan carve_noalloc(Carver& cv, int64_t m, int64_t nnz, int64_t f) {
+    const int64_t c = kDefaultChunk;
+    NoAllocPlan P;
+    P.cap_chunks = m + nnz / c;
+    P.cap_split = std::min(m, nnz / (c + 1));
+    P.cap_partials = P.cap_split > 0 ? P.cap_split + nnz / c : 0;
+    P.t = carve_temps(cv, m);
+    P.chunks = cv.take<int4>(static_cast<size_t>(P.cap_chunks));
+    P.split = cv.take<int4>(static_cast<size_t>(std::max<int64_t>(P.cap_split, 1)));
+    P.partials = cv.take<float>(static_cast<size_t>(P.cap_partials * round_up(f, 4)));
+    return P;
+}
+
+void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const int32_t* ci,
+                  const float* v, const float* b, int64_t ldb, float* c, int64_t ldc,
+                  hipStream_t s) {
+    // sizes first: a rejected call does no device work
+    Carver sizing(nullptr, 0);
+    carve_noalloc(sizing, m, nnz, f);
+    if (sizing.bytes() > TG_SPMM_NOALLOC_SCRATCH_BYTES)
+        throw std::invalid_argument(
+            "tg_spmm_noalloc: the plan for m=" + std::to_string(m) + ", nnz=" +
+            std::to_string(nnz) + ", f=" + std::to_string(f) + " needs " +
+            std::to_string(sizing.bytes()) + " bytes of scratch; the maximum is " +
+            std::to_string(static_cast<size_t>(TG_SPMM_NOALLOC_SCRATCH_BYTES)) +
+            " (use tg_spmm or a plan)");
+    Carver cv(noalloc_scratch(), TG_SPMM_NOALLOC_SCRATCH_BYTES);
+    const NoAllocPlan P = carve_noalloc(cv, m, nnz, f);
+    const int chunk = static_cast<int>(kDefaultChunk);
+    const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
+    fill_i32(P.t.bin_count, kPlanBins, 0, s);  // a kernel, so the call stays capturable
+    plan_count_kernel<<<nblk, 256, 0, s>>>(rp, m, chunk, P.t.split_cnt, P.t.is_split,
+                                           P.t.bin_count);
+    TG_LAUNCH_CHECK();
+    exclusive_scan_i32(P.t.split_cnt, P.t.slot_base, m, P.t.scan_tmp, s);
+    exclusive_scan_i32(P.t.is_split, P.t.split_pos, m, P.t.scan_tmp, s);
+    plan_bins_kernel<<<1, 64, 0, s>>>(P.t.bin_count, P.t.bin_cursor, P.t.slot_base,
+                                      P.t.split_pos, m, P.t.totals, P.cap_chunks, P.cap_split,
+                                      P.cap_partials);
+    TG_LAUNCH_CHECK();
+    plan_scatter_kernel<<<nblk, 256, 0, s>>>(rp, m, chunk, P.t.slot_base, P.t.split_pos,
+                                             P.t.bin_cursor, P.chunks, P.split, P.cap_chunks,
+                                             P.cap_split);
+    TG_LAUNCH_CHECK();
+    PlanView pv;
+    pv.m = m;
+    pv.max_f = f;
+    pv.n_chunks = P.cap_chunks;
+    pv.n_split = P.cap_split;
+    pv.chunks = P.chunks;
+    pv.split = P.split;
+    pv.partials = P.partials;
+    pv.dev_counts = P.t.totals;  // [0] chunks, [1] split rows
+    AggEpilogue epi;
+    run_aggregate(pv, f, ci, v, b, ldb, c, ldc, epi, s);
+}
+
+}  // namespace
 }  // namespace tg
 
 // ---------------------------------------------------------------------------
@@ -772,6 +909,25 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
         tg::AggEpilogue epi;
         tg::run_aggregate(p, f, col_ind, val, b, ldb, c, ldc, epi, s);
         TG_HIP(hipStreamSynchronize(s));  // the plan's buffers are freed on return
+    });
+}
+
+int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+                    const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
+                    float* c, int64_t ldc, tg_stream_t stream) {
+    return guard([&] {
+        require(m >= 0 && k >= 0 && f >= 0 && nnz >= 0, "spmm: negative dimension");
+        require(m < (int64_t(1) << 31) && nnz < (int64_t(1) << 31),
+                "spmm: m and nnz must be < 2^31 (int32 CSR)");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        if (m == 0 || f == 0) return;
+        if (nnz == 0) {
+            // ops.cpp:231-236: the result is the zero-initialised C.
+            tg::fill_zero_2d(c, m, f, ldc, s);
+            return;
+        }
+        require(row_ptr && col_ind && val && b && c, "spmm: null pointer");
+        tg::spmm_noalloc(m, f, nnz, row_ptr, col_ind, val, b, ldb, c, ldc, s);
     });
 }
 

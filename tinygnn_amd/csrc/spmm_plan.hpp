@@ -35,6 +35,35 @@ struct tg_spmm_plan_s {
 
 namespace tg {
 
+// A plan's arrays as the aggregation launches read them.  For an owning
+// plan the counts are exact and dev_counts is null.  For a plan built into
+// tg_spmm_noalloc's static scratch the host never learns the counts:
+// n_chunks / n_split are upper bounds (they size the grids) and
+// dev_counts[0] / dev_counts[1] hold the true counts in device memory, read
+// by the kernels (workgroups past them exit).
+struct PlanView {
+    int64_t m = 0;
+    int64_t max_f = 0;
+    int64_t n_chunks = 0;
+    int64_t n_split = 0;
+    const int4* chunks = nullptr;
+    const int4* split = nullptr;
+    float* partials = nullptr;
+    const int64_t* dev_counts = nullptr;
+};
+
+inline PlanView plan_view(const tg_spmm_plan_s& p) {
+    PlanView v;
+    v.m = p.m;
+    v.max_f = p.max_f;
+    v.n_chunks = p.n_chunks;
+    v.n_split = p.n_split;
+    v.chunks = p.chunks.as<int4>();
+    v.split = p.split.as<int4>();
+    v.partials = p.partials.as<float>();
+    return v;
+}
+
 constexpr int kPlanBins = 64;
 constexpr int64_t kDefaultChunk = 1024;
 
