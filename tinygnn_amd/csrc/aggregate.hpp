@@ -44,11 +44,20 @@ struct AggEpilogue {
     int64_t b_tile_stride = 0;
     // self's layout: > 0 = tile-major as B (ld_self = 32); 0 = row-major
     int64_t self_tile_stride = 0;
-    // edge weights in planes of one column group each (GAT: one per head):
-    // the lane group's tile takes plane (first column / w_head_cols), at
-    // val + plane * w_head_stride (tiles never straddle two groups)
-    int64_t w_head_stride = 0;
+    // columns per head of the attention mode below (tiles never straddle
+    // two heads)
     int w_head_cols = 1;
+    // GAT attention computed in the pass (att_dst non-null): the weight of
+    // entry (i, j) for the tile's head h = first column / w_head_cols is
+    // exp(LeakyReLU(att_src[i,h] + att_dst[j,h]) - att_max[i,h]) *
+    // att_rinv[i,h], with exact_exp choosing exp_rn; all four arrays are
+    // [n x att_heads].  No value stream is read.
+    const float* att_src = nullptr;
+    const float* att_dst = nullptr;
+    const float* att_max = nullptr;
+    const float* att_rinv = nullptr;
+    int att_heads = 1;
+    float att_slope = 0.2f;
 };
 
 
@@ -112,16 +121,12 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
 int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_cols = 32);
 
 // The same aggregation as run_aggregate over the unblocked structure (same
-// epilogue; weights from the blocked values when bk is weighted), computed
-// block by block, each pass continuing the rows' sums.  With bk.in_order and
-// plans that split no row, the result is bit-identical to the unblocked
-// in-order sums; rows split into chunks are summed from per-chunk partials.
-// epi.max is not supported.
-//
-// weights (optional): per-entry weights in blocked entry order instead of the
-// structure's values (with epi.w_head_stride, one plane per column group).
+// epilogue; weights from the blocked values when bk is weighted, or computed
+// per entry in the attention mode), computed block by block, each pass
+// continuing the rows' sums.  With bk.in_order and plans that split no row,
+// the result is bit-identical to the unblocked in-order sums; rows split
+// into chunks are summed from per-chunk partials.  epi.max is not supported.
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
-                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
-                           const float* weights = nullptr);
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s);
 
 }  // namespace tg

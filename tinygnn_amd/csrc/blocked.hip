@@ -244,21 +244,22 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
 }
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
-                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s,
-                           const float* weights) {
+                           float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s) {
     require(!epi.max, "blocked aggregation: max is not supported");
     require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
     if (bk.n == 0 || f == 0) return;
     const int32_t* bci = bk.bci.as<int32_t>();
-    const float* bv = weights ? weights : bk.weighted ? bk.bv.as<float>() : nullptr;
+    // attention passes compute their weights (no value stream)
+    const float* bv = epi.att_dst == nullptr && bk.weighted ? bk.bv.as<float>() : nullptr;
     // One launch per block over all column groups of f (grid.y), blocks in
     // order: the first pass stores every row (zero where the block has no
     // entries), middle passes touch only rows with entries, the last pass
     // adds and applies the epilogue to every row.  64-column groups only
-    // where a group has two tiles' worth of columns and lies in one weight
-    // plane.
+    // where a group has two tiles' worth of columns and, for attention
+    // passes, lies in one head.
+    const bool per_head = epi.att_dst != nullptr;
     const bool wide = bk.group_cols == 64 && f > 32 &&
-                      (epi.w_head_stride == 0 || epi.w_head_cols >= f || epi.w_head_cols % 64 == 0);
+                      (!per_head || epi.w_head_cols >= f || epi.w_head_cols % 64 == 0);
     const int group_cols = wide ? 64 : 32;
     for (int64_t blk = 0; blk < bk.n_blocks; ++blk) {
         const bool first = blk == 0, last = blk + 1 == bk.n_blocks;
@@ -271,9 +272,14 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         e.skip_empty = (!first && !last) ? 1 : 0;
         // the operands' layouts, in every pass
         e.b_tile_stride = epi.b_tile_stride;
-        e.w_head_stride = epi.w_head_stride;
         e.w_head_cols = epi.w_head_cols;
         e.exact_exp = epi.exact_exp;
+        e.att_src = epi.att_src;
+        e.att_dst = epi.att_dst;
+        e.att_max = epi.att_max;
+        e.att_rinv = epi.att_rinv;
+        e.att_heads = epi.att_heads;
+        e.att_slope = epi.att_slope;
         run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, group_cols);
     }
 }

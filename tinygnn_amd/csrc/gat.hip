@@ -20,10 +20,11 @@
 //     with its own (max, sum); gat_reduce_kernel merges them in chunk order
 //     (max of maxima, sums rescaled by exp(m_c - M)).
 //   * column-blocked form (large, dense graphs): gat_stats_kernel first
-//     finds each row's max score and 1/sum per head, gat_weights_kernel
-//     writes alpha_ij = exp(e_ij - max_i) / sum_i once per entry and head,
-//     and the blocked passes (blocked.hip) aggregate alpha_ij Wh_j block by
-//     block as weighted sums, one weight plane per head.
+//     finds each row's max score and 1/sum per head; then the blocked passes
+//     (blocked.hip) aggregate alpha_ij Wh_j block by block, each pass
+//     computing alpha_ij = exp(e_ij - max_i) * (1/sum_i) per entry and head
+//     from the [n x heads] scores and statistics (the attention mode of the
+//     aggregation kernel): the attention matrix is never stored here either.
 #include "aggregate.hpp"
 #include "common.hpp"
 #include "device_utils.hpp"
@@ -689,58 +690,6 @@ __global__ __launch_bounds__(256) void gat_exact_stats_kernel(const int4* __rest
     }
 }
 
-// The attention weights of the column-blocked passes, once per entry and
-// head: alpha_ij = exp(e_ij - max_i) * (1/sum_i) (layers.cpp:1076-1090;
-// exact: exp_rn), e_ij = LeakyReLU(src_i + dst_j), written to plane h at the
-// entry's blocked position (w[h * plane + position]).  One wave per SEGS
-// consecutive (block, row) segments of the blocked structure: their entries
-// are one contiguous range, walked 64 at a time; an entry's segment is the
-// number of the range's inner boundaries at or below it, and its row's
-// statistics come from L1.  (One wave per segment, 16-lane groups per
-// segment and one wave per row all measured slower: a segment holds about
-// 50 entries at config E, too few to hide a wave's dependent loads.)
-template <int NH, int SEGS>
-__global__ __launch_bounds__(256) void gat_weights_kernel(
-    const int32_t* __restrict__ brp, const int32_t* __restrict__ bci, int64_t n, int64_t nseg,
-    int heads, const float* __restrict__ src, const float* __restrict__ dst,
-    const float* __restrict__ rmax, const float* __restrict__ rinv, float slope, int exact,
-    float* __restrict__ w, int64_t plane) {
-    const int lane = threadIdx.x & 63;
-    const int64_t s0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * SEGS;
-    if (s0 >= nseg) return;  // uniform per wave
-    const int ns = static_cast<int>(nseg - s0 < SEGS ? nseg - s0 : SEGS);
-    // the ns + 1 boundaries, one per lane, then wave-uniform
-    const int bl = lane <= ns ? brp[s0 + lane] : 0;
-    int bnd[SEGS + 1];
-#pragma unroll
-    for (int k = 0; k <= SEGS; ++k) bnd[k] = __shfl(bl, k <= ns ? k : ns);
-    const int b = bnd[0], e = bnd[ns];
-    if (b == e) return;
-    const int64_t row0 = s0 % n;
-    for (int h0 = 0; h0 < heads; h0 += NH) {
-        for (int i = b + lane; i < e; i += 64) {
-            int k = 0;
-#pragma unroll
-            for (int t = 1; t < SEGS; ++t) k += (t < ns && i >= bnd[t]) ? 1 : 0;
-            int64_t row = row0 + k;
-            while (row >= n) row -= n;  // the group ran into the next block(s)
-            float si[NH], mi[NH], ri[NH], d[NH];
-#pragma unroll
-            for (int q = 0; q < NH; ++q) {
-                si[q] = src[row * heads + h0 + q];
-                mi[q] = rmax[row * heads + h0 + q];
-                ri[q] = rinv[row * heads + h0 + q];
-            }
-            gat_dst<NH>(dst, heads, h0, bci[i], d);
-#pragma unroll
-            for (int q = 0; q < NH; ++q) {
-                const float x = lrelu(si[q] + d[q], slope) - mi[q];
-                w[static_cast<int64_t>(h0 + q) * plane + i] = (exact ? exp_rn(x) : expf(x)) * ri[q];
-            }
-        }
-    }
-}
-
 // Split rows: the chunks' (max, sum) pairs merged in chunk order, one
 // thread per row and head.
 __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __restrict__ split,
@@ -865,12 +814,11 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
-                           float* rmax, float* rinv, float* weights, void* work,
-                           size_t work_bytes, hipStream_t s, bool exact) {
+                           float* rmax, float* rinv, void* work, size_t work_bytes,
+                           hipStream_t s, bool exact) {
     require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
     require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
-    require(weights != nullptr, "GATLayer: no weight buffer");
     if (n == 0) return;
     const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
     const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
@@ -916,27 +864,21 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
             TG_LAUNCH_CHECK();
         }
     }
-    // the attention weights, once per entry and head, in blocked entry order
-    constexpr int kSegs = 8;  // (block, row) segments per wave
-    const int64_t nseg = bk.n_blocks * n;
-    const unsigned wgrid = static_cast<unsigned>(ceil_div(nseg, 4 * kSegs));
-    if (vec4)
-        gat_weights_kernel<4, kSegs><<<wgrid, 256, 0, s>>>(
-            bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
-            rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
-    else
-        gat_weights_kernel<1, kSegs><<<wgrid, 256, 0, s>>>(
-            bk.brp.as<int32_t>(), bk.bci.as<int32_t>(), n, nseg, static_cast<int>(heads), src, dst,
-            rmax, rinv, slope, exact ? 1 : 0, weights, bk.nnz);
-    TG_LAUNCH_CHECK();
+    // the passes compute alpha_ij per entry and head from the scores and
+    // the row statistics: the nnz x heads attention matrix is never stored
     AggEpilogue epi;
     epi.bias = bias;
     epi.act = act;
     epi.post = post;
     epi.exact_exp = exact ? 1 : 0;
-    epi.w_head_stride = bk.nnz;
     epi.w_head_cols = static_cast<int>(f);
-    run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s, weights);
+    epi.att_src = src;
+    epi.att_dst = dst;
+    epi.att_max = rmax;
+    epi.att_rinv = rinv;
+    epi.att_heads = static_cast<int>(heads);
+    epi.att_slope = slope;
+    run_aggregate_blocked(bk, heads * f, wh, ldwh, out, ldo, epi, s);
 }
 
 }  // namespace tg

@@ -62,16 +62,17 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
 // allows it (concatenated or single head, heads of whole 32-column tiles),
 // and the aggregation itself over the blocked
 // form of the structure (p, ci: the unblocked structure's plan and columns,
-// for the softmax statistics; rmax, rinv: n x heads scratch; weights:
-// heads x bk.nnz floats (the attention weights, one plane per head); work: at least
-// gat_workspace(p, ...) bytes; exact: the reference's operation order, for
-// a plan that splits no row and a blocked structure in block order).
+// for the softmax statistics; rmax, rinv: n x heads scratch; the passes
+// compute each entry's attention weight from them and the scores, storing
+// none; work: at least gat_workspace(p, ...) bytes; exact: the reference's
+// operation order, for a plan that splits no row and a blocked structure in
+// block order).
 bool gat_blocked_ok(int64_t heads, int64_t f, int concat);
 void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
-                           float* rmax, float* rinv, float* weights, void* work,
-                           size_t work_bytes, hipStream_t s, bool exact = false);
+                           float* rmax, float* rinv, void* work, size_t work_bytes,
+                           hipStream_t s, bool exact = false);
 
 }  // namespace tg

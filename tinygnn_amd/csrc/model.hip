@@ -122,7 +122,6 @@ struct tg_model_s {
 
     // per-forward buffers
     DeviceBuffer act[2], tmp, scores, work;
-    DeviceBuffer gat_w;  // blocked GAT: attention weights, one plane per head
 
     bool need_norm() const {
         for (auto& l : layers) if (l.type == LType::GCN) return true;
@@ -565,12 +564,11 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             if (blocked) {
                 float* rmax = dst + n * l.heads;
                 float* rinv = rmax + n * l.heads;
-                m.gat_w.reserve(static_cast<size_t>(l.heads * m.blk_sl->nnz) * sizeof(float));
                 gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,
                                       m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
                                       l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
-                                      l.out_cols(), rmax, rinv, m.gat_w.as<float>(),
-                                      m.work.get(), m.work.size(), s, exact);
+                                      l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s,
+                                      exact);
             } else {
                 gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh,
                               src, dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act,

@@ -401,7 +401,9 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
     store_vec<VEC>(c + static_cast<int64_t>(row) * ldc + fo, x);
 }
 
-enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2 };
+// kAggAttn: GAT's attention weights, computed per entry inside the pass
+// (AggEpilogue.att_*), then accumulated as kAggWeighted's.
+enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2, kAggAttn = 3 };
 
 // One step of a row's reduction: fma with the edge weight (SpMM's value,
 // ops.cpp:266-287, or a GAT attention weight), a plain add (SAGE mean,
@@ -409,7 +411,7 @@ enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2 };
 // std::max(acc, x) = (acc < x) ? x : acc (layers.cpp:398-417).
 template <int MODE>
 __device__ __forceinline__ float combine(float acc, float x, float w) {
-    if constexpr (MODE == kAggWeighted) return __builtin_fmaf(w, x, acc);
+    if constexpr (MODE == kAggWeighted || MODE == kAggAttn) return __builtin_fmaf(w, x, acc);
     if constexpr (MODE == kAggSum) return acc + x;
     return (acc < x) ? x : acc;
 }
@@ -448,9 +450,17 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     const int4 ch = chunks[cid];
     if (epi.skip_empty && ch.z == ch.y) return;  // the row keeps its value in C
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
-    // weights in planes per column group: the tile's group's plane
-    if constexpr (MODE == kAggWeighted) {
-        if (epi.w_head_stride > 0) av += (fbase / epi.w_head_cols) * epi.w_head_stride;
+    // attention weights: the row's score, max and 1/sum for the tile's head
+    // (every tile lies in one head's columns); dst scores of that head
+    float att_s = 0.0f, att_m = 0.0f, att_r = 0.0f;
+    const float* att_d = nullptr;
+    if constexpr (MODE == kAggAttn) {
+        const int64_t h = fbase / epi.w_head_cols;
+        const int64_t o = static_cast<int64_t>(ch.x) * epi.att_heads + h;
+        att_s = epi.att_src[o];
+        att_m = epi.att_max[o];
+        att_r = epi.att_rinv[o];
+        att_d = epi.att_dst + h;
     }
 
     int64_t fo[VPL], fl[VPL];
@@ -521,13 +531,18 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
         }
     };
     fetch(ch.y);
+    const int att_stride = epi.att_heads;
     for (int base = ch.y; base < e; base += BE) {
         int cl[CPL];
-        float wl[CPL];
+        float wl[CPL], dl[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             cl[j] = ncl[j];
             wl[j] = nwl[j];
+            // the batch's destination scores, loaded before its row gathers
+            // so that their latency overlaps the gathers'
+            if constexpr (MODE == kAggAttn)
+                dl[j] = att_d[static_cast<int64_t>(cl[j]) * att_stride];
         }
         // U gathers in flight per step; in the chunk's last, partial batch
         // the slots past its end gather row 0 (in bounds: cl is 0 there) and
@@ -554,23 +569,46 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                         load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
                 }
                 if (s0 == 0) fetch(base + BE);
+                if constexpr (MODE == kAggAttn) {
+                    // alpha_ij = exp(LeakyReLU(s_i + d_j) - max_i) * (1/sum_i)
+                    // (layers.cpp:1068-1090), once per entry and head
+                    if (s0 == 0) {
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) {
+                            const float x = att_s + dl[j];
+                            const float t = ((x >= 0.0f) ? x : epi.att_slope * x) - att_m;
+                            wl[j] = (epi.exact_exp ? exp_rn(t) : expf(t)) * att_r;
+                        }
+                    }
+                }
+                // the weight of slot u: attention weights are broadcast at
+                // their fma (not all U held at once: fewer live registers)
+                auto wt = [&](int u) {
+                    if constexpr (MODE == kAggAttn)
+                        return shfl_f(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+                    else
+                        return w[u];
+                };
                 if (cnt == BE) {  // a full batch: every slot is an entry
 #pragma unroll
-                    for (int u = 0; u < U; ++u)
+                    for (int u = 0; u < U; ++u) {
+                        const float wu = wt(u);
 #pragma unroll
                         for (int v = 0; v < VPL; ++v)
 #pragma unroll
                             for (int k = 0; k < VEC; ++k)
-                                acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
+                                acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                    }
                 } else {
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const bool valid = s0 + u < cnt;  // a select, not a branch
+                        const float wu = wt(u);
 #pragma unroll
                         for (int v = 0; v < VPL; ++v)
 #pragma unroll
                             for (int k = 0; k < VEC; ++k) {
-                                const float nx = combine<MODE>(acc[v][k], bv[u][v][k], w[u]);
+                                const float nx = combine<MODE>(acc[v][k], bv[u][v][k], wu);
                                 acc[v][k] = valid ? nx : acc[v][k];
                             }
                     }
@@ -712,11 +750,6 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
         L.tile = tile_cols;
         L.n_tiles = static_cast<int>(ceil_div(f, tile_cols));
     }
-    // weight planes per column group: every lane group's tile lies in one group
-    require(epi.w_head_stride == 0 ||
-                (av && epi.w_head_cols >= 1 &&
-                 (epi.w_head_cols >= f || epi.w_head_cols % L.tile == 0)),
-            "aggregate: weight planes must cover whole column tiles");
 #define TG_AGG_MODE(M_)                                                                \
     if (vec == 4) return dispatch_lpr<4, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
     if (vec == 2) return dispatch_lpr<2, M_>(p, L, f, ci, av, B, ldb, C, ldc, e, s);      \
@@ -724,6 +757,12 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
     if (epi.max) {
         require(!epi.mean, "aggregate: max and mean are exclusive");
         TG_AGG_MODE(kAggMax)
+    }
+    if (epi.att_dst) {
+        require(!av && !epi.mean && epi.w_head_cols >= 1 &&
+                    (epi.w_head_cols >= f || epi.w_head_cols % L.tile == 0),
+                "aggregate: attention weights need whole column tiles per head");
+        TG_AGG_MODE(kAggAttn)
     }
     if (av) {
         TG_AGG_MODE(kAggWeighted)
