@@ -34,7 +34,11 @@ def test_matmul_inorder_bitexact(gpu, restate, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(128, 16, 128), (1000, 602, 256), (777, 256, 41),
-                                   (300, 33, 130), (64, 1433, 64)])
+                                   (300, 33, 130), (64, 1433, 64),
+                                   # thin products (n <= 64: 16-column MFMA tiles), k not a
+                                   # multiple of the 32-wide chunk, m not of 64
+                                   (4099, 37, 16), (1000, 256, 48), (130, 300, 33), (64, 64, 60),
+                                   (65, 19, 3), (2500, 256, 41)])
 def test_matmul_mfma_bound(gpu, m, k, n):
     import tinygnn_amd as tg
     rng = np.random.default_rng(m + k + n)
@@ -46,15 +50,17 @@ def test_matmul_mfma_bound(gpu, m, k, n):
     assert (np.abs(got - exact) <= bound).all(), float((np.abs(got - exact) / bound).max())
 
 
+@pytest.mark.parametrize("n", [96, 41])
 @pytest.mark.parametrize("algo", [1, 2])
 @pytest.mark.parametrize("epi", [0, 1, 2])
-def test_matmul_epilogue(gpu, restate, algo, epi):
-    """Fused bias + act equals add_bias then relu/elu (ops.cpp:622, :328, :380)."""
+def test_matmul_epilogue(gpu, restate, algo, epi, n):
+    """Fused bias + act equals add_bias then relu/elu (ops.cpp:622, :328, :380);
+    n = 41 takes the thin MFMA kernel."""
     import tinygnn_amd as tg
-    rng = np.random.default_rng(10 + epi)
+    rng = np.random.default_rng(10 + epi + n)
     a = rng.standard_normal((200, 70)).astype(np.float32)
-    b = rng.standard_normal((70, 96)).astype(np.float32)
-    bias = rng.standard_normal((1, 96)).astype(np.float32)
+    b = rng.standard_normal((70, n)).astype(np.float32)
+    bias = rng.standard_normal((1, n)).astype(np.float32)
     got = tg.matmul(_t(gpu, a), _t(gpu, b), bias=_t(gpu, bias), epilogue=epi,
                     algo=algo).cpu().numpy()
     want = restate.add_bias(restate.matmul(a, b), bias)

@@ -408,6 +408,205 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// Thin MFMA GEMM (n <= 64): each wavefront owns 64 rows x 16 NT columns
+// (4 x NT tiles of v_mfma_f32_16x16x4f32) and reads its operands straight
+// from global memory in the MFMA layout, with no LDS and no barrier.  In a
+// chunk of 32 k values lane (q, r) feeds k = k0 + 8q + s at MFMA step s
+// (s = 0..7) for both operands, so its A values of a row are 8 consecutive
+// floats (two 128-bit loads; the wavefront reads whole 128-byte lines) and
+// its B values are column 16 j + r of rows k0 + 8q .. k0 + 8q + 7 (B is a
+// few KB and stays in L1/L2).  The next chunk's operands are loaded while
+// the current chunk's MFMAs run.  A 128 x 128 tile would do 128/n times the
+// needed MFMA work at n = 41; here it is 16 NT / n (48 / 41).
+// ---------------------------------------------------------------------------
+constexpr int kTK = 32;  // k per chunk
+
+template <int NT, bool ALIGNED>
+__global__ __launch_bounds__(256) void gemm_mfma_thin_kernel(GemmArgs g) {
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4, r = lane & 15;
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 64;
+    const int64_t M = g.m, N = g.n;
+    if (m0 >= M) return;  // no barrier in this kernel: waves retire independently
+    const int64_t t1 = (g.k1 + kTK - 1) / kTK;
+    const int64_t nt = t1 + (g.a2 ? (g.k2 + kTK - 1) / kTK : 0);
+
+    float a[4][8], b[NT][8];
+    auto fetch = [&](int64_t kt, float (&ra)[4][8], float (&rb)[NT][8]) {
+        const bool seg2 = kt >= t1;
+        const float* A = seg2 ? g.a2 : g.a1;
+        const float* B = seg2 ? g.b2 : g.b1;
+        const int64_t lda = seg2 ? g.lda2 : g.lda1;
+        const int64_t ldb = seg2 ? g.ldb2 : g.ldb1;
+        const int64_t K = seg2 ? g.k2 : g.k1;
+        const int64_t k = (seg2 ? kt - t1 : kt) * kTK + 8 * q;  // this lane's first k
+        const int64_t kv = K - k;  // valid k values from k on (may be <= 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t gm = m0 + 16 * i + r;
+            const float* p = A + (gm < M ? gm : 0) * lda + (kv > 0 ? k : 0);
+            if (ALIGNED && gm < M && kv >= 8) {
+                const float4 x0 = *reinterpret_cast<const float4*>(p);
+                const float4 x1 = *reinterpret_cast<const float4*>(p + 4);
+                ra[i][0] = x0.x; ra[i][1] = x0.y; ra[i][2] = x0.z; ra[i][3] = x0.w;
+                ra[i][4] = x1.x; ra[i][5] = x1.y; ra[i][6] = x1.z; ra[i][7] = x1.w;
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) ra[i][t] = (gm < M && t < kv) ? p[t] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t gn = 16 * j + r;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                rb[j][t] = (gn < N && t < kv) ? B[(k + t) * ldb + gn] : 0.0f;
+        }
+    };
+
+    v4f acc[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (nt > 0) fetch(0, a, b);
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        float na[4][8], nb[NT][8];
+        if (kt + 1 < nt) fetch(kt + 1, na, nb);
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j],
+                                                                     0, 0, 0);
+        if (kt + 1 < nt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) a[i][t] = na[i][t];
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) b[j][t] = nb[j][t];
+        }
+    }
+    // D layout of 16x16x4 f32: lane (q, r) holds rows 4q..4q+3 of column r.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t gn = 16 * j + r;
+            if (gn >= N) continue;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t gm = m0 + 16 * i + 4 * q + rr;
+                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
+            }
+        }
+}
+
+// Thin MFMA GEMM with B in LDS (one pair, n <= 64, round_up(k, 32) x 16 NT
+// floats of B <= 64 KB): B is staged once per workgroup, packed so that a
+// lane's 8 k values of its column are two 128-bit LDS reads; each wavefront
+// owns 32 rows (2 x NT tiles) and keeps A two chunks ahead in registers, so
+// more waves and more bytes are in flight than with B in registers.
+constexpr int kThinRows = 32;                  // rows per wavefront
+constexpr int kThinWaves = 8;                  // wavefronts per workgroup
+constexpr int64_t kThinLdsFloats = 16 * 1024;  // B panel budget (64 KB)
+
+template <int NT>
+__global__ __launch_bounds__(512) void gemm_mfma_thin_lds_kernel(GemmArgs g) {
+    extern __shared__ __attribute__((aligned(16))) float Bs[];  // [k/8][16 NT][8]
+    constexpr int BN = 16 * NT;
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4, r = lane & 15;
+    const int64_t M = g.m, N = g.n, K = g.k1;
+    const int64_t nt = (K + kTK - 1) / kTK;
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * kThinWaves + (threadIdx.x >> 6)) *
+                       kThinRows;
+    const bool active = m0 < M;  // every wave joins the barrier below
+    const float* A = g.a1;
+    const int64_t lda = g.lda1;
+
+    float a0[2][8], a1[2][8], a2[2][8];
+    auto fetch = [&](int64_t kt, float (&ra)[2][8]) {
+        const int64_t k = kt * kTK + 8 * q;
+        const int64_t kv = K - k;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t gm = m0 + 16 * i + r;
+            const float* p = A + (gm < M ? gm : 0) * lda + (kv > 0 ? k : 0);
+            if (gm < M && kv >= 8) {
+                const float4 x0 = *reinterpret_cast<const float4*>(p);
+                const float4 x1 = *reinterpret_cast<const float4*>(p + 4);
+                ra[i][0] = x0.x; ra[i][1] = x0.y; ra[i][2] = x0.z; ra[i][3] = x0.w;
+                ra[i][4] = x1.x; ra[i][5] = x1.y; ra[i][6] = x1.z; ra[i][7] = x1.w;
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) ra[i][t] = (gm < M && t < kv) ? p[t] : 0.0f;
+            }
+        }
+    };
+    if (active && nt > 0) fetch(0, a0);
+    if (active && nt > 1) fetch(1, a1);
+    // stage B, zero-padded to nt * 32 rows and BN columns
+    const int64_t kp = nt * kTK;
+    for (int64_t e = threadIdx.x; e < kp * BN; e += blockDim.x) {
+        const int64_t k = e / BN, c = e % BN;
+        Bs[((k >> 3) * BN + c) * 8 + (k & 7)] = (k < K && c < N) ? g.b1[k * g.ldb1 + c] : 0.0f;
+    }
+    __syncthreads();
+    if (!active) return;
+
+    v4f acc[2][NT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        if (kt + 2 < nt) fetch(kt + 2, a2);
+        float b[NT][8];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const float* src = Bs + ((kt * 4 + q) * BN + 16 * j + r) * 8;
+            const float4 x0 = *reinterpret_cast<const float4*>(src);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+            b[j][0] = x0.x; b[j][1] = x0.y; b[j][2] = x0.z; b[j][3] = x0.w;
+            b[j][4] = x1.x; b[j][5] = x1.y; b[j][6] = x1.z; b[j][7] = x1.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[i][s], b[j][s], acc[i][j],
+                                                                     0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                a0[i][t] = a1[i][t];
+                a1[i][t] = a2[i][t];
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t gn = 16 * j + r;
+            if (gn >= N) continue;
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t gm = m0 + 16 * i + 4 * q + rr;
+                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Elementwise and row epilogues
 // ---------------------------------------------------------------------------
 enum { OP_RELU = 0, OP_LEAKY = 1, OP_ELU = 2, OP_SIGMOID = 3, OP_TANH = 4, OP_GELU = 5 };
@@ -582,9 +781,14 @@ int resolve_gemm_algo(int algo, int64_t m, int64_t n, int64_t k) {
     // MFMA only where the product is a real contraction (wide n, deep k and
     // enough work to fill the chip); small products keep the bit-exact
     // in-order kernel.
-    if (algo == TG_GEMM_AUTO)
-        return (n >= 64 && k >= 32 && m * n * k >= (int64_t(1) << 32)) ? TG_GEMM_MFMA
-                                                                        : TG_GEMM_INORDER;
+    // A thin product (n < 64) takes MFMA when A alone is large (m k >= 2^25:
+    // config E's n x 256 x 41 layer-2 transforms, 212 us in order); Cora-scale
+    // products stay in order.
+    if (algo == TG_GEMM_AUTO) {
+        if (n >= 64) return (k >= 32 && m * n * k >= (int64_t(1) << 32)) ? TG_GEMM_MFMA
+                                                                          : TG_GEMM_INORDER;
+        return (k >= 32 && m * k >= (int64_t(1) << 25)) ? TG_GEMM_MFMA : TG_GEMM_INORDER;
+    }
     return algo;
 }
 
@@ -605,6 +809,39 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
     if (dual)
         require(g.b2 && g.lda2 >= g.k2 && g.ldb2 >= g.n, "matmul: bad second operand pair");
     algo = resolve_gemm_algo(algo, g.m, g.n, g.k1 + g.k2);
+    if (algo == TG_GEMM_MFMA && g.n <= 64) {
+        // thin: one wavefront per 64 rows, 16-column MFMA tiles up to n
+        const unsigned grid = static_cast<unsigned>(ceil_div(g.m, 256));
+        auto al4 = [](const float* p, int64_t ld) {
+            return p == nullptr || (ld % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0);
+        };
+        const bool aligned = al4(g.a1, g.lda1) && (!dual || al4(g.a2, g.lda2));
+        const int ntile = static_cast<int>(ceil_div(g.n, 16));
+        const int64_t panel = ceil_div(g.k1, kTK) * kTK * 16 * ntile;  // B floats in LDS
+        if (!dual && aligned && panel <= kThinLdsFloats) {
+            const unsigned lgrid = static_cast<unsigned>(ceil_div(g.m, kThinRows * kThinWaves));
+            const size_t lds = static_cast<size_t>(panel) * sizeof(float);
+#define TG_THIN_LDS_CASE(NT_)                                                                      \
+            if (ntile == NT_) {                                                                    \
+                gemm_mfma_thin_lds_kernel<NT_><<<lgrid, 64 * kThinWaves, lds, s>>>(g);             \
+                TG_LAUNCH_CHECK();                                                                 \
+                return;                                                                            \
+            }
+            TG_THIN_LDS_CASE(1) TG_THIN_LDS_CASE(2) TG_THIN_LDS_CASE(3) TG_THIN_LDS_CASE(4)
+#undef TG_THIN_LDS_CASE
+        }
+#define TG_THIN_CASE(NT_)                                                                  \
+        if (ntile == NT_) {                                                                \
+            if (aligned)                                                                   \
+                gemm_mfma_thin_kernel<NT_, true><<<grid, 256, 0, s>>>(g);                  \
+            else                                                                           \
+                gemm_mfma_thin_kernel<NT_, false><<<grid, 256, 0, s>>>(g);                 \
+            TG_LAUNCH_CHECK();                                                             \
+            return;                                                                        \
+        }
+        TG_THIN_CASE(1) TG_THIN_CASE(2) TG_THIN_CASE(3) TG_THIN_CASE(4)
+#undef TG_THIN_CASE
+    }
     if (algo == TG_GEMM_MFMA) {
         dim3 grid(static_cast<unsigned>(ceil_div(g.m, kMBM)),
                   static_cast<unsigned>(ceil_div(g.n, kMBN)));
