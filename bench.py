@@ -22,6 +22,9 @@ Default run (N=1):
     (gcn_norm / add_self_loops inside every forward), the reference's
     Model::forward timed once on the host cores, and the parity of the
     log-softmax logits against it (|err| <= 1e-5 + 1e-4|ref|, argmax).
+  * ``cora``: configs A/B/C (Cora-synth GCN / SAGE / GAT): microseconds per
+    forward, cached and with the reference's semantics, beside the compiled
+    reference at all host threads and at one, and raw-output parity;
   * ``ingest``: GraphLoader's CSV parsing on the device -- a 20M-line edge
     list and a 50,000 x 602 feature table -- with the text in HBM and through
     the file path, against the compiled reference's parser on a sample.
@@ -206,18 +209,123 @@ def run_spmm_d(args, torch, tg):
         del b, c
 
     head = results[args.f]
+    cpp = None
+    if not args.no_cpp_api:
+        cpp = cpp_api_spmm(torch, tg, a, rp, ci, val, b_full[:, :args.f].contiguous(), plan,
+                           args.steps)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_spmm(rp, ci, val, b_full[:, :args.f].contiguous().cpu().numpy(),
                                 args)
     return dict(m=m, nnz=nnz, max_deg=int(deg.max()), plan=info, results=results,
-                head=head, cpu=cpu, csr_build_ms=csr_ms)
+                head=head, cpu=cpu, csr_build_ms=csr_ms, cpp_api=cpp)
+
+
+def _tinygnn_pkg():
+    """The reference's Python surface (package ``tinygnn``: pybind
+    ``_tinygnn_core`` over this build's C++ API, libtinygnn.so)."""
+    pkg = os.path.join(ROOT, "tinygnn_amd")
+    if pkg not in sys.path:
+        sys.path.insert(0, pkg)
+    import tinygnn
+    return tinygnn
+
+
+def wall_ms_per_call(torch, fn, reps: int, warmup: int = 2) -> float:
+    """Wall milliseconds per call of fn over reps calls, the device
+    synchronised before and after the loop (each call's launches, host work
+    and allocation included)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / reps
+
+
+def _csr_view(n_rows, n_cols, rp, ci, val):
+    """The attributes Tensor.from_scipy_csr reads (shape, indptr, indices, data)."""
+    from types import SimpleNamespace
+    return SimpleNamespace(shape=(n_rows, n_cols), indptr=rp, indices=ci, data=val)
+
+
+def cpp_api_spmm(torch, tg, a, rp, ci, val, b, plan, reps):
+    """tinygnn::spmm(A, B) (the reference's ops.hpp:112, this build's
+    include/tinygnn/ops.hpp over libtinygnn.so) through the pybind module,
+    against the C-ABI call tg_spmm_execute on the same device data: wall ms
+    per call.  The C++ API returns a new tensor per call (value semantics);
+    the C-ABI call writes into a preallocated output.  Both reuse a plan (the
+    C++ API caches one per CSR tensor version).  The outputs must agree bit
+    for bit."""
+    T = _tinygnn_pkg()
+    m = a.n_rows
+    A = T.Tensor.from_scipy_csr(_csr_view(m, a.n_cols, rp, ci, val))
+    B = T.from_torch(b)
+    keep = [None]
+
+    def cpp():
+        keep[0] = T.spmm(A, B)
+
+    c = torch.empty((m, b.shape[1]), device=b.device)
+    cpp_ms = wall_ms_per_call(torch, cpp, reps)
+    cabi_ms = wall_ms_per_call(torch, lambda: tg.spmm(a, b, plan=plan, out=c), reps)
+    same = bool(torch.equal(T.to_torch(keep[0]).view(torch.int32), c.view(torch.int32)))
+    log(f"C++ API spmm: {cpp_ms:.3f} ms/call, C-ABI {cabi_ms:.3f} ms/call, bit-identical {same}")
+    del keep, A, B
+    return dict(cpp_api_ms_per_call=round(cpp_ms, 4), c_abi_ms_per_call=round(cabi_ms, 4),
+                ratio=round(cpp_ms / cabi_ms, 4), bit_identical=same, calls=reps)
+
+
+def cpp_api_model(torch, tg, spec, w, adj, rp, ci, val, x, y_cabi, reps):
+    """Model::forward (the reference's model.hpp:148) through the pybind
+    module over libtinygnn.so, against tg_model_forward through ctypes on the
+    same graph, features and weights (loaded from a TGNN weight file by the
+    C++ side): wall ms per cached forward (the C++ Model reuses the derived
+    adjacency while the tensor and its version are unchanged).  Outputs must
+    agree bit for bit with the C-ABI forward's."""
+    import tempfile
+    T = _tinygnn_pkg()
+    M = T.Model()
+    post = {0: T.Model.InterActivation.NONE, 1: T.Model.InterActivation.RELU,
+            2: T.Model.InterActivation.ELU}
+    act = {0: T.Activation.NONE, 1: T.Activation.RELU}
+    for l in spec:
+        if l["type"] == "gcn":
+            M.add_gcn_layer(l["in"], l["out"], True, act[l["act"]], post[l["post"]])
+        elif l["type"] == "sage":
+            M.add_sage_layer(l["in"], l["out"], T.SAGELayer.Aggregator.Mean, True,
+                             act[l["act"]], post[l["post"]])
+        else:
+            M.add_gat_layer(l["in"], l["out"], l["heads"], l["concat"], l["slope"], True,
+                            act[l["act"]], post[l["post"]])
+    fd, path = tempfile.mkstemp(suffix=".tgnn")
+    os.close(fd)
+    try:
+        tg.save_weight_file(path, w)
+        M.load_weights(path)
+    finally:
+        os.remove(path)
+    n = adj.n_rows
+    A = T.Tensor.from_scipy_csr(_csr_view(n, n, rp, ci, val))
+    X = T.from_torch(x)
+    keep = [None]
+
+    def cpp():
+        keep[0] = M.forward(A, X)
+
+    cpp_ms = wall_ms_per_call(torch, cpp, reps)
+    same = bool(torch.equal(T.to_torch(keep[0]).view(torch.int32), y_cabi.view(torch.int32)))
+    del keep, A, X, M
+    return cpp_ms, same
 
 
 def logit_parity(got, want):
     """|err| <= 1e-5 + 1e-4|want| elementwise, argmax agreement, and the
     number of nodes whose reference top-2 gap is within the largest error
-    (near-ties, where any non-bit-exact path may flip the argmax)."""
+    (near-ties, where any non-bit-exact path may flip the argmax).  Applied
+    to raw Model::forward outputs and to log-softmax logits alike."""
     err = np.abs(got.astype(np.float64) - want)
     tol = 1e-5 + 1e-4 * np.abs(want.astype(np.float64))
     top2 = np.sort(want, axis=1)[:, -2:]
@@ -227,12 +335,89 @@ def logit_parity(got, want):
                 argmax_mismatch=int((got.argmax(1) != want.argmax(1)).sum()), near_ties=ties)
 
 
-# HBM-gather roofline times at config E (8 TB/s, 157.3 TF/s): every gathered
-# row read from HBM once per nonzero, as the unblocked dataflows do (GCN and
-# GAT aggregate at F_out, SAGE runs transform-first).  The column-blocked
-# aggregations serve those gathers from L2, so the measured forwards can run
-# below these times (roofline_frac > 1).
-FORWARD_ROOFLINE_MS = {"gcn": 17.81, "sage": 18.18, "gat": 17.70}
+MFMA_PEAK_TFS = 157.3  # fp32 dense MFMA, MI355X
+
+
+def _gemm_cost(m, k, n):
+    """(bytes, flops) of C[m x n] = A[m x k] B[k x n], each operand once."""
+    return 4 * (m * k + k * n + m * n), 2 * m * n * k
+
+
+def _blocked_cost(n, nnz, f, nb, gc, values=False, self_term=False, score_heads=0):
+    """Compulsory L2 fills of one blocked aggregation (all its passes) of
+    width f over a structure of nnz entries cut into nb column blocks, with
+    lane groups of gc columns (g = ceil(f / gc) groups):
+      * the index stream (and values) once per column group: 4 nnz g (x2);
+      * the chunk descriptors once per column group and block: 16 n nb g;
+      * each block's slice of the gathered matrix once per XCD's L2:
+        8 x 4 n f (with f padded to whole 32-column tiles);
+      * the output read and written once per block after the first:
+        4 n f (2 nb - 1);
+      * a self term (SAGE) and score arrays (GAT) once: 4 n f, 8 x 4 n heads.
+    The gathers themselves (4 f bytes per entry) are served by L2 and are not
+    counted; they are what the passes spend their time on."""
+    g = -(-f // gc)
+    fpad = -(-f // 32) * 32
+    b = (4 * nnz * g * (2 if values else 1) + 16 * n * nb * g + 8 * 4 * n * fpad +
+         4 * n * f * (2 * nb - 1))
+    if self_term:
+        b += 4 * n * f
+    if score_heads:
+        b += 8 * 4 * n * score_heads
+    return b
+
+
+def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
+    """T_roof of the config-E cached forward in fast precision, over the
+    kernels of the dataflow the library ran (info = Model.blocking_info()):
+    sum over kernels of max(bytes / 8 TB/s, flops / 157.3 TFLOP/s), bytes as
+    _gemm_cost / _blocked_cost (the reference's SpMM cost model,
+    ops.cpp:186-191, where a pass is unblocked).  Returns (ms, per-kernel
+    list)."""
+    nnz_s = nnz_a + n
+    ks = []
+
+    def gemm(label, m, k, nn):
+        b, fl = _gemm_cost(m, k, nn)
+        ks.append((label, b, fl))
+
+    def agg(label, nnz, f, nb, gc, **kw):
+        if nb > 0:
+            ks.append((label, _blocked_cost(n, nnz, f, nb, gc, **kw), 2 * nnz * f))
+        else:  # unblocked: the reference's cost model
+            v = 0 if kw.get("values") is False else 4 * nnz
+            ks.append((label, 4 * (n + 1) + 4 * nnz + v + 4 * f * nnz + 4 * f * n, 2 * nnz * f))
+
+    if name == "gcn":
+        nb, gc = info["blocks_sl"], info["cols_sl"]
+        weighted = not (nb > 0 and gc == 32)  # factored GCN passes carry no values
+        gemm("L1 transform", n, f_in, hidden)
+        agg("L1 aggregation", nnz_s, hidden, nb, gc, values=weighted)
+        gemm("L2 transform", n, hidden, classes)
+        agg("L2 aggregation", nnz_s, classes, nb, gc, values=weighted)
+    elif name == "sage":
+        nb, gc = info["blocks_raw"], info["cols_raw"]
+        gemm("L1 transform [Ws|Wn]", n, f_in, 2 * hidden)
+        agg("L1 mean aggregation", nnz_a, hidden, nb, gc, values=False, self_term=True)
+        gemm("L2 transform [Ws|Wn]", n, hidden, 2 * 64)  # 41 + 41 padded to 64 + 64
+        agg("L2 mean aggregation", nnz_a, classes, nb, gc, values=False, self_term=True)
+    else:
+        nb, gc = info["blocks_sl"], info["cols_sl"]
+        for li, (fi, fo, h) in enumerate(((f_in, hidden, heads), (hidden * heads, classes, 1))):
+            gemm(f"L{li + 1} transform", n, fi, fo * h)
+            ks.append((f"L{li + 1} scores", 4 * n * fo * h + 8 * n * h, 4 * n * fo * h))
+            ks.append((f"L{li + 1} softmax statistics", 16 * n + 4 * nnz_s + 16 * n * h,
+                       4 * nnz_s * h))
+            agg(f"L{li + 1} attention aggregation", nnz_s, fo * h, nb, gc, values=False,
+                score_heads=h)
+    out, tot = [], 0.0
+    for label, b, fl in ks:
+        t = max(b / (HBM_PEAK_GBS * 1e6), fl / (MFMA_PEAK_TFS * 1e9))
+        tot += t
+        out.append(dict(kernel=label, bytes=int(b), flops=int(fl), t_roof_ms=round(t, 4),
+                        bound="hbm" if b / (HBM_PEAK_GBS * 1e6) >= fl / (MFMA_PEAK_TFS * 1e9)
+                        else "mfma"))
+    return tot, out
 
 
 def run_forward_e(args, torch, tg):
@@ -261,10 +446,12 @@ def run_forward_e(args, torch, tg):
             ref = oracle.reference()
             rp, ci, val = adj.to_numpy()
             t1 = time.time()
-            ref_tensors = (ref.csr(oracle.CSR(n, n, rp, ci, val)), ref.dense(x_h))
+            ref_csr = oracle.CSR(n, n, rp, ci, val)
+            ref_tensors = (ref.csr(ref_csr), ref.dense(x_h))
             log(f"reference tensors built in {time.time()-t1:.1f}s")
             del rp, ci, val
     out = {}
+    rp_e = ci_e = val_e = None
     for name, spec in specs.items():
         w = synth.model_weights(spec, seed=args.seed + 20)
         model = tg.Model.from_spec(spec, w)
@@ -279,7 +466,21 @@ def run_forward_e(args, torch, tg):
             timer.stop(e0)
         torch.cuda.synchronize()
         cached = float(np.median(timer.ms()))
-        # the timed (cached) forward's logits are the ones checked
+        blocking = model.blocking_info()
+        cpp = None
+        if not args.no_cpp_api:
+            reps = max(3, args.fwd_steps // 2)
+            cabi_wall = wall_ms_per_call(
+                torch, lambda: model.forward(adj, x, mode=tg.FORWARD_CACHED, out=y), reps)
+            if rp_e is None:
+                rp_e, ci_e, val_e = adj.to_numpy()
+            cpp_ms, same = cpp_api_model(torch, tg, spec, w, adj, rp_e, ci_e, val_e, x, y, reps)
+            cpp = dict(cpp_api_ms_per_call=round(cpp_ms, 3), c_abi_ms_per_call=round(cabi_wall, 3),
+                       ratio=round(cpp_ms / cabi_wall, 4), bit_identical=same, calls=reps)
+            log(f"{name}: C++ API Model::forward {cpp_ms:.2f} ms/call, C-ABI {cabi_wall:.2f} "
+                f"ms/call, bit-identical {same}")
+        # the timed (cached) forward's raw outputs and logits are the ones checked
+        raw = y.cpu().numpy()
         logits = tg.log_softmax_(y.clone()).cpu().numpy()
         timer = StreamTimer(torch, stream)
         for _ in range(3):
@@ -289,6 +490,7 @@ def run_forward_e(args, torch, tg):
             timer.stop(e0)
         torch.cuda.synchronize()
         refsem = float(np.median(timer.ms()))
+        raw_r = y.cpu().numpy()
         logits_r = tg.log_softmax_(y.clone()).cpu().numpy()
         # the same model in exact precision (the reference's operation order)
         model.set_precision(tg.PRECISION_EXACT)
@@ -304,10 +506,16 @@ def run_forward_e(args, torch, tg):
         raw_x = y.cpu().numpy()
         logits_x = tg.log_softmax_(y.clone()).cpu().numpy()
         model.set_precision(tg.PRECISION_FAST)
+        troof, kern = forward_roofline(name, n, adj.nnz, synth.E_FEATURES, 256 if name != "gat"
+                                       else 64, synth.E_CLASSES, 4, blocking)
         r = dict(gpu_ms=round(cached, 3), gpu_ms_reference_semantics=round(refsem, 3),
-                 gpu_ms_exact=round(exact_ms, 3),
-                 roofline_ms=FORWARD_ROOFLINE_MS[name],
-                 roofline_frac=round(FORWARD_ROOFLINE_MS[name] / cached, 4))
+                 cpp_api=cpp,
+                 gpu_ms_exact=round(exact_ms, 3), blocking=blocking,
+                 roofline_ms=round(troof, 4), roofline_frac=round(troof / cached, 4),
+                 roofline_kernels=kern,
+                 roofline_note="T_roof = sum over the dataflow's kernels of max(compulsory "
+                               "bytes / 8 TB/s, flops / 157.3 TF/s); blocked passes count "
+                               "their compulsory L2 fills, not the L2-served gathers")
         log(f"{name}: cached {cached:.2f} ms, reference semantics {refsem:.2f} ms, "
             f"exact {exact_ms:.2f} ms")
         if ref is not None:
@@ -316,8 +524,14 @@ def run_forward_e(args, torch, tg):
             want_raw = rm.forward_handles(ref_tensors[0], ref_tensors[1], n)
             cpu_ms = (time.perf_counter() - t1) * 1e3
             want = ref.activation("log_softmax", want_raw)
+            layers = ref_layer_only(ref, oracle.restate(), spec, w, ref_csr, x_h)
+            cpu_layers_ms = cpu_median_ms(layers, 1, warmup=0)
+            del layers
             r.update(cpu_ms=round(cpu_ms, 1), cpu_threads=ref.num_threads(),
+                     cpu_ms_layers=round(cpu_layers_ms, 1),
                      speedup=round(cpu_ms / cached, 1),
+                     parity_raw=logit_parity(raw, want_raw),
+                     parity_raw_reference_semantics=logit_parity(raw_r, want_raw),
                      parity=logit_parity(logits, want),
                      parity_reference_semantics=logit_parity(logits_r, want),
                      parity_exact=dict(
@@ -327,9 +541,172 @@ def run_forward_e(args, torch, tg):
             log(f"{name}: cpu {cpu_ms:.0f} ms ({ref.num_threads()} thr), parity {r['parity']}, "
                 f"exact {r['parity_exact']}")
             del rm, want, want_raw
+        del raw, raw_r
         out[name] = r
         del model, y
     return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)
+
+
+def host_info():
+    """The CPU the baselines ran on: model name, logical CPUs, the CPUs this
+    process may use, and OMP_NUM_THREADS."""
+    model = "?"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(cpu_model=model, nproc=os.cpu_count(), affinity=len(os.sched_getaffinity(0)),
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
+
+
+def cpu_median_ms(fn, reps: int, warmup: int = 1):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return float(np.median(ts))
+
+
+def ref_layer_only(ref, restate, spec, w, a, x):
+    """A closure timing only the reference's layer forwards of a 2-layer
+    model (layers.cpp:286-339, :538-752, :945-1129): the normalised / self-looped
+    adjacency, every layer's input and the weights are prepared beforehand, so
+    the per-call gcn_norm / add_self_loops and feature copy of Model::forward
+    (model.cpp:373-391) and the head concat are left out."""
+    import oracle
+    kinds = {l["type"] for l in spec}
+    a_gcn = ref.csr(restate.gcn_norm(a)) if "gcn" in kinds else None
+    a_sl = ref.csr(restate.add_self_loops(a)) if "gat" in kinds else None
+    a_raw = ref.csr(a)
+    calls, h = [], x
+    acsr = {"gcn": restate.gcn_norm(a) if a_gcn else None,
+            "gat": restate.add_self_loops(a) if a_sl else None}
+    for li, l in enumerate(spec):
+        p = f"layer{li}"
+        th = ref.dense(h)
+        if l["type"] == "gcn":
+            wt, b = oracle._f(w[p + ".weight"]), oracle._f(w[p + ".bias"])
+            out = np.zeros((a.n_rows, l["out"]), np.float32)
+            calls.append((ref.L.ref_gcn_layer, (a_gcn.h, th.h, l["in"], l["out"],
+                                                 oracle._ptr(wt), oracle._ptr(b), 1,
+                                                 l.get("act", 1), oracle._ptr(out)), (th, wt, b)))
+            h = restate.gcn_layer(acsr["gcn"], h, wt, b, l.get("act", 1))
+        elif l["type"] == "sage":
+            wn, ws = oracle._f(w[p + ".weight_neigh"]), oracle._f(w[p + ".weight_self"])
+            b = oracle._f(w[p + ".bias"])
+            out = np.zeros((a.n_rows, l["out"]), np.float32)
+            calls.append((ref.L.ref_sage_layer, (a_raw.h, th.h, l["in"], l["out"], 0,
+                                                  oracle._ptr(wn), oracle._ptr(ws),
+                                                  oracle._ptr(b), 1, l.get("act", 1),
+                                                  oracle._ptr(out)), (th, wn, ws, b)))
+            h = restate.sage_layer(a, h, wn, ws, b, l.get("act", 1))
+        else:
+            heads = []
+            for hd in range(l.get("heads", 1)):
+                hp = f"{p}.head{hd}"
+                wt, al, ar = (oracle._f(w[hp + k]) for k in (".weight", ".attn_left",
+                                                               ".attn_right"))
+                b = oracle._f(w[hp + ".bias"])
+                out = np.zeros((a.n_rows, l["out"]), np.float32)
+                calls.append((ref.L.ref_gat_layer, (a_sl.h, th.h, l["in"], l["out"],
+                                                     oracle._ptr(wt), oracle._ptr(al),
+                                                     oracle._ptr(ar), oracle._ptr(b),
+                                                     l.get("slope", 0.2), 1, l.get("act", 0),
+                                                     oracle._ptr(out)), (th, wt, al, ar, b)))
+                heads.append(restate.gat_layer(acsr["gat"], h, wt, al, ar, b,
+                                               l.get("slope", 0.2), l.get("act", 0)))
+            h = np.ascontiguousarray(np.concatenate(heads, axis=1)) if len(heads) > 1 else heads[0]
+            if l.get("post", 0) == 2:
+                h = restate.activation("elu", h, 1.0)
+    keep = (a_gcn, a_sl, a_raw)
+
+    def run():
+        for fn, argv, _ in calls:
+            ref._check(fn(*argv))
+    run.keep = (keep, calls)
+    return run
+
+
+def run_cora(args, torch, tg):
+    """Configs A/B/C: 2-layer GCN / SAGE-mean / GAT on the Cora-synth graph
+    (2,708 nodes, 10,858 entries, 1,433 features).  GPU: microseconds per
+    forward with cached preprocessing and with the reference's semantics
+    (HIP events on the stream around each forward, median of args.cora_steps
+    after 3 warm-ups).  Host: the compiled reference's Model::forward plus
+    the caller's log_softmax (test_e2e.cpp:316) at all OpenMP threads and at
+    one, and its layer-only time (median of 5).  Parity of the raw outputs
+    and of the logits against the reference's."""
+    from tinygnn_amd import synth
+    import oracle
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    src, dst, x_h = synth.cora_synth()
+    n = synth.CORA_NODES
+    adj = tg.edge_list_to_csr(torch.from_numpy(src).to(dev), torch.from_numpy(dst).to(dev), n)
+    x = torch.from_numpy(x_h).to(dev)
+    ref = restate = None
+    if not args.no_cpu and oracle.has_reference():
+        ref, restate = oracle.reference(), oracle.restate()
+        rp, ci, val = adj.to_numpy()
+        a = oracle.CSR(n, n, rp, ci, val)
+        ta, tx = ref.csr(a), ref.dense(x_h)
+    out = {}
+    for name, (spec, w) in synth.cora_models().items():
+        m = tg.Model.from_spec(spec, w)
+        y = torch.empty((n, m.output_cols()), device=dev)
+        r = {}
+        for mode, key in ((tg.FORWARD_CACHED, "gpu_us"),
+                          (tg.FORWARD_REFERENCE, "gpu_us_reference_semantics")):
+            for _ in range(3):
+                m.forward(adj, x, mode=mode, out=y)
+            torch.cuda.synchronize()
+            timer = StreamTimer(torch, stream)
+            for _ in range(args.cora_steps):
+                e0 = timer.start()
+                m.forward(adj, x, mode=mode, out=y)
+                timer.stop(e0)
+            torch.cuda.synchronize()
+            r[key] = round(float(np.median(timer.ms())) * 1e3, 1)
+        raw = y.cpu().numpy()
+        logits = tg.log_softmax_(y.clone()).cpu().numpy()
+        if ref is not None:
+            rm = ref.model(spec, w)
+            threads = ref.num_threads()
+
+            def fwd():
+                return ref.activation("log_softmax", rm.forward_handles(ta, tx, n))
+
+            r["cpu_us"] = round(cpu_median_ms(fwd, 5) * 1e3, 1)
+            ref.set_num_threads(1)
+            r["cpu_us_1thread"] = round(cpu_median_ms(fwd, 5) * 1e3, 1)
+            layers = ref_layer_only(ref, restate, spec, w, a, x_h)
+            r["cpu_us_layers_1thread"] = round(cpu_median_ms(layers, 5) * 1e3, 1)
+            ref.set_num_threads(threads)
+            r["cpu_us_layers"] = round(cpu_median_ms(layers, 5) * 1e3, 1)
+            r["cpu_threads"] = threads
+            r["speedup"] = round(r["cpu_us"] / r["gpu_us"], 1)
+            r["speedup_reference_semantics"] = round(r["cpu_us"] /
+                                                     r["gpu_us_reference_semantics"], 1)
+            want_raw = rm.forward_handles(ta, tx, n)
+            r["parity_raw"] = logit_parity(raw, want_raw)
+            r["raw_bit_identical_frac"] = float((raw.view(np.int32) ==
+                                                 want_raw.view(np.int32)).mean())
+            r["parity"] = logit_parity(logits, ref.activation("log_softmax", want_raw))
+            del rm, layers
+        log(f"cora {name}: gpu {r['gpu_us']} us cached, {r['gpu_us_reference_semantics']} us "
+            f"reference semantics; cpu {r.get('cpu_us')} us ({r.get('cpu_threads')} thr), "
+            f"{r.get('cpu_us_1thread')} us (1 thr); raw bit-identical "
+            f"{r.get('raw_bit_identical_frac')}")
+        out[name] = r
+        del m, y
+    return dict(n=n, nnz=adj.nnz, features=synth.CORA_FEATURES, models=out)
 
 
 def run_ingest(args, torch, tg):
@@ -469,9 +846,30 @@ def cpu_baseline_spmm(rp, ci, val, b, args):
     nbytes = spmm_bytes(r, nnz_s, f)
     log(f"cpu baseline ({kind}, {cores} threads): rows [0,{r}) nnz {nnz_s}: "
         f"{med*1e3:.1f} ms -> {nbytes/med/1e9:.1f} GB/s")
+    # one thread, on the first tenth of the same sample
+    r1 = max(1, int(np.searchsorted(rp, nnz_s // 10)))
+    nnz1 = int(rp[r1])
+    sub1 = oracle.CSR(r1, m, rp[:r1 + 1].copy(), ci[:nnz1].copy(), val[:nnz1].copy())
+    lib.set_num_threads(1)
+    if kind == "reference":
+        import ctypes
+        t1a = lib.csr(sub1)
+        out1 = np.zeros((r1, f), np.float32)
+        med1 = cpu_median_ms(lambda: lib._check(lib.L.ref_spmm(
+            t1a.h, tb.h, out1.ctypes.data_as(ctypes.c_void_p))), 3) / 1e3
+    else:
+        med1 = cpu_median_ms(lambda: lib.spmm(sub1, b), 3) / 1e3
+    lib.set_num_threads(cores)
+    g1 = spmm_bytes(r1, nnz1, f) / med1 / 1e9
+    log(f"cpu baseline ({kind}, 1 thread): rows [0,{r1}) nnz {nnz1}: {med1*1e3:.1f} ms -> "
+        f"{g1:.2f} GB/s")
     return dict(value=nbytes / med / 1e9, unit="GB/s", cores=cores, kind=kind,
                 sample=f"spmm rows [0,{r}) of the config-D matrix ({nnz_s} nnz) x full B "
-                       f"(F={f}); median of {len(times)} calls, {med*1e3:.1f} ms each")
+                       f"(F={f}); median of {len(times)} calls, {med*1e3:.1f} ms each",
+                one_thread=dict(value=round(g1, 3), unit="GB/s", cores=1,
+                                sample=f"rows [0,{r1}) ({nnz1} nnz), median of 3, "
+                                       f"{med1*1e3:.1f} ms each"),
+                host=host_info())
 
 
 def main():
@@ -492,6 +890,10 @@ def main():
     ap.add_argument("--fwd-steps", type=int, default=10)
     ap.add_argument("--fwd-warmup", type=int, default=2)
     ap.add_argument("--no-ingest", action="store_true", help="skip the CSV ingestion leg")
+    ap.add_argument("--no-cora", action="store_true", help="skip the Cora-synth (A/B/C) leg")
+    ap.add_argument("--no-cpp-api", action="store_true",
+                    help="skip timing the C++ API (tinygnn::spmm, Model::forward) beside the C-ABI")
+    ap.add_argument("--cora-steps", type=int, default=20)
     ap.add_argument("--ingest-edges", type=int, default=20_000_000)
     ap.add_argument("--ingest-rows", type=int, default=50_000)
     ap.add_argument("--ingest-steps", type=int, default=5)
@@ -525,12 +927,13 @@ def main():
         del xc, yc
     fwd = None if args.no_forward else run_forward_e(args, torch, tg)
     torch.cuda.empty_cache()
+    cora = None if args.no_cora else run_cora(args, torch, tg)
     ingest = None if args.no_ingest else run_ingest(args, torch, tg)
     if r is None:
         print(json.dumps({"metric": "CSR SpMM GB/s & % HBM peak; forward ms at 233K nodes / "
                                     "114.6M edges", "value": None, "unit": "GB/s",
                           "note": "--no-spmm: the SpMM leg was skipped", "forward": fwd,
-                          "ingest": ingest}), flush=True)
+                          "cora": cora, "ingest": ingest, "host": host_info()}), flush=True)
         return
     head = r["head"]
     line = {
@@ -566,9 +969,12 @@ def main():
                    "pct_hbm_peak": round(100 * v["kernel_gbs"] / HBM_PEAK_GBS, 2)}
                   for v in r["results"].values()],
         "cpu_baseline": r["cpu"],
+        "cpp_api_spmm": r["cpp_api"],
         "csr_build_ms": round(r["csr_build_ms"], 2),
         "forward": fwd,
+        "cora": cora,
         "ingest": ingest,
+        "host": host_info(),
     }
     print(json.dumps(line), flush=True)
 

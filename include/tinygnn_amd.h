@@ -345,6 +345,12 @@ int tg_model_forward(tg_model_t model, int64_t n, int64_t nnz,
                      int64_t f_in, const float* x, float* out, int mode,
                      tg_stream_t stream);
 int tg_model_invalidate(tg_model_t model);
+/* The column blocking of the cached adjacency state (diagnostics; no
+ * counterpart in the reference): blocks and columns per lane group of A + I's
+ * blocked copy (GCN, GAT) and of A's (SAGE mean); 0 blocks = unblocked or no
+ * cached state.  Filled by the last forward. */
+int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
+                           int64_t* blocks_raw, int64_t* cols_raw);
 
 /* ------------------------------------------------------------------------
  * CSV ingestion -- replaces GraphLoader::parse_edges / parse_features and

@@ -11,14 +11,7 @@ def cora_inputs() -> dict:
     """Configs A/B/C: the Cora-synth graph, features and the three model
     stacks with their Glorot weights (zero biases)."""
     src, dst, x = synth.cora_synth()
-    f, c = synth.CORA_FEATURES, synth.CORA_CLASSES
-    specs = {
-        "gcn": synth.spec_gcn(f, 16, c),
-        "sage": synth.spec_sage(f, 64, c),
-        "gat": synth.spec_gat(f, 8, 8, c),
-    }
-    weights = {k: (s, synth.model_weights(s, seed=100 + i)) for i, (k, s) in
-               enumerate(sorted(specs.items()))}
+    weights = synth.cora_models()
     return {"src": src, "dst": dst, "x": x, "weights": weights}
 
 

@@ -410,6 +410,14 @@ class Model:
         unit-valued A + I -- on graphs dense enough to pay)."""
         lib.check(lib.tg_model_set_blocking(self.h, rows_per_block))
 
+    def blocking_info(self) -> dict:
+        """The column blocking the last forward used (tg_model_blocking_info):
+        blocks and lane-group columns of A + I's and A's blocked copies."""
+        v = [C.c_int64() for _ in range(4)]
+        lib.check(lib.tg_model_blocking_info(self.h, *[C.byref(x) for x in v]))
+        return dict(blocks_sl=v[0].value, cols_sl=v[1].value, blocks_raw=v[2].value,
+                    cols_raw=v[3].value)
+
     def invalidate(self) -> None:
         """Forgets the cached adjacency state (tg_model_invalidate)."""
         self._adj_key = None

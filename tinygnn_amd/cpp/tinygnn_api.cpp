@@ -2,7 +2,8 @@
 // graph_loader) over the C-ABI of libtinygnn_amd.so.
 //
 // Everything numeric happens on the device through tg_* calls on the
-// default HIP stream; this file holds the host-side contract of the
+// default (null) HIP stream, with temporaries from the stream-ordered
+// allocator on that stream; this file holds the host-side contract of the
 // reference: value-semantics tensors, argument validation with the
 // reference's exception types and messages (file:line cited per check), and
 // the coherence of host views with the device copies.
@@ -38,31 +39,43 @@ void check(int status) {
     throw std::runtime_error(msg);
 }
 
+// Device buffers come from the stream-ordered allocator on the null stream,
+// the stream every op of this API runs on: a buffer released while kernels
+// that use it are still queued is only reused by work queued after them, so
+// no release waits for the device.  The device's default pool keeps freed
+// memory (release threshold raised once per device), so a warm loop of ops
+// allocates without calling into the driver.
+void prepare_pool() {
+    static bool done[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
+    hipMemPool_t pool = nullptr;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess && pool) {
+        uint64_t keep = ~uint64_t(0);
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
+    done[dev] = true;
+}
+
 struct DevBuf {
     void* p = nullptr;
     size_t n = 0;
     DevBuf() = default;
     DevBuf(const DevBuf&) = delete;
     DevBuf& operator=(const DevBuf&) = delete;
-    // Buffers are released only after the device is idle: a temporary may
-    // die while a kernel launched on it is still running.
-    ~DevBuf() {
-        if (p) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(p);
-        }
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFreeAsync(p, nullptr);
+        p = nullptr;
+        n = 0;
     }
     void ensure(size_t bytes) {
         if (bytes <= n && p) return;
-        if (p) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(p);
-        }
-        p = nullptr;
-        n = 0;
+        release();
         if (bytes == 0) bytes = 4;
-        hipError_t e = hipMalloc(&p, bytes);
-        if (e != hipSuccess) hip_fail(e, "hipMalloc");
+        prepare_pool();
+        hipError_t e = hipMallocAsync(&p, bytes, nullptr);
+        if (e != hipSuccess) hip_fail(e, "hipMallocAsync");
         n = bytes;
     }
 };
@@ -781,8 +794,7 @@ Tensor GATLayer::forward(const Tensor& A, const Tensor& H) const {
                            activation_ == Activation::ReLU ? TG_ACT_RELU : TG_ACT_NONE,
                            TG_POST_NONE, 1, out.device_data_mutable(), i64(f), nullptr, 0,
                            nullptr));
-    detail::sync();  // `scores` and `wh` are released on return
-    return out;
+    return out;  // `scores` and `wh` are released in stream order
 }
 
 // ===========================================================================

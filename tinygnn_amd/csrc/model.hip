@@ -698,6 +698,19 @@ int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block) {
     });
 }
 
+int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
+                           int64_t* blocks_raw, int64_t* cols_raw) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        const tg::BlockedCSR* sl = model->have_cache ? model->blk_sl.get() : nullptr;
+        const tg::BlockedCSR* raw = model->have_cache ? model->blk_raw.get() : nullptr;
+        if (blocks_sl) *blocks_sl = sl ? sl->n_blocks : 0;
+        if (cols_sl) *cols_sl = sl ? sl->group_cols : 0;
+        if (blocks_raw) *blocks_raw = raw ? raw->n_blocks : 0;
+        if (cols_raw) *cols_raw = raw ? raw->group_cols : 0;
+    });
+}
+
 int tg_model_invalidate(tg_model_t model) {
     return guard([&] {
         require(model != nullptr, "model is null");

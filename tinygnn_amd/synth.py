@@ -195,6 +195,16 @@ def spec_gat(f_in, hidden, heads, classes):
                  slope=0.2, act=0, post=0)]
 
 
+def cora_models() -> dict:
+    """Configs A/B/C on the Cora-synth graph: name -> (spec, Glorot weights
+    with zero biases), GCN 1433->16->7, SAGE-mean 1433->64->7, GAT 8 x 8
+    concat + ELU -> 1 x 7 (the golden fixtures' seeds)."""
+    f, c = CORA_FEATURES, CORA_CLASSES
+    specs = {"gcn": spec_gcn(f, 16, c), "sage": spec_sage(f, 64, c), "gat": spec_gat(f, 8, 8, c)}
+    return {k: (sp, model_weights(sp, seed=100 + i))
+            for i, (k, sp) in enumerate(sorted(specs.items()))}
+
+
 # ---------------------------------------------------------------------------
 # CSV texts for the ingestion benchmark (GraphLoader's formats,
 # graph_loader.hpp:26-35), generated with vectorised byte arithmetic.
