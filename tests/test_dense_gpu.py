@@ -23,7 +23,9 @@ def _t(gpu, x):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (5, 3, 7), (37, 41, 16), (130, 602, 41),
                                    (64, 1433, 16), (300, 256, 41), (257, 17, 64),
-                                   (100, 64, 7), (513, 33, 300)])
+                                   (100, 64, 7), (513, 33, 300),
+                                   # above 2^21 outputs: the large in-order kernels
+                                   (9000, 40, 300), (70000, 33, 31), (300000, 9, 8)])
 def test_matmul_inorder_bitexact(gpu, restate, m, k, n):
     import tinygnn_amd as tg
     rng = np.random.default_rng(m * 31 + k * 7 + n)

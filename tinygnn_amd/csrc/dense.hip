@@ -141,6 +141,104 @@ __global__ __launch_bounds__(256) void gemm_inorder_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// In-order GEMM for small products (bit-exact; m n <= 2^21, e.g. the
+// Cora-scale transforms): one output per thread, a workgroup covers BM x BN
+// outputs (BM = 256 / BN), so a 2,708-row product gets 170-680 workgroups
+// instead of 11-22, and the k loop runs over 64-wide tiles with the next
+// tile loaded into registers while the current one is consumed from LDS.
+// Each output is one fma chain over k ascending from 0 (padded k is never
+// accumulated); DUAL interleaves the pairs per k and applies the scalar tail
+// exactly as gemm_inorder_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kSBK = 64;
+
+template <int BN, bool DUAL>
+__global__ __launch_bounds__(256) void gemm_inorder_small_kernel(GemmArgs g) {
+    constexpr int BM = 256 / BN;
+    constexpr int NP = DUAL ? 2 : 1;
+    constexpr int LA = BM * kSBK / 256;  // A values per thread per tile
+    constexpr int LB = kSBK * BN / 256;  // B values per thread per tile
+    static_assert(LA >= 1 && LB >= 1, "tile shape");
+    __shared__ float As[2][NP][kSBK][BM];
+    __shared__ float Bs[2][NP][kSBK][BN];
+    const int tx = threadIdx.x % BN, ty = threadIdx.x / BN;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * BM;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * BN;
+    const int64_t M = g.m, N = g.n, K = g.k1;
+    const int64_t nt = (K + kSBK - 1) / kSBK;
+    const bool tail = DUAL && g.tail_from >= 0 && (n0 + tx) >= g.tail_from;
+
+    float ra[NP][LA], rb[NP][LB];
+    auto fetch = [&](int64_t kt) {
+        const int64_t k0 = kt * kSBK;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float* A = p ? g.a2 : g.a1;
+            const float* B = p ? g.b2 : g.b1;
+            const int64_t lda = p ? g.lda2 : g.lda1;
+            const int64_t ldb = p ? g.ldb2 : g.ldb1;
+#pragma unroll
+            for (int t = 0; t < LA; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                const int64_t gm = m0 + e / kSBK, gk = k0 + e % kSBK;
+                ra[p][t] = (gm < M && gk < K) ? A[gm * lda + gk] : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < LB; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                const int64_t gk = k0 + e / BN, gn = n0 + e % BN;
+                rb[p][t] = (gk < K && gn < N) ? B[gk * ldb + gn] : 0.0f;
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+#pragma unroll
+            for (int t = 0; t < LA; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                As[buf][p][e % kSBK][e / kSBK] = ra[p][t];
+            }
+#pragma unroll
+            for (int t = 0; t < LB; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                Bs[buf][p][e / BN][e % BN] = rb[p][t];
+            }
+        }
+    };
+
+    float acc = 0.0f;
+    if (nt > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        const int cb = static_cast<int>(kt & 1);
+        if (kt + 1 < nt) fetch(kt + 1);
+        const int64_t k0 = kt * kSBK;
+        const int kmax = static_cast<int>(K - k0 < kSBK ? K - k0 : kSBK);
+        for (int kk = 0; kk < kmax; ++kk) {
+            const float a = As[cb][0][kk][ty], b = Bs[cb][0][kk][tx];
+            if constexpr (DUAL) {
+                const float a2 = As[cb][NP - 1][kk][ty], b2 = Bs[cb][NP - 1][kk][tx];
+                if (tail) {
+                    acc = acc + __builtin_fmaf(a, b, a2 * b2);
+                } else {
+                    acc = __builtin_fmaf(a2, b2, __builtin_fmaf(a, b, acc));
+                }
+            } else {
+                acc = __builtin_fmaf(a, b, acc);
+            }
+        }
+        if (kt + 1 < nt) stage(cb ^ 1);
+        __syncthreads();
+    }
+    const int64_t gm = m0 + ty, gn = n0 + tx;
+    if (gm < M && gn < N) g.c[c_index(g, gm, gn)] = epi_out(g, acc, gm, gn);
+}
+
+// ---------------------------------------------------------------------------
 // Wide in-order GEMM (bit-exact, n > 32): 128x128 workgroup tile, an 8x8
 // register micro-tile per thread, BK = 8, two LDS buffers with register
 // prefetch.  Each output is still one fma chain over k ascending from 0 (the
@@ -721,8 +819,25 @@ void launch_inorder(const GemmArgs& g, hipStream_t s) {
     TG_LAUNCH_CHECK();
 }
 
+template <int BN, bool DUAL>
+void launch_inorder_small(const GemmArgs& g, hipStream_t s) {
+    dim3 grid(static_cast<unsigned>(ceil_div(g.m, 256 / BN)),
+              static_cast<unsigned>(ceil_div(g.n, BN)));
+    gemm_inorder_small_kernel<BN, DUAL><<<grid, 256, 0, s>>>(g);
+    TG_LAUNCH_CHECK();
+}
+
 template <bool DUAL>
 void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
+    // Small products (m n <= 2^21): one output per thread, many workgroups
+    // (Cora-scale GCN / SAGE / GAT forwards); the kernels below give such
+    // products a few dozen workgroups at most.
+    if (g.m * g.n <= (int64_t(1) << 21)) {
+        if (g.n <= 8) return launch_inorder_small<8, DUAL>(g, s);
+        if (g.n <= 16) return launch_inorder_small<16, DUAL>(g, s);
+        if (g.n <= 32) return launch_inorder_small<32, DUAL>(g, s);
+        return launch_inorder_small<64, DUAL>(g, s);
+    }
     if (g.n > 32) {
         // the 8x8 register-blocked kernel; 128-bit A loads when rows allow
         auto aligned = [](const float* p, int64_t ld) {
