@@ -402,14 +402,18 @@ def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
         gemm("L2 transform [Ws|Wn]", n, hidden, 2 * 64)  # 41 + 41 padded to 64 + 64
         agg("L2 mean aggregation", nnz_a, classes, nb, gc, values=False, self_term=True)
     else:
+        # fast precision: the softmax rides along the blocked passes (a
+        # running (max, sum) per row and head, read and written per pass);
+        # unblocked, one online-softmax pass
         nb, gc = info["blocks_sl"], info["cols_sl"]
         for li, (fi, fo, h) in enumerate(((f_in, hidden, heads), (hidden * heads, classes, 1))):
             gemm(f"L{li + 1} transform", n, fi, fo * h)
             ks.append((f"L{li + 1} scores", 4 * n * fo * h + 8 * n * h, 4 * n * fo * h))
-            ks.append((f"L{li + 1} softmax statistics", 16 * n + 4 * nnz_s + 16 * n * h,
-                       4 * nnz_s * h))
             agg(f"L{li + 1} attention aggregation", nnz_s, fo * h, nb, gc, values=False,
                 score_heads=h)
+            if nb > 0:
+                lbl, b, fl = ks[-1]
+                ks[-1] = (lbl, b + 8 * n * h * (2 * nb - 1), fl)
     out, tot = [], 0.0
     for label, b, fl in ks:
         t = max(b / (HBM_PEAK_GBS * 1e6), fl / (MFMA_PEAK_TFS * 1e9))

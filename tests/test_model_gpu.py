@@ -586,3 +586,35 @@ def test_cached_forward_follows_adjacency(gpu, restate):
     w2 = synth.model_weights(spec2, seed=4)
     m.load_weights(w2)
     check("after layers were added", spec2, w2)
+
+
+@pytest.mark.parametrize("blocking", [1500, 500])
+def test_blocked_gat_online_split_rows(gpu, restate, blocking):
+    """Fast blocked GAT carries the softmax across the passes: rows whose
+    segment in a block is longer than one plan chunk (1,024 entries) are
+    merged from per-chunk (max, sum, partial) triples with the state the
+    earlier passes left; 2 and 6 blocks (middle passes included).  Within
+    tolerance of the oracle and of the unblocked fast path."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(71)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=20, max_deg=9000, empty_frac=0.02)
+    # some row's segment in a block exceeds one chunk (uniform columns)
+    assert np.diff(a.row_ptr).max() > 1024 * -(-n // blocking)
+    spec = synth.spec_gat(24, 64, 2, 5)
+    w = synth.model_weights(spec, seed=13)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = rng.standard_normal(w[k].shape).astype(np.float32)
+    x = rng.standard_normal((n, 24)).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = {}
+    for blk in (blocking, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(blk)
+        outs[blk] = m.forward(da, _t(gpu, x), mode=tg.FORWARD_CACHED).cpu().numpy()
+        if blk:
+            assert m.blocking_info()["blocks_sl"] == -(-n // blocking)
+        assert_close(outs[blk], want, what=f"blocking={blk}")
+    assert_close(outs[blocking], outs[0], what="online blocked vs unblocked")

@@ -710,6 +710,299 @@ __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __rest
     rinv[static_cast<int64_t>(sp.x) * heads + h] = (s > 0.0f) ? 1.0f / s : 0.0f;
 }
 
+// ---------------------------------------------------------------------------
+// Blocked GAT passes with the softmax carried across the passes (fast
+// precision): no statistics sweep.  Every (row, head) keeps a running max m
+// and a running sum s of exp(e - m) in state arrays [n x heads], and the
+// output row holds the unnormalised sum of exp(e_ij - m) Wh_j over the
+// blocks so far.  A pass raises m to the maximum of its entries' scores,
+// rescaling the carried sum and output by exp(m_old - m_new) (the online
+// softmax of gat_chunk_kernel, across blocks); the last pass multiplies by
+// 1/s and applies bias and activations.  One lane group of LPR lanes (VEC 4
+// floats each) covers one head's columns of one chunk, so (row, head) state
+// has a single owner per pass; rows split into several chunks leave
+// per-chunk (m, s, sum) partials, merged with the state by
+// gat_online_reduce_kernel.
+// ---------------------------------------------------------------------------
+struct GatPass {
+    const float* src;  // [n x heads] a_l . Wh_i
+    const float* dst;  // [n x heads] a_r . Wh_j
+    float* m_state;    // [n x heads] running max
+    float* s_state;    // [n x heads] running sum
+    float* pstats;     // [partial slots x heads x 2] (m, s) of split rows' chunks
+    const float* bias;
+    int heads;
+    int head_cols;
+    float slope;
+    int act, post;
+    int first, last;   // the pass's position among the blocks
+    int vec_io;        // output rows 16-byte aligned: vector loads / stores
+};
+
+__device__ __forceinline__ void ld4_nt(const float* p, float (&x)[4]) {
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    const v4 t = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
+    x[0] = t.x;
+    x[1] = t.y;
+    x[2] = t.z;
+    x[3] = t.w;
+}
+
+__device__ __forceinline__ void st4_nt(float* p, const float (&x)[4]) {
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    v4 t;
+    t.x = x[0];
+    t.y = x[1];
+    t.z = x[2];
+    t.w = x[3];
+    __builtin_nontemporal_store(t, reinterpret_cast<v4*>(p));
+}
+
+// The output row's four floats at fo (those below f), vector or element-wise.
+__device__ __forceinline__ void out_load(const float* row, int64_t fo, int64_t f, bool vec,
+                                         float (&x)[4]) {
+    if (vec) {
+        ld4_nt(row + fo, x);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) x[k] = fo + k < f ? row[fo + k] : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void out_store(float* row, int64_t fo, int64_t f, bool vec,
+                                          const float (&x)[4]) {
+    if (vec) {
+        st4_nt(row + fo, x);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (fo + k < f) row[fo + k] = x[k];
+    }
+}
+
+template <int LPR>
+__global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
+    const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
+    const float* __restrict__ B, int64_t ldb, float* __restrict__ C, int64_t ldc,
+    float* __restrict__ partials, int64_t ldp, int64_t f, GatPass P) {
+    constexpr int U = 16;                    // row gathers in flight per lane
+    constexpr int CPL = U > LPR ? U / LPR : 1;
+    constexpr int BE = LPR * CPL;            // entries per batch (== U)
+    static_assert(BE == U, "one gather step per batch");
+    constexpr int GPB = 256 / LPR;
+    constexpr int TILE = LPR * 4;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (cid >= n_chunks) return;
+    const int4 ch = chunks[cid];
+    const int e = ch.z;
+    // a middle pass leaves rows without entries in its block as they are
+    if (!P.first && !P.last && ch.z == ch.y) return;
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+    const int h = static_cast<int>(fbase / P.head_cols);
+    const int64_t so = static_cast<int64_t>(ch.x) * P.heads + h;
+    const float si = P.src[so];
+    const float* dh = P.dst + h;
+    const int64_t fo = fbase + static_cast<int64_t>(l) * 4;
+    const bool ok = fo < f;
+    const int64_t fl = ok ? fo : fbase;  // lanes past f gather the tile's first vector
+    float* crow = C + static_cast<int64_t>(ch.x) * ldc;
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, s = 0.0f;  // s: this lane's share of the running sum
+    const bool unsplit = ch.w < 0;
+    if (unsplit && !P.first) {
+        m = P.m_state[so];
+        if (l == 0) s = P.s_state[so];  // the carried sum, counted once in the group
+        if (ok) out_load(crow, fo, f, P.vec_io, acc);
+    }
+
+    const char* bl = reinterpret_cast<const char*>(B + fl);
+    const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
+    const int stride = P.heads;
+    int ncl[CPL];
+    auto fetch = [&](int base) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int idx = base + l * CPL + j;
+            ncl[j] = idx < e ? ci[idx] : 0;
+        }
+    };
+    fetch(ch.y);
+    for (int base = ch.y; base < e; base += BE) {
+        int cl[CPL];
+        float d[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            cl[j] = ncl[j];
+            d[j] = dh[static_cast<int64_t>(cl[j]) * stride];  // before the row gathers
+        }
+        const int cnt = e - base < BE ? e - base : BE;
+        float bv[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int col = __shfl(cl[u % CPL], u / CPL, LPR);
+            const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
+            ldv<4>(reinterpret_cast<const float*>(bl + off), bv[u]);
+        }
+        fetch(base + BE);
+        // the batch's scores, the group's maximum, the rescaled carry
+        float ev[CPL];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            ev[j] = lrelu(si + d[j], P.slope);
+            if (base + l * CPL + j < e) bm = (bm < ev[j]) ? ev[j] : bm;
+        }
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(bm, off, LPR);
+            bm = (bm < o) ? o : bm;
+        }
+        if (m < bm) {  // uniform in the group
+            const float fct = expf(m - bm);  // 0 when nothing was carried (m = -inf)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] *= fct;
+            s *= fct;
+            m = bm;
+        }
+        float wl[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            wl[j] = base + l * CPL + j < e ? expf(ev[j] - m) : 0.0f;
+            s += wl[j];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float w = __shfl(wl[u % CPL], u / CPL, LPR);
+            const bool valid = u < cnt;  // a select, not a branch
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float nx = __builtin_fmaf(w, bv[u][k], acc[k]);
+                acc[k] = valid ? nx : acc[k];
+            }
+        }
+    }
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, LPR);
+
+    if (!unsplit) {
+        if (ok) stv<4>(partials + static_cast<int64_t>(ch.w) * ldp + fo, acc);
+        if (l == 0) {
+            float* st = P.pstats + (static_cast<int64_t>(ch.w) * P.heads + h) * 2;
+            st[0] = m;
+            st[1] = s;
+        }
+        return;
+    }
+    if (P.last) {
+        const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+        float x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            x[k] = finish_val(acc[k] * inv, P.bias, fo + k < f ? fo + k : fo, P.act, P.post);
+        if (ok) out_store(crow, fo, f, P.vec_io, x);
+        return;
+    }
+    if (ok) out_store(crow, fo, f, P.vec_io, acc);
+    if (l == 0) {
+        P.m_state[so] = m;
+        P.s_state[so] = s;
+    }
+}
+
+// Split rows of a pass: the state carried from the earlier passes and the
+// chunks' (m_c, s_c, sum_c) merged into M = max, S = sum s exp(m - M), out =
+// sum sum_c exp(m_c - M); the last pass normalises and applies the epilogue.
+template <int LPR>
+__global__ __launch_bounds__(256) void gat_online_reduce_kernel(
+    const int4* __restrict__ split, int64_t n_split, const float* __restrict__ partials,
+    int64_t ldp, float* __restrict__ C, int64_t ldc, int64_t f, GatPass P) {
+    constexpr int GPB = 256 / LPR;
+    constexpr int TILE = LPR * 4;
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t sid = static_cast<int64_t>(blockIdx.x) * GPB + g;
+    if (sid >= n_split) return;
+    const int4 sp = split[sid];
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
+    const int h = static_cast<int>(fbase / P.head_cols);
+    const int64_t so = static_cast<int64_t>(sp.x) * P.heads + h;
+    const int64_t fo = fbase + static_cast<int64_t>(l) * 4;
+    const bool ok = fo < f;
+    float* crow = C + static_cast<int64_t>(sp.x) * ldc;
+    float mp = -INFINITY, sprev = 0.0f, prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (!P.first) {
+        mp = P.m_state[so];
+        sprev = P.s_state[so];
+        if (ok) out_load(crow, fo, f, P.vec_io, prev);
+    }
+    float M = mp;
+    for (int c = 0; c < sp.z; ++c) {
+        const float mc = P.pstats[(static_cast<int64_t>(sp.y + c) * P.heads + h) * 2];
+        M = (M < mc) ? mc : M;
+    }
+    const float fp = expf(mp - M);  // 0 when nothing was carried
+    float S = sprev * fp, acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = prev[k] * fp;
+    for (int c = 0; c < sp.z; ++c) {
+        const float* st = P.pstats + (static_cast<int64_t>(sp.y + c) * P.heads + h) * 2;
+        const float fc = expf(st[0] - M);
+        S += st[1] * fc;
+        if (ok) {
+            float t[4];
+            ldv<4>(partials + static_cast<int64_t>(sp.y + c) * ldp + fo, t);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(t[k], fc, acc[k]);
+        }
+    }
+    if (P.last) {
+        const float inv = S > 0.0f ? 1.0f / S : 0.0f;
+        float x[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            x[k] = finish_val(acc[k] * inv, P.bias, fo + k < f ? fo + k : fo, P.act, P.post);
+        if (ok) out_store(crow, fo, f, P.vec_io, x);
+        return;
+    }
+    if (ok) out_store(crow, fo, f, P.vec_io, acc);
+    if (l == 0) {
+        P.m_state[so] = M;
+        P.s_state[so] = S;
+    }
+}
+
+template <int LPR>
+void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t ldwh,
+                       float* out, int64_t ldo, const GatPass& base, int64_t max_partials,
+                       hipStream_t s) {
+    constexpr int GPB = 256 / LPR;
+    const int64_t ldp = round_up(f, 4);
+    const unsigned ytiles = static_cast<unsigned>(ceil_div(f, LPR * 4));
+    for (int64_t blk = 0; blk < bk.n_blocks; ++blk) {
+        const tg_spmm_plan_s& p = *bk.plans[blk];
+        require(p.n_partials <= max_partials, "GATLayer: block plan has more partial slots");
+        GatPass P = base;
+        P.first = blk == 0;
+        P.last = blk + 1 == bk.n_blocks;
+        if (p.n_chunks > 0) {
+            dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)), ytiles);
+            gat_online_chunk_kernel<LPR><<<grid, 256, 0, s>>>(
+                p.chunks.as<int4>(), p.n_chunks, bk.bci.as<int32_t>(), wh, ldwh, out, ldo,
+                p.partials.as<float>(), ldp, f, P);
+            TG_LAUNCH_CHECK();
+        }
+        if (p.n_split > 0) {
+            dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)), ytiles);
+            gat_online_reduce_kernel<LPR><<<grid, 256, 0, s>>>(
+                p.split.as<int4>(), p.n_split, p.partials.as<float>(), ldp, out, ldo, f, P);
+            TG_LAUNCH_CHECK();
+        }
+    }
+}
+
 size_t gat_ws(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
     Carver c(nullptr, 0);
     c.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
@@ -820,6 +1113,37 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
     require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
     if (n == 0) return;
+    // fast precision, each head inside one lane group's columns and Wh rows
+    // 16-byte aligned: the softmax rides along the passes (no statistics
+    // sweep); the lane-group width is the one run_aggregate_blocked picks
+    const int64_t ftot = heads * f;
+    const bool wide = bk.group_cols == 64 && ftot > 32 && (f >= ftot || f % 64 == 0);
+    const int gc = wide ? 64 : 32;
+    const bool online = !exact && (heads == 1 ? ftot <= gc : f == gc) && ldwh % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(wh) % 16 == 0;
+    if (online) {
+        Carver cw(work, work_bytes);
+        GatPass P{};
+        P.src = src;
+        P.dst = dst;
+        P.m_state = rmax;
+        P.s_state = rinv;
+        P.pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+        P.bias = bias;
+        P.heads = static_cast<int>(heads);
+        P.head_cols = static_cast<int>(f);
+        P.slope = slope;
+        P.act = act;
+        P.post = post;
+        P.vec_io = ftot % 4 == 0 && ldo % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                   (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
+        const int64_t maxp = std::max<int64_t>(p.n_partials, 1);
+        if (gc == 64)
+            gat_online_passes<16>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+        else
+            gat_online_passes<8>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+        return;
+    }
     const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
     const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
     if (exact) {
