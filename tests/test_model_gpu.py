@@ -618,3 +618,29 @@ def test_blocked_gat_online_split_rows(gpu, restate, blocking):
             assert m.blocking_info()["blocks_sl"] == -(-n // blocking)
         assert_close(outs[blk], want, what=f"blocking={blk}")
     assert_close(outs[blocking], outs[0], what="online blocked vs unblocked")
+
+
+@pytest.mark.parametrize("model", ["gcn", "sage"])
+def test_blocked_wide_blocks_int32(gpu, restate, model):
+    """Blocks wider than 65,536 source rows keep int32 columns (narrower ones
+    store 16-bit offsets within the block): exact precision over 140,000
+    nodes in blocks of 70,000 rows is bit-identical to the unblocked exact
+    forward, and within tolerance of the oracle."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(61)
+    n = 140_000
+    a = random_csr(rng, n, n, avg_deg=24, weighted=False)
+    spec = (synth.spec_gcn(16, 32, 5) if model == "gcn" else synth.spec_sage(16, 32, 5))
+    w = synth.model_weights(spec, seed=21)
+    x = rng.standard_normal((n, 16)).astype(np.float32)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    outs = {}
+    for blocking in (70_000, 0):
+        m = tg.Model.from_spec(spec, w)
+        m.set_precision(tg.PRECISION_EXACT)
+        m.set_blocking(blocking)
+        outs[blocking] = m.forward(da, _t(gpu, x), mode=tg.FORWARD_CACHED).cpu().numpy()
+        info = m.blocking_info()
+        assert info["blocks_sl" if model == "gcn" else "blocks_raw"] == (2 if blocking else 0)
+    np.testing.assert_array_equal(bits(outs[70_000]), bits(outs[0]))
+    assert_close(outs[0], restate.model_forward(spec, w, a, x), what=model)

@@ -14,7 +14,10 @@
 // bci/bv[brp[b*n + i] .. brp[b*n + i + 1]), blocks outermost, in the order
 // they have in row i of the source structure.  brp[b*n + n] = brp[(b+1)*n],
 // so block b's row pointer is the slice brp + b*n and ordinary row plans
-// (absolute offsets) index it.
+// (absolute offsets) index it.  With blocks of at most 65,536 rows (every
+// default) bci holds uint16 offsets within the entry's block, column -
+// b * rows_per_block, and a pass reads B from the block's first row; wider
+// blocks keep int32 columns.
 #include "aggregate.hpp"
 #include "common.hpp"
 #include "spmm_plan.hpp"
@@ -79,8 +82,8 @@ template <bool SCATTER>
 __global__ __launch_bounds__(256) void block_split_kernel(
     const int32_t* __restrict__ rp, const int32_t* __restrict__ ci,
     const float* __restrict__ v, int64_t n, int rows_per_block, double inv_rows, int nb,
-    int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, float* __restrict__ bv,
-    int32_t* __restrict__ disorder) {
+    int32_t* __restrict__ cnt_or_brp, int32_t* __restrict__ bci, uint16_t* __restrict__ bci16,
+    float* __restrict__ bv, int32_t* __restrict__ disorder) {
     __shared__ int32_t slots[4][64];
     const int lane = threadIdx.x & 63;
     int32_t* slot = slots[threadIdx.x >> 6];
@@ -153,7 +156,10 @@ __global__ __launch_bounds__(256) void block_split_kernel(
             }
             __builtin_amdgcn_wave_barrier();
             if (valid) {
-                bci[pos] = c;
+                if (bci16)
+                    bci16[pos] = static_cast<uint16_t>(c - blk * rows_per_block);
+                else
+                    bci[pos] = c;
                 if (bv) bv[pos] = val;
             }
         }
@@ -201,7 +207,9 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     bk.rp = rp;
     bk.weighted = v != nullptr;
     bk.brp.reserve(static_cast<size_t>(nb * n + 1) * sizeof(int32_t));
-    bk.bci.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(int32_t));
+    bk.idx16 = rows_per_block <= 65536;
+    bk.bci.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) *
+                   (bk.idx16 ? sizeof(uint16_t) : sizeof(int32_t)));
     if (v) bk.bv.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
 
     Carver cv(nullptr, 0);
@@ -219,13 +227,14 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     const double inv_rows = 1.0 / static_cast<double>(rows_per_block);
     block_split_kernel<false><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
                                                    inv_rows, static_cast<int>(nb), cnt, nullptr,
-                                                   nullptr, disorder);
+                                                   nullptr, nullptr, disorder);
     TG_LAUNCH_CHECK();
     int32_t* brp = bk.brp.as<int32_t>();
     exclusive_scan_i32(cnt, brp, nb * n, scan_tmp, s);
     block_split_kernel<true><<<grid, 256, 0, s>>>(rp, ci, v, n, static_cast<int>(rows_per_block),
                                                   inv_rows, static_cast<int>(nb), brp,
-                                                  bk.bci.as<int32_t>(),
+                                                  bk.idx16 ? nullptr : bk.bci.as<int32_t>(),
+                                                  bk.idx16 ? bk.bci.as<uint16_t>() : nullptr,
                                                   v ? bk.bv.as<float>() : nullptr, nullptr);
     TG_LAUNCH_CHECK();
     // one plan per block, all counted before one synchronisation, then
@@ -248,7 +257,7 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
     require(!epi.max, "blocked aggregation: max is not supported");
     require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
     if (bk.n == 0 || f == 0) return;
-    const int32_t* bci = bk.bci.as<int32_t>();
+    const int32_t* bci = bk.idx16 ? nullptr : bk.bci.as<int32_t>();
     // attention passes compute their weights (no value stream)
     const float* bv = epi.att_dst == nullptr && bk.weighted ? bk.bv.as<float>() : nullptr;
     // One launch per block over all column groups of f (grid.y), blocks in
@@ -280,7 +289,14 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         e.att_rinv = epi.att_rinv;
         e.att_heads = epi.att_heads;
         e.att_slope = epi.att_slope;
-        run_aggregate(*bk.plans[blk], f, bci, bv, b, ldb, c, ldc, e, s, group_cols);
+        // 16-bit indices count from the block's first source row
+        const int64_t r0 = bk.idx16 ? blk * bk.rows_per_block : 0;
+        const float* bb = b + r0 * (epi.b_tile_stride > 0 ? 32 : ldb);
+        if (bk.idx16) {
+            e.ci16 = bk.bci.as<uint16_t>();
+            if (e.att_dst) e.att_dst = epi.att_dst + r0 * epi.att_heads;
+        }
+        run_aggregate(*bk.plans[blk], f, bci, bv, bb, ldb, c, ldc, e, s, group_cols);
     }
 }
 

@@ -783,8 +783,9 @@ __device__ __forceinline__ void out_store(float* row, int64_t fo, int64_t f, boo
 template <int LPR>
 __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
-    const float* __restrict__ B, int64_t ldb, float* __restrict__ C, int64_t ldc,
-    float* __restrict__ partials, int64_t ldp, int64_t f, GatPass P) {
+    const uint16_t* __restrict__ ci16, const float* __restrict__ B, int64_t ldb,
+    float* __restrict__ C, int64_t ldc, float* __restrict__ partials, int64_t ldp, int64_t f,
+    GatPass P) {
     constexpr int U = 16;                    // row gathers in flight per lane
     constexpr int CPL = U > LPR ? U / LPR : 1;
     constexpr int BE = LPR * CPL;            // entries per batch (== U)
@@ -826,7 +827,7 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int idx = base + l * CPL + j;
-            ncl[j] = idx < e ? ci[idx] : 0;
+            ncl[j] = idx < e ? (ci16 ? static_cast<int>(ci16[idx]) : ci[idx]) : 0;
         }
     };
     fetch(ch.y);
@@ -988,10 +989,15 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
         P.first = blk == 0;
         P.last = blk + 1 == bk.n_blocks;
         if (p.n_chunks > 0) {
+            // 16-bit indices count from the block's first source row
+            const int64_t r0 = bk.idx16 ? blk * bk.rows_per_block : 0;
+            GatPass Q = P;
+            Q.dst = P.dst + r0 * P.heads;
             dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)), ytiles);
             gat_online_chunk_kernel<LPR><<<grid, 256, 0, s>>>(
-                p.chunks.as<int4>(), p.n_chunks, bk.bci.as<int32_t>(), wh, ldwh, out, ldo,
-                p.partials.as<float>(), ldp, f, P);
+                p.chunks.as<int4>(), p.n_chunks, bk.idx16 ? nullptr : bk.bci.as<int32_t>(),
+                bk.idx16 ? bk.bci.as<uint16_t>() : nullptr, wh + r0 * ldwh, ldwh, out, ldo,
+                p.partials.as<float>(), ldp, f, Q);
             TG_LAUNCH_CHECK();
         }
         if (p.n_split > 0) {

@@ -555,7 +555,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int idx = base + l * CPL + j;
-            ncl[j] = idx < e ? ci[idx] : 0;
+            ncl[j] = idx < e ? (epi.ci16 ? static_cast<int>(epi.ci16[idx]) : ci[idx]) : 0;
             nwl[j] = 1.0f;
             if constexpr (MODE == kAggWeighted) nwl[j] = idx < e ? av[idx] : 0.0f;
         }
