@@ -83,9 +83,10 @@ def measure_copy(torch, reps: int = 10):
 
 
 def measured_traffic(f: int, seed: int):
-    """HBM bytes per SpMM launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (copy-kernel calibrated), for the default workload
-    only; None when no profile covers this configuration."""
+    """Bytes per SpMM launch between L2 and the fabric (HBM and Infinity
+    Cache), from the committed rocprofv3 summary: fetched = 32/64/128 x the
+    per-size L2 read-request counters, written = WRITE_SIZE.  For the
+    default workload only; None when no profile covers this configuration."""
     import re
 
     if seed != DEFAULT_SEED or not os.path.exists(PMC_SUMMARY):
@@ -551,6 +552,37 @@ def run_forward_e(args, torch, tg):
     return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)
 
 
+def run_calib_gather(torch, tg, rows: int = 1 << 23):
+    """Calibration dispatches for rocprofv3 FETCH_SIZE on gather-shaped
+    traffic: SpMM by a permutation matrix (one entry per row, every column
+    once), so every row of B is gathered exactly once, in random order:
+    F = 32 (one 128-byte line per gather, B 1 GiB) and F = 16 (64-byte
+    gathers, half lines, B 512 MB), both beyond the MALL.  A dispatch's unique
+    bytes are B + 12 rows (column, value, row pointer) read and 4 F rows
+    written; its FETCH_SIZE against that figure gives the counter's scale for
+    gathers of that size."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    perm = torch.randperm(rows, generator=g, device=dev).to(torch.int32)
+    rp = torch.arange(rows + 1, device=dev, dtype=torch.int32)
+    a = tg.DeviceCSR(rows, rows, rp, perm, torch.ones(rows, device=dev))
+    out = {}
+    for f in (32, 16):
+        b = torch.randn(rows, f, generator=g, device=dev)
+        c = torch.empty(rows, f, device=dev)
+        plan = tg.SpmmPlan(rp, rows, rows, f)
+        for _ in range(2):
+            tg.spmm(a, b, plan=plan, out=c)
+        torch.cuda.synchronize()
+        out[f] = dict(rows=rows, read_bytes=4 * rows * f + 12 * rows, written_bytes=4 * rows * f)
+        del b, c, plan
+    del a, perm, rp
+    torch.cuda.empty_cache()
+    log(f"gather calibration dispatches: {out}")
+    return out
+
+
 def host_info():
     """The CPU the baselines ran on: model name, logical CPUs, the CPUs this
     process may use, and OMP_NUM_THREADS."""
@@ -901,6 +933,9 @@ def main():
     ap.add_argument("--ingest-edges", type=int, default=20_000_000)
     ap.add_argument("--ingest-rows", type=int, default=50_000)
     ap.add_argument("--ingest-steps", type=int, default=5)
+    ap.add_argument("--calib-gather", action="store_true",
+                    help="also run permutation SpMMs (every B row gathered once; F=32, 16), the "
+                         "gather-shaped dispatches for scaling rocprofv3 FETCH_SIZE")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 1 GiB copy kernel (out = x * 1), the reference "
                          "dispatch for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -929,6 +964,8 @@ def main():
             torch.mul(xc, 1.0, out=yc)
         torch.cuda.synchronize()
         del xc, yc
+    if args.calib_gather:
+        run_calib_gather(torch, tg)
     fwd = None if args.no_forward else run_forward_e(args, torch, tg)
     torch.cuda.empty_cache()
     cora = None if args.no_cora else run_cora(args, torch, tg)
@@ -963,8 +1000,9 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["kernel_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.f, args.seed),
-                     "traffic_source": "profiles/spmm_configD_pmc.md (FETCH_SIZE x2 + "
-                                       "WRITE_SIZE x1, copy-kernel calibrated)",
+                     "traffic_source": "profiles/spmm_configD_pmc.md (TCC_EA0_RDREQ "
+                                       "32B/64B/128B x size + WRITE_SIZE, checked on a "
+                                       "permutation SpMM and a 1 GiB copy)",
                      "kernel": "spmm pass (agg_chunk_kernel + agg_reduce_kernel)",
                      "kernel_ms_avg": round(head["kernel_ms_avg"], 4),
                      "bytes_per_launch": head["bytes"]},
