@@ -348,23 +348,28 @@ def _blocked_cost(n, nnz, f, nb, gc, values=False, self_term=False, score_heads=
     """Compulsory L2 fills of one blocked aggregation (all its passes) of
     width f over a structure of nnz entries cut into nb column blocks, with
     lane groups of gc columns (g = ceil(f / gc) groups):
-      * the index stream (and values) once per column group: 4 nnz g (x2);
+      * the index stream once per column group: 2 nnz g for blocks of at
+        most 65,536 rows (16-bit offsets in the block), else 4 nnz g; values
+        4 nnz g more;
       * the chunk descriptors once per column group and block: 16 n nb g;
       * each block's slice of the gathered matrix once per XCD's L2:
         8 x 4 n f (with f padded to whole 32-column tiles);
       * the output read and written once per block after the first:
         4 n f (2 nb - 1);
-      * a self term (SAGE) and score arrays (GAT) once: 4 n f, 8 x 4 n heads.
+      * a self term (SAGE) and score arrays (GAT) once: 4 n f, 8 x 4 n heads;
+      * GAT's online softmax state (max, sum) per row and column group, read
+        and written once per block after the first: 8 n g (2 nb - 1).
     The gathers themselves (4 f bytes per entry) are served by L2 and are not
     counted; they are what the passes spend their time on."""
     g = -(-f // gc)
     fpad = -(-f // 32) * 32
-    b = (4 * nnz * g * (2 if values else 1) + 16 * n * nb * g + 8 * 4 * n * fpad +
+    idx = 2 if -(-n // nb) <= 65536 else 4
+    b = (idx * nnz * g + (4 * nnz * g if values else 0) + 16 * n * nb * g + 8 * 4 * n * fpad +
          4 * n * f * (2 * nb - 1))
     if self_term:
         b += 4 * n * f
     if score_heads:
-        b += 8 * 4 * n * score_heads
+        b += 8 * 4 * n * score_heads + 8 * n * g * (2 * nb - 1)
     return b
 
 
@@ -404,7 +409,7 @@ def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
         agg("L2 mean aggregation", nnz_a, classes, nb, gc, values=False, self_term=True)
     else:
         # fast precision: the softmax rides along the blocked passes (a
-        # running (max, sum) per row and head, read and written per pass);
+        # running (max, sum) per row and column group, read and written per pass);
         # unblocked, one online-softmax pass
         nb, gc = info["blocks_sl"], info["cols_sl"]
         for li, (fi, fo, h) in enumerate(((f_in, hidden, heads), (hidden * heads, classes, 1))):
@@ -412,9 +417,6 @@ def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
             ks.append((f"L{li + 1} scores", 4 * n * fo * h + 8 * n * h, 4 * n * fo * h))
             agg(f"L{li + 1} attention aggregation", nnz_s, fo * h, nb, gc, values=False,
                 score_heads=h)
-            if nb > 0:
-                lbl, b, fl = ks[-1]
-                ks[-1] = (lbl, b + 8 * n * h * (2 * nb - 1), fl)
     out, tot = [], 0.0
     for label, b, fl in ks:
         t = max(b / (HBM_PEAK_GBS * 1e6), fl / (MFMA_PEAK_TFS * 1e9))

@@ -588,12 +588,15 @@ def test_cached_forward_follows_adjacency(gpu, restate):
     check("after layers were added", spec2, w2)
 
 
-@pytest.mark.parametrize("blocking", [1500, 500])
-def test_blocked_gat_online_split_rows(gpu, restate, blocking):
+@pytest.mark.parametrize("blocking,hidden,heads,classes",
+                         [(1500, 64, 2, 5), (500, 64, 2, 5), (500, 128, 1, 100)])
+def test_blocked_gat_online_split_rows(gpu, restate, blocking, hidden, heads, classes):
     """Fast blocked GAT carries the softmax across the passes: rows whose
     segment in a block is longer than one plan chunk (1,024 entries) are
     merged from per-chunk (max, sum, partial) triples with the state the
-    earlier passes left; 2 and 6 blocks (middle passes included).  Within
+    earlier passes left; 2 and 6 blocks (middle passes included).  A single
+    head wider than a 64-column lane group (128 and 100 columns) spans two
+    groups, each carrying its own copy of the head's state.  Within
     tolerance of the oracle and of the unblocked fast path."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(71)
@@ -601,7 +604,7 @@ def test_blocked_gat_online_split_rows(gpu, restate, blocking):
     a = random_csr(rng, n, n, avg_deg=20, max_deg=9000, empty_frac=0.02)
     # some row's segment in a block exceeds one chunk (uniform columns)
     assert np.diff(a.row_ptr).max() > 1024 * -(-n // blocking)
-    spec = synth.spec_gat(24, 64, 2, 5)
+    spec = synth.spec_gat(24, hidden, heads, classes)
     w = synth.model_weights(spec, seed=13)
     for k in w:
         if k.endswith("bias"):
@@ -615,7 +618,8 @@ def test_blocked_gat_online_split_rows(gpu, restate, blocking):
         m.set_blocking(blk)
         outs[blk] = m.forward(da, _t(gpu, x), mode=tg.FORWARD_CACHED).cpu().numpy()
         if blk:
-            assert m.blocking_info()["blocks_sl"] == -(-n // blocking)
+            info = m.blocking_info()
+            assert info["blocks_sl"] == -(-n // blocking) and info["cols_sl"] == 64
         assert_close(outs[blk], want, what=f"blocking={blk}")
     assert_close(outs[blocking], outs[0], what="online blocked vs unblocked")
 

@@ -33,6 +33,13 @@
 #include <string>
 
 namespace tg {
+
+// (m, s) per partial slot and head, or per 32-column group (blocked online
+// passes), whichever is more
+int64_t gat_stat_slots(int64_t heads, int64_t f) {
+    return std::max<int64_t>(heads, ceil_div(heads * f, 32));
+}
+
 namespace {
 
 template <int VEC>
@@ -712,24 +719,26 @@ __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __rest
 
 // ---------------------------------------------------------------------------
 // Blocked GAT passes with the softmax carried across the passes (fast
-// precision): no statistics sweep.  Every (row, head) keeps a running max m
-// and a running sum s of exp(e - m) in state arrays [n x heads], and the
-// output row holds the unnormalised sum of exp(e_ij - m) Wh_j over the
-// blocks so far.  A pass raises m to the maximum of its entries' scores,
-// rescaling the carried sum and output by exp(m_old - m_new) (the online
-// softmax of gat_chunk_kernel, across blocks); the last pass multiplies by
-// 1/s and applies bias and activations.  One lane group of LPR lanes (VEC 4
-// floats each) covers one head's columns of one chunk, so (row, head) state
-// has a single owner per pass; rows split into several chunks leave
-// per-chunk (m, s, sum) partials, merged with the state by
-// gat_online_reduce_kernel.
+// precision): no statistics sweep.  Every (row, column group) keeps a
+// running max m and a running sum s of exp(e - m) in state arrays
+// [n x G] (G = the launch's column groups, grid.y), and the output row
+// holds the unnormalised sum of exp(e_ij - m) Wh_j over the blocks so far.
+// A pass raises m to the maximum of its entries' scores, rescaling the
+// carried sum and output by exp(m_old - m_new) (the online softmax of
+// gat_chunk_kernel, across blocks); the last pass multiplies by 1/s and
+// applies bias and activations.  One lane group of LPR lanes (VEC 4 floats
+// each) covers one column group of one chunk, inside one head.  The groups
+// of a head compute the same m and s from the same entries in the same
+// order; each keeps its own copy, so every state slot has a single owner
+// per pass.  Rows split into several chunks leave per-chunk (m, s, sum)
+// partials, merged with the state by gat_online_reduce_kernel.
 // ---------------------------------------------------------------------------
 struct GatPass {
     const float* src;  // [n x heads] a_l . Wh_i
     const float* dst;  // [n x heads] a_r . Wh_j
-    float* m_state;    // [n x heads] running max
-    float* s_state;    // [n x heads] running sum
-    float* pstats;     // [partial slots x heads x 2] (m, s) of split rows' chunks
+    float* m_state;    // [n x G] running max per row and column group
+    float* s_state;    // [n x G] running sum
+    float* pstats;     // [partial slots x G x 2] (m, s) of split rows' chunks
     const float* bias;
     int heads;
     int head_cols;
@@ -802,9 +811,9 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     if (!P.first && !P.last && ch.z == ch.y) return;
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
     const int h = static_cast<int>(fbase / P.head_cols);
-    const int64_t so = static_cast<int64_t>(ch.x) * P.heads + h;
-    const float si = P.src[so];
+    const float si = P.src[static_cast<int64_t>(ch.x) * P.heads + h];
     const float* dh = P.dst + h;
+    const int64_t so = static_cast<int64_t>(ch.x) * gridDim.y + blockIdx.y;  // state slot
     const int64_t fo = fbase + static_cast<int64_t>(l) * 4;
     const bool ok = fo < f;
     const int64_t fl = ok ? fo : fbase;  // lanes past f gather the tile's first vector
@@ -891,7 +900,7 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     if (!unsplit) {
         if (ok) stv<4>(partials + static_cast<int64_t>(ch.w) * ldp + fo, acc);
         if (l == 0) {
-            float* st = P.pstats + (static_cast<int64_t>(ch.w) * P.heads + h) * 2;
+            float* st = P.pstats + (static_cast<int64_t>(ch.w) * gridDim.y + blockIdx.y) * 2;
             st[0] = m;
             st[1] = s;
         }
@@ -928,8 +937,7 @@ __global__ __launch_bounds__(256) void gat_online_reduce_kernel(
     if (sid >= n_split) return;
     const int4 sp = split[sid];
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
-    const int h = static_cast<int>(fbase / P.head_cols);
-    const int64_t so = static_cast<int64_t>(sp.x) * P.heads + h;
+    const int64_t so = static_cast<int64_t>(sp.x) * gridDim.y + blockIdx.y;  // state slot
     const int64_t fo = fbase + static_cast<int64_t>(l) * 4;
     const bool ok = fo < f;
     float* crow = C + static_cast<int64_t>(sp.x) * ldc;
@@ -941,7 +949,7 @@ __global__ __launch_bounds__(256) void gat_online_reduce_kernel(
     }
     float M = mp;
     for (int c = 0; c < sp.z; ++c) {
-        const float mc = P.pstats[(static_cast<int64_t>(sp.y + c) * P.heads + h) * 2];
+        const float mc = P.pstats[(static_cast<int64_t>(sp.y + c) * gridDim.y + blockIdx.y) * 2];
         M = (M < mc) ? mc : M;
     }
     const float fp = expf(mp - M);  // 0 when nothing was carried
@@ -949,7 +957,8 @@ __global__ __launch_bounds__(256) void gat_online_reduce_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = prev[k] * fp;
     for (int c = 0; c < sp.z; ++c) {
-        const float* st = P.pstats + (static_cast<int64_t>(sp.y + c) * P.heads + h) * 2;
+        const float* st =
+            P.pstats + (static_cast<int64_t>(sp.y + c) * gridDim.y + blockIdx.y) * 2;
         const float fc = expf(st[0] - M);
         S += st[1] * fc;
         if (ok) {
@@ -1011,7 +1020,7 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
 
 size_t gat_ws(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
     Carver c(nullptr, 0);
-    c.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+    c.take<float>(std::max<int64_t>(p.n_partials, 1) * gat_stat_slots(heads, f) * 2);
     if (!concat && heads > 1) c.take<float>(n * heads * f);
     return c.bytes();
 }
@@ -1125,16 +1134,18 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
     const int64_t ftot = heads * f;
     const bool wide = bk.group_cols == 64 && ftot > 32 && (f >= ftot || f % 64 == 0);
     const int gc = wide ? 64 : 32;
-    const bool online = !exact && (heads == 1 ? ftot <= gc : f == gc) && ldwh % 4 == 0 &&
+    const bool online = !exact && (heads == 1 || f % gc == 0) && ldwh % 4 == 0 &&
                         reinterpret_cast<uintptr_t>(wh) % 16 == 0;
     if (online) {
+        // state per (row, column group): G <= gat_stat_slots(heads, f)
+        const int64_t groups = ceil_div(ftot, gc);
         Carver cw(work, work_bytes);
         GatPass P{};
         P.src = src;
         P.dst = dst;
         P.m_state = rmax;
         P.s_state = rinv;
-        P.pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * heads * 2);
+        P.pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * groups * 2);
         P.bias = bias;
         P.heads = static_cast<int>(heads);
         P.head_cols = static_cast<int>(f);

@@ -53,6 +53,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
 void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
                 const float* al, const float* ar, float* src, float* dst, hipStream_t s);
 size_t gat_workspace(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat);
+int64_t gat_stat_slots(int64_t heads, int64_t f);
 void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
                    const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
                    const float* dst, float slope, const float* bias, int act, int post,
@@ -62,9 +63,11 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
 // allows it (concatenated or single head, heads of whole 32-column tiles),
 // and the aggregation itself over the blocked
 // form of the structure (p, ci: the unblocked structure's plan and columns,
-// for the softmax statistics; rmax, rinv: n x heads scratch; the passes
-// compute each entry's attention weight from them and the scores, storing
-// none; work: at least gat_workspace(p, ...) bytes; exact: the reference's
+// for the softmax statistics; rmax, rinv: n x max(heads, ceil(heads*f/32))
+// scratch, the row statistics or, in fast precision, the softmax state the
+// passes carry per (row, column group); the passes compute each entry's
+// attention weight and store none; work: at least gat_workspace(p, ...)
+// bytes; exact: the reference's
 // operation order, for a plan that splits no row and a blocked structure in
 // block order).
 bool gat_blocked_ok(int64_t heads, int64_t f, int concat);

@@ -287,7 +287,9 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     // (a factored GCN aggregation reads no values either).  Passes without a
     // value stream run in 32-column groups, as SAGE's (config-E GCN, factored:
     // 64-column groups at 10 blocks 9.64 ms, 32-column groups at 6 blocks
-    // 9.36 ms); a GAT layer's weighted passes keep 64-column groups.
+    // 9.36 ms).  GAT keeps 64-column groups: its passes compute a weight per
+    // entry and lane group, and 32-column groups double that work (config-E
+    // fast GAT, 32-column groups: 13.5-13.9 ms at 5-10 blocks against 12.0 ms).
     const int gc_sl = (m.unit_sl && !m.need_sl()) ? 32 : 64;
     const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, gc_sl);
     if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
@@ -473,10 +475,11 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
 
     // buffers
     const int64_t wmax = m.max_wide();
-    int64_t heads_max = 1;
+    int64_t heads_max = 1, slots_max = 1;
     size_t ws = 0;
     for (auto& l : m.layers) {
         heads_max = std::max(heads_max, l.heads);
+        if (l.type == LType::GAT) slots_max = std::max(slots_max, gat_stat_slots(l.heads, l.out));
         if (l.type == LType::SAGE)
             ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, dataflow, nnz));
         if (l.type == LType::GAT)
@@ -487,8 +490,9 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     // the transform's output: row-major at gather_pitch, or tile-major (32-column
     // tiles of n rows) for the blocked aggregations
     m.tmp.reserve(n * round_up(gather_pitch(wmax), 32) * sizeof(float));
-    // GAT: src and dst scores, then the blocked path's row max and 1/sum
-    m.scores.reserve(4 * n * heads_max * sizeof(float) + 256);
+    // GAT: src and dst scores [n x heads], then the blocked path's row
+    // statistics or softmax state [n x slots]
+    m.scores.reserve((2 * heads_max + 2 * slots_max) * n * sizeof(float) + 256);
     m.work.reserve(ws);
 
     const float* h = x;
@@ -563,7 +567,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
                        s);
             if (blocked) {
                 float* rmax = dst + n * l.heads;
-                float* rinv = rmax + n * l.heads;
+                float* rinv = rmax + n * gat_stat_slots(l.heads, l.out);
                 gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,
                                       m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
                                       l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
