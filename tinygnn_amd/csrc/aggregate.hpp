@@ -107,8 +107,9 @@ struct BlockedCSR {
     bool idx16 = false;
     DeviceBuffer bci;
     DeviceBuffer bv;   // float [nnz] (weighted structures)
-    DeviceBuffer scratch;  // the build's temporaries
-    PinnedBuffer host;     // the build's device-to-host results (plan totals, disorder)
+    DeviceBuffer scratch;       // the build's temporaries
+    DeviceBuffer plan_scratch;  // the block plans' build temporaries
+    PinnedBuffer host;          // the build's device-to-host results (plan totals, disorder)
     std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
 };
 

@@ -246,6 +246,197 @@ void build_plan(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int32_t* 
     build_plan_finish(p, tot, s);
 }
 
+// ---------------------------------------------------------------------------
+// Several plans over consecutive row ranges of one row-pointer array (the
+// per-block plans of a column-blocked copy: block b's row r at b*m + r),
+// built with one launch per step for all of them and one synchronisation.
+// Each step is the single-plan build's, with grid.y = the plan.
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ __launch_bounds__(256) void plan_count_multi_kernel(
+    const int32_t* __restrict__ row_ptr, int64_t m, int chunk, int32_t* __restrict__ split_cnt,
+    int32_t* __restrict__ is_split, int32_t* __restrict__ bin_count) {
+    __shared__ int32_t hist[kPlanBins];
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r < m) {
+        const int64_t q = static_cast<int64_t>(blockIdx.y) * m + r;
+        const int deg = row_ptr[q + 1] - row_ptr[q];
+        const int nch = deg <= chunk ? 1 : (deg + chunk - 1) / chunk;
+        split_cnt[q] = nch > 1 ? nch : 0;
+        is_split[q] = nch > 1 ? 1 : 0;
+        if (nch == 1) {
+            atomicAdd(&hist[chunk_bin(deg)], 1);
+        } else {
+            const int full = deg / chunk, rem = deg - full * chunk;
+            atomicAdd(&hist[chunk_bin(chunk)], full);
+            if (rem) atomicAdd(&hist[chunk_bin(rem)], 1);
+        }
+    }
+    __syncthreads();
+    int32_t* bc = bin_count + static_cast<int64_t>(blockIdx.y) * kPlanBins;
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+        if (hist[i]) atomicAdd(&bc[i], hist[i]);
+}
+
+// One thread per plan: bin cursors (longest bin first) and the plan's
+// totals {chunks, split rows, partial slots}, from the scans over all plans.
+__global__ void plan_bins_multi_kernel(const int32_t* __restrict__ bin_count,
+                                       int32_t* __restrict__ bin_cursor,
+                                       const int32_t* __restrict__ slot_base,
+                                       const int32_t* __restrict__ split_pos, int64_t m,
+                                       int nplans, int64_t* __restrict__ totals) {
+    const int b = threadIdx.x;
+    if (b >= nplans) return;
+    int64_t acc = 0;
+    for (int k = kPlanBins - 1; k >= 0; --k) {
+        bin_cursor[b * kPlanBins + k] = static_cast<int32_t>(acc);
+        acc += bin_count[b * kPlanBins + k];
+    }
+    const int64_t lo = static_cast<int64_t>(b) * m, hi = lo + m;
+    totals[4 * b + 0] = acc;
+    totals[4 * b + 1] = split_pos[hi] - split_pos[lo];
+    totals[4 * b + 2] = slot_base[hi] - slot_base[lo];
+    totals[4 * b + 3] = 0;
+}
+
+struct MultiPlanOut {
+    int4* chunks[kMaxMultiPlans];
+    int4* split[kMaxMultiPlans];
+};
+
+__global__ __launch_bounds__(256) void plan_scatter_multi_kernel(
+    const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
+    const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
+    int32_t* __restrict__ bin_cursor, MultiPlanOut out) {
+    __shared__ int hist[kPlanBins], gbase[kPlanBins];
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __syncthreads();
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t lo = static_cast<int64_t>(blockIdx.y) * m;
+    int b = 0, e = 0, deg = 0, full = 0, rem = 0;
+    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0;
+    if (r < m) {
+        b = row_ptr[lo + r];
+        e = row_ptr[lo + r + 1];
+        deg = e - b;
+        if (deg <= chunk) {
+            bin_r = chunk_bin(deg);
+            pos_r = atomicAdd(&hist[bin_r], 1);
+            rem = -1;  // one direct chunk
+        } else {
+            full = deg / chunk;
+            rem = deg - full * chunk;
+            bin_f = chunk_bin(chunk);
+            pos_f = atomicAdd(&hist[bin_f], full);
+            if (rem) {
+                bin_r = chunk_bin(rem);
+                pos_r = atomicAdd(&hist[bin_r], 1);
+            }
+        }
+    }
+    __syncthreads();
+    int32_t* cur = bin_cursor + static_cast<int64_t>(blockIdx.y) * kPlanBins;
+    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+        if (hist[i] > 0) gbase[i] = atomicAdd(&cur[i], hist[i]);
+    __syncthreads();
+    if (r >= m) return;
+    int4* chunks = out.chunks[blockIdx.y];
+    const int row = static_cast<int>(r);
+    if (rem < 0) {
+        chunks[gbase[bin_r] + pos_r] = make_int4(row, b, e, -1);
+        return;
+    }
+    // slots and split positions count from the plan's first row
+    const int slot0 = slot_base[lo + r] - slot_base[lo];
+    for (int c = 0; c < full; ++c) {
+        const int cb = b + c * chunk;
+        chunks[gbase[bin_f] + pos_f + c] = make_int4(row, cb, cb + chunk, slot0 + c);
+    }
+    if (rem) chunks[gbase[bin_r] + pos_r] = make_int4(row, b + full * chunk, e, slot0 + full);
+    out.split[blockIdx.y][split_pos[lo + r] - split_pos[lo]] =
+        make_int4(row, slot0, full + (rem ? 1 : 0), deg);
+}
+
+struct MultiTemps {
+    int32_t *split_cnt, *is_split, *slot_base, *split_pos, *bin_count, *bin_cursor;
+    int64_t *totals, *scan_tmp;
+};
+
+MultiTemps carve_multi(Carver& c, int64_t rows, int nplans) {
+    MultiTemps t;
+    t.split_cnt = c.take<int32_t>(rows);
+    t.is_split = c.take<int32_t>(rows);
+    t.slot_base = c.take<int32_t>(rows + 1);
+    t.split_pos = c.take<int32_t>(rows + 1);
+    t.bin_count = c.take<int32_t>(static_cast<int64_t>(nplans) * kPlanBins);
+    t.bin_cursor = c.take<int32_t>(static_cast<int64_t>(nplans) * kPlanBins);
+    t.totals = c.take<int64_t>(4 * static_cast<int64_t>(nplans));
+    t.scan_tmp = c.take<int64_t>(scan_temp_elems(rows));
+    return t;
+}
+
+}  // namespace
+
+void build_plans_multi(tg_spmm_plan_s* const* plans, int nplans, int64_t m,
+                       int64_t nnz_bound, const int32_t* row_ptr, int64_t max_f, int64_t chunk,
+                       DeviceBuffer& scratch, int64_t* host_totals, hipStream_t s) {
+    require(nplans >= 1 && nplans <= kMaxMultiPlans, "spmm plans: 1 to 64 plans per build");
+    require(m >= 1 && static_cast<int64_t>(nplans) * m < (int64_t(1) << 31),
+            "spmm plans: plans x rows must be < 2^31");
+    require(nnz_bound >= 0 && nnz_bound < (int64_t(1) << 31),
+            "spmm plans: nnz must be < 2^31 (int32 CSR)");
+    require(row_ptr != nullptr && max_f >= 0, "spmm plans: bad arguments");
+    if (chunk <= 0) chunk = kDefaultChunk;
+    require(chunk <= (1 << 24), "spmm plans: chunk_nnz too large");
+    const int64_t rows = static_cast<int64_t>(nplans) * m;
+    Carver cv(nullptr, 0);
+    carve_multi(cv, rows, nplans);
+    scratch.reserve(cv.bytes());
+    Carver c(scratch.get(), scratch.size());
+    const MultiTemps t = carve_multi(c, rows, nplans);
+    fill_i32(t.bin_count, static_cast<int64_t>(nplans) * kPlanBins, 0, s);
+    const dim3 grid(static_cast<unsigned>(ceil_div(m, 256)), static_cast<unsigned>(nplans));
+    plan_count_multi_kernel<<<grid, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk),
+                                                 t.split_cnt, t.is_split, t.bin_count);
+    TG_LAUNCH_CHECK();
+    exclusive_scan_i32(t.split_cnt, t.slot_base, rows, t.scan_tmp, s);
+    exclusive_scan_i32(t.is_split, t.split_pos, rows, t.scan_tmp, s);
+    plan_bins_multi_kernel<<<1, kMaxMultiPlans, 0, s>>>(t.bin_count, t.bin_cursor, t.slot_base,
+                                                        t.split_pos, m, nplans, t.totals);
+    TG_LAUNCH_CHECK();
+    TG_HIP(hipMemcpyAsync(host_totals, t.totals, 4 * nplans * sizeof(int64_t),
+                          hipMemcpyDeviceToHost, s));
+    TG_HIP(hipStreamSynchronize(s));
+    int device = 0;
+    TG_HIP(hipGetDevice(&device));
+    MultiPlanOut out{};
+    for (int b = 0; b < nplans; ++b) {
+        tg_spmm_plan_s& p = *plans[b];
+        p.device = device;
+        p.m = m;
+        p.nnz_bound = nnz_bound;
+        p.max_f = max_f;
+        p.chunk = chunk;
+        p.row_ptr = row_ptr + static_cast<int64_t>(b) * m;
+        p.n_chunks = host_totals[4 * b + 0];
+        p.n_split = host_totals[4 * b + 1];
+        p.n_partials = host_totals[4 * b + 2];
+        p.chunks.reserve(static_cast<size_t>(std::max<int64_t>(p.n_chunks, 1)) * sizeof(int4));
+        p.split.reserve(static_cast<size_t>(std::max<int64_t>(p.n_split, 1)) * sizeof(int4));
+        if (p.n_partials > 0 && p.max_f > 0)
+            p.partials.reserve(static_cast<size_t>(p.n_partials) *
+                               static_cast<size_t>(round_up(p.max_f, 4)) * sizeof(float));
+        out.chunks[b] = p.chunks.as<int4>();
+        out.split[b] = p.split.as<int4>();
+    }
+    plan_scatter_multi_kernel<<<grid, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk),
+                                                   t.slot_base, t.split_pos, t.bin_cursor, out);
+    TG_LAUNCH_CHECK();
+}
+
 LaneLayout choose_layout(int64_t f, int vec) {
     LaneLayout L{};
     L.vec = vec;

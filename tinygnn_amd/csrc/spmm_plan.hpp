@@ -82,6 +82,18 @@ void build_plan_count(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int
                       int64_t max_f, int64_t chunk, hipStream_t s, int64_t* host_totals);
 void build_plan_finish(tg_spmm_plan_s& p, const int64_t* host_totals, hipStream_t s);
 
+// nplans (<= kMaxMultiPlans) plans, plan b over rows [b*m, (b+1)*m) of one
+// row-pointer array of nplans*m + 1 absolute offsets (a column-blocked
+// copy's block row pointers), built together: one launch per step for all
+// plans and one synchronisation of `s`.  Plan b is the plan build_plan
+// would make over row_ptr + b*m.  scratch holds the temporaries (it only
+// grows); host_totals is pinned host memory of 4*nplans int64.  Work
+// enqueued on `s` before the call is complete when it returns.
+constexpr int kMaxMultiPlans = 64;
+void build_plans_multi(tg_spmm_plan_s* const* plans, int nplans, int64_t m, int64_t nnz_bound,
+                       const int32_t* row_ptr, int64_t max_f, int64_t chunk,
+                       DeviceBuffer& scratch, int64_t* host_totals, hipStream_t s);
+
 // Lane layout for an aggregation of width f: each lane owns VPL (= 1)
 // vectors of VEC consecutive floats, LPR lanes own one row's feature tile,
 // and n_tiles tiles cover f.
