@@ -348,9 +348,20 @@ int tg_model_invalidate(tg_model_t model);
 /* The column blocking of the cached adjacency state (diagnostics; no
  * counterpart in the reference): blocks and columns per lane group of A + I's
  * blocked copy (GCN, GAT) and of A's (SAGE mean); 0 blocks = unblocked or no
- * cached state.  Filled by the last forward. */
+ * cached state; sl_direct = 1 when A + I's blocked copy was split from A
+ * directly (below).  Filled by the last forward; any pointer may be null. */
 int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
-                           int64_t* blocks_raw, int64_t* cols_raw);
+                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct);
+/* How a fast-precision GCN-only model gets the blocked A + I its factored
+ * passes read (no counterpart in the reference; for tests and measurement).
+ * direct = 1 (the default): when A's values are all 1, its rows sorted and
+ * without a diagonal, the blocked copy is split from A directly, each row's
+ * diagonal placed where add_self_loops would insert it, and gcn_norm's
+ * degrees come from the row lengths; A + I itself is never written.  The
+ * build checks those conditions and otherwise takes the path of direct = 0:
+ * gcn_norm writes A + I's structure, which is then split.  Both give the same
+ * blocked copy and the same outputs bit for bit.  Drops the cached state. */
+int tg_model_set_self_loop_split(tg_model_t model, int direct);
 
 /* ------------------------------------------------------------------------
  * CSV ingestion -- replaces GraphLoader::parse_edges / parse_features and

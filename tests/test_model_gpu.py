@@ -420,6 +420,16 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     assert_close(outs[100], outs[0], what="blocked vs unblocked")
     if variant == "unit":  # the factored sums round differently from the unblocked ones
         assert (bits(outs[100]) != bits(outs[0])).any(), "factoring had no effect"
+    # A + I's blocked copy split from A directly (GCN alone, unit values, no
+    # diagonal) or from the A + I gcn_norm writes: the same bits
+    m = tg.Model.from_spec(spec, w)
+    m.set_blocking(100)
+    m.forward(da, xt)
+    assert m.blocking_info()["sl_direct"] == (variant == "unit")
+    m.set_self_loop_split(False)
+    got = m.forward(da, xt).cpu().numpy()
+    assert not m.blocking_info()["sl_direct"]
+    np.testing.assert_array_equal(bits(got), bits(outs[100]), err_msg="A + I written, then split")
     # the values at an address off 16-byte alignment (the unit check's
     # entry-wise reads): the same decision, the same bits
     vbuf = gpu.zeros(g.nnz + 1, dtype=gpu.float32, device="cuda")
@@ -447,6 +457,44 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     np.testing.assert_array_equal(exact[100].view(np.int32), exact[0].view(np.int32))
     if variant != "unit_gat_stack":
         np.testing.assert_array_equal(exact[100].view(np.int32), want.view(np.int32))
+
+
+@pytest.mark.parametrize("order", ["sorted", "unsorted"])
+def test_direct_self_loop_split_long_rows(gpu, restate, order):
+    """The factored GCN's blocked A + I split straight from A (rows of up to
+    9,000 entries: the workgroup-per-row kernels past 4,096) equals the copy
+    split from the A + I gcn_norm writes, bit for bit in both forward modes,
+    and the oracle within tolerance.  A row out of order makes the direct
+    split decline (sl_direct False) and the forward take the written A + I."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(91)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=30, max_deg=9000, empty_frac=0.03)
+    rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
+    keep = rows != a.col_ind
+    g = restate.edge_list_to_csr(rows[keep], a.col_ind[keep].astype(np.int32), n)
+    assert np.diff(g.row_ptr).max() > 4096
+    if order == "unsorted":  # one long row reversed
+        i = int(np.argmax(np.diff(g.row_ptr)))
+        g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]] = g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]][::-1]
+    spec = synth.spec_gcn(16, 64, 5)
+    w = synth.model_weights(spec, seed=9)
+    x = rng.standard_normal((n, 16)).astype(np.float32)
+    da = tg.DeviceCSR.from_numpy(n, n, g.row_ptr, g.col_ind, g.val)
+    xt = _t(gpu, x)
+    outs = {}
+    for direct in (True, False):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(500)
+        m.set_self_loop_split(direct)
+        outs[direct] = m.forward(da, xt, mode=tg.FORWARD_CACHED).cpu().numpy()
+        info = m.blocking_info()
+        assert info["blocks_sl"] == 6 and info["cols_sl"] == 32
+        assert info["sl_direct"] == (direct and order == "sorted")
+        again = m.forward(da, xt, mode=tg.FORWARD_REFERENCE).cpu().numpy()
+        np.testing.assert_array_equal(bits(again), bits(outs[direct]))
+    np.testing.assert_array_equal(bits(outs[True]), bits(outs[False]))
+    assert_close(outs[True], restate.model_forward(spec, w, g, x), what=f"direct split {order}")
 
 
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),

@@ -115,10 +115,20 @@ struct BlockedCSR {
 
 // Blocks with at most 64 column blocks; v may be null (structure only);
 // chunk: the per-block plans' chunk size (0 = default).  Rebuilding into the
-// same object reuses its buffers and plans (they only grow).
+// same object reuses its buffers and plans (they only grow).  Synchronises
+// `s` (once when every row is sorted, twice otherwise).
 void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
                    hipStream_t s, int64_t chunk = 0);
+
+// The blocked copy of A + I's structure (nnz + n entries, no values) built
+// from A's (n x n, nnz entries) directly, each row's diagonal entry placed
+// before its first column > i, as add_self_loops inserts it: valid when
+// every row of A is sorted and none has a diagonal.  Returns false when
+// that does not hold (the copy is then unusable); bk.rp is A's row_ptr.
+bool build_blocked_self_loops(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
+                              const int32_t* ci, int64_t rows_per_block, int64_t max_f,
+                              hipStream_t s, int64_t chunk = 0);
 
 // Rows per block for an n-node structure with nnz entries whose passes use
 // lane groups of group_cols columns: `requested` > 0 is taken as given, 0

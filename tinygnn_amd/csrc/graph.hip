@@ -625,6 +625,20 @@ __global__ __launch_bounds__(256) void self_loop_copy_kernel(
     }
 }
 
+// gcn_norm's degree and 1/sqrt(degree) for an A whose values are all 1 and
+// which has no diagonal: every row of A + I sums to its length + 1, exactly
+// (the integral case of self_loop_info_kernel), when that is at most 2^24;
+// a longer row sets *flag (its fp32 sequential sum would saturate).
+__global__ __launch_bounds__(256) void unit_dis_kernel(const int32_t* __restrict__ row_ptr,
+                                                       int64_t n, float* __restrict__ dis,
+                                                       int32_t* __restrict__ flag) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const int64_t d = static_cast<int64_t>(row_ptr[r + 1] - row_ptr[r]) + 1;
+    if (d > (int64_t(1) << 24)) atomicOr(flag, 1);
+    dis[r] = cr_rcp(cr_sqrt(static_cast<float>(d)));
+}
+
 // Rows longer than kLongRow, listed for the workgroup-per-row kernels
 // (list[0..*count)); count starts at zero.
 __global__ __launch_bounds__(256) void long_rows_kernel(const int32_t* __restrict__ row_ptr,
@@ -1143,6 +1157,13 @@ void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col
 }
 
 size_t self_loops_workspace(int64_t n) { return self_loops_ws(n); }
+
+void unit_self_loop_dis(int64_t n, const int32_t* row_ptr, float* dis, int32_t* flag,
+                        hipStream_t s) {
+    if (n == 0) return;
+    unit_dis_kernel<<<static_cast<unsigned>(ceil_div(n, 256)), 256, 0, s>>>(row_ptr, n, dis, flag);
+    TG_LAUNCH_CHECK();
+}
 
 }  // namespace tg
 

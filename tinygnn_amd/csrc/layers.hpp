@@ -34,6 +34,12 @@ void gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr, const int32_t* col
               float* deg_out, float* dis_out, void* ws, size_t ws_bytes, hipStream_t s,
               bool values = true);
 size_t self_loops_workspace(int64_t n);
+// gcn_norm's dis_out for an A (n x n) whose values are all 1 and which has
+// no diagonal, from the row lengths alone (bit-identical to gcn_norm's);
+// sets *flag (not cleared) when a row of A + I is longer than 2^24, where
+// gcn_norm's result differs.
+void unit_self_loop_dis(int64_t n, const int32_t* row_ptr, float* dis, int32_t* flag,
+                        hipStream_t s);
 
 // sage.hip
 // `blocked` (optional): the column-blocked form of the same structure; the

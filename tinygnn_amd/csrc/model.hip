@@ -90,6 +90,7 @@ struct tg_model_s {
     int precision = TG_PRECISION_FAST;
     int built_precision = -1;  // precision the cached plans were built for
     int64_t block_rows = -1;   // column blocking (tg_model_set_blocking)
+    bool direct_split = true;  // tg_model_set_self_loop_split
     int64_t built_block_rows = -2;  // blocking the blocked copies were built for (-2: none)
 
     // bumped by every add_*_layer: the cached adjacency state (which of
@@ -112,6 +113,9 @@ struct tg_model_s {
     // sl_v holds A + I's values (GCN present, unless only the factored
     // blocked path reads A + I)
     bool sl_values = false;
+    // blk_sl was split from A directly with the diagonal placed per row, and
+    // A + I itself (sl_rp, sl_ci, sl_v) was not written
+    bool blk_sl_direct = false;
     DeviceBuffer flag;
     tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
@@ -292,7 +296,9 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     // fast GAT, 32-column groups: 13.5-13.9 ms at 5-10 blocks against 12.0 ms).
     const int gc_sl = (m.unit_sl && !m.need_sl()) ? 32 : 64;
     const int64_t r_sl = resolve_block_rows(m.block_rows, n, nnz + n, gc_sl);
-    if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
+    if (m.blk_sl_direct) {
+        // A + I's blocked copy was split from A by prepare_adjacency
+    } else if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() && !m.unit_sl ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s,
@@ -357,11 +363,9 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     }
     m.unit_sl = false;
     m.sl_values = false;
+    m.blk_sl_direct = false;
     if (m.need_norm() || m.need_sl()) {
         require(nnz + n < (int64_t(1) << 31), "Model::forward: nnz + n must be < 2^31");
-        m.sl_rp.reserve((n + 1) * sizeof(int32_t));
-        m.sl_ci.reserve((nnz + n) * sizeof(int32_t));
-        m.sl_v.reserve((nnz + n) * sizeof(float));
         m.work.reserve(self_loops_workspace(n));
         m.flag.reserve(sizeof(int32_t));
         m.flag_host.reserve(2 * sizeof(int32_t));
@@ -390,28 +394,56 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         // normalised values unless its aggregation will run factored (the
         // blocking prepare_blocked resolves for a unit A + I)
         const int gc_unit = m.need_sl() ? 64 : 32;
-        const bool will_block = resolve_block_rows(m.block_rows, n, nnz + n, gc_unit) > 0;
-        m.sl_values = m.need_norm() && !(unit_v && will_block);
-        if (m.need_norm()) {
+        const int64_t r_unit = resolve_block_rows(m.block_rows, n, nnz + n, gc_unit);
+        const bool will_block = r_unit > 0;
+        if (m.direct_split && unit_v && will_block && !m.need_sl()) {
+            // Only the factored blocked GCN reads A + I: its blocked copy is
+            // split from A directly, each row's diagonal placed where
+            // add_self_loops inserts it, and dis comes from the row lengths;
+            // A + I itself is never written (config-E reference-semantics GCN
+            // 10.3 -> 9.x ms).  Valid for sorted rows of A without a
+            // diagonal, which the build checks; otherwise the path below.
             m.dis.reserve(n * sizeof(float));
-            gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                     m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(), m.work.size(),
-                     s, m.sl_values);
-        } else {
-            add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
-                           m.sl_v.as<float>(), m.work.get(), m.work.size(), s, false);
-        }
-        if (unit_v) {
-            // no diagonal in A: A + I has nnz + n entries
-            TG_HIP(hipMemcpyAsync(host + 1, m.sl_rp.as<int32_t>() + n, sizeof(int32_t),
+            fill_i32(m.flag.as<int32_t>(), 1, 0, s);
+            unit_self_loop_dis(n, rp, m.dis.as<float>(), m.flag.as<int32_t>(), s);
+            TG_HIP(hipMemcpyAsync(host + 1, m.flag.as<int32_t>(), sizeof(int32_t),
                                   hipMemcpyDeviceToHost, s));
-            TG_HIP(hipStreamSynchronize(s));
-            m.unit_sl = host[1] == nnz + n;
-            if (!m.unit_sl && !m.sl_values) {  // a diagonal of A: A + I holds a 2
-                m.sl_values = true;
+            if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
+            // (synchronises s: host[1] is current after the call)
+            const bool built =
+                build_blocked_self_loops(*m.blk_sl, n, nnz, rp, ci, r_unit, maxf, s, chunk);
+            if (built && host[1] == 0) {
+                m.blk_sl->group_cols = 32;
+                m.blk_sl_direct = true;
+                m.unit_sl = true;
+            }
+        }
+        if (!m.blk_sl_direct) {
+            m.sl_rp.reserve((n + 1) * sizeof(int32_t));
+            m.sl_ci.reserve((nnz + n) * sizeof(int32_t));
+            m.sl_v.reserve((nnz + n) * sizeof(float));
+            m.sl_values = m.need_norm() && !(unit_v && will_block);
+            if (m.need_norm()) {
+                m.dis.reserve(n * sizeof(float));
                 gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                          m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(),
-                         m.work.size(), s, true);
+                         m.work.size(), s, m.sl_values);
+            } else {
+                add_self_loops(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                               m.sl_v.as<float>(), m.work.get(), m.work.size(), s, false);
+            }
+            if (unit_v) {
+                // no diagonal in A: A + I has nnz + n entries
+                TG_HIP(hipMemcpyAsync(host + 1, m.sl_rp.as<int32_t>() + n, sizeof(int32_t),
+                                      hipMemcpyDeviceToHost, s));
+                TG_HIP(hipStreamSynchronize(s));
+                m.unit_sl = host[1] == nnz + n;
+                if (!m.unit_sl && !m.sl_values) {  // a diagonal of A: A + I holds a 2
+                    m.sl_values = true;
+                    gcn_norm(n, nnz, rp, ci, v, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
+                             m.sl_v.as<float>(), nullptr, m.dis.as<float>(), m.work.get(),
+                             m.work.size(), s, true);
+                }
             }
         }
         // A + I's row plan is built by ensure_plan_sl, once the blocking is known
@@ -703,7 +735,7 @@ int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block) {
 }
 
 int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
-                           int64_t* blocks_raw, int64_t* cols_raw) {
+                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct) {
     return guard([&] {
         require(model != nullptr, "model is null");
         const tg::BlockedCSR* sl = model->have_cache ? model->blk_sl.get() : nullptr;
@@ -712,6 +744,15 @@ int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_s
         if (cols_sl) *cols_sl = sl ? sl->group_cols : 0;
         if (blocks_raw) *blocks_raw = raw ? raw->n_blocks : 0;
         if (cols_raw) *cols_raw = raw ? raw->group_cols : 0;
+        if (sl_direct) *sl_direct = sl && model->blk_sl_direct ? 1 : 0;
+    });
+}
+
+int tg_model_set_self_loop_split(tg_model_t model, int direct) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        model->direct_split = direct != 0;
+        model->have_cache = false;
     });
 }
 
