@@ -23,7 +23,8 @@ def _t(gpu, x):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (5, 3, 7), (37, 41, 16), (130, 602, 41),
                                    (64, 1433, 16), (300, 256, 41), (257, 17, 64),
-                                   (100, 64, 7), (513, 33, 300),
+                                   (100, 64, 7), (513, 33, 300), (1000, 77, 24),
+                                   (2708, 1433, 64),
                                    # above 2^21 outputs: the large in-order kernels
                                    (9000, 40, 300), (70000, 33, 31), (300000, 9, 8)])
 def test_matmul_inorder_bitexact(gpu, restate, m, k, n):

@@ -370,11 +370,16 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         m.flag.reserve(sizeof(int32_t));
         m.flag_host.reserve(2 * sizeof(int32_t));
         int32_t* host = m.flag_host.as<int32_t>();
-        // fast precision: all of A's values exactly 1?  Then, with no
-        // diagonal in A, every value of A + I is 1 and a blocked GCN
-        // aggregation is factored (it reads no values)
+        // the blocking prepare_blocked resolves for a unit A + I
+        const int gc_unit = m.need_sl() ? 64 : 32;
+        const int64_t r_unit = resolve_block_rows(m.block_rows, n, nnz + n, gc_unit);
+        const bool will_block = r_unit > 0;
+        // fast precision, blocked: all of A's values exactly 1?  Then, with
+        // no diagonal in A, every value of A + I is 1 and the blocked GCN
+        // aggregation is factored (it reads no values); unblocked, the
+        // check and its synchronisation are skipped
         bool unit_v = false;
-        if (m.need_norm() && m.precision != TG_PRECISION_EXACT) {
+        if (m.need_norm() && m.precision != TG_PRECISION_EXACT && will_block) {
             fill_i32(m.flag.as<int32_t>(), 1, 1, s);
             const int64_t blocks =
                 std::min<int64_t>(std::max<int64_t>(ceil_div(nnz, 1024), 1), 4096);
@@ -391,11 +396,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
             unit_v = host[0] == 1;
         }
         // A + I's values: GAT reads the structure alone; GCN needs the
-        // normalised values unless its aggregation will run factored (the
-        // blocking prepare_blocked resolves for a unit A + I)
-        const int gc_unit = m.need_sl() ? 64 : 32;
-        const int64_t r_unit = resolve_block_rows(m.block_rows, n, nnz + n, gc_unit);
-        const bool will_block = r_unit > 0;
+        // normalised values unless its aggregation will run factored
         if (m.direct_split && unit_v && will_block && !m.need_sl()) {
             // Only the factored blocked GCN reads A + I: its blocked copy is
             // split from A directly, each row's diagonal placed where
