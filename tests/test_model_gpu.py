@@ -459,13 +459,16 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
         np.testing.assert_array_equal(exact[100].view(np.int32), want.view(np.int32))
 
 
+@pytest.mark.parametrize("model", ["gcn", "gat"])
 @pytest.mark.parametrize("order", ["sorted", "unsorted"])
-def test_direct_self_loop_split_long_rows(gpu, restate, order):
-    """The factored GCN's blocked A + I split straight from A (rows of up to
-    9,000 entries: the workgroup-per-row kernels past 4,096) equals the copy
-    split from the A + I gcn_norm writes, bit for bit in both forward modes,
-    and the oracle within tolerance.  A row out of order makes the direct
-    split decline (sl_direct False) and the forward take the written A + I."""
+def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
+    """The blocked A + I split straight from A (rows of up to 9,000 entries:
+    the workgroup-per-row kernels past 4,096) equals the copy split from the
+    A + I gcn_norm / add_self_loops write, bit for bit in both forward modes,
+    and the oracle within tolerance: the factored GCN (32-column groups) and a
+    GAT carrying its softmax across the passes (64-column groups).  A row
+    out of order makes the direct split decline (sl_direct False) and the
+    forward take the written A + I."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(91)
     n = 3000
@@ -477,7 +480,7 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order):
     if order == "unsorted":  # one long row reversed
         i = int(np.argmax(np.diff(g.row_ptr)))
         g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]] = g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]][::-1]
-    spec = synth.spec_gcn(16, 64, 5)
+    spec = synth.spec_gcn(16, 64, 5) if model == "gcn" else synth.spec_gat(16, 64, 2, 5)
     w = synth.model_weights(spec, seed=9)
     x = rng.standard_normal((n, 16)).astype(np.float32)
     da = tg.DeviceCSR.from_numpy(n, n, g.row_ptr, g.col_ind, g.val)
@@ -489,10 +492,14 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order):
         m.set_self_loop_split(direct)
         outs[direct] = m.forward(da, xt, mode=tg.FORWARD_CACHED).cpu().numpy()
         info = m.blocking_info()
-        assert info["blocks_sl"] == 6 and info["cols_sl"] == 32
+        assert info["blocks_sl"] == 6 and info["cols_sl"] == (32 if model == "gcn" else 64)
         assert info["sl_direct"] == (direct and order == "sorted")
         again = m.forward(da, xt, mode=tg.FORWARD_REFERENCE).cpu().numpy()
         np.testing.assert_array_equal(bits(again), bits(outs[direct]))
+        # a new blocking setting between cached calls rebuilds the copy
+        m.set_blocking(1000)
+        m.forward(da, xt, mode=tg.FORWARD_CACHED)
+        assert m.blocking_info()["blocks_sl"] == 3
     np.testing.assert_array_equal(bits(outs[True]), bits(outs[False]))
     assert_close(outs[True], restate.model_forward(spec, w, g, x), what=f"direct split {order}")
 

@@ -1018,9 +1018,9 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
     }
 }
 
-size_t gat_ws(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
+size_t gat_ws_partials(int64_t n_partials, int64_t n, int64_t heads, int64_t f, int concat) {
     Carver c(nullptr, 0);
-    c.take<float>(std::max<int64_t>(p.n_partials, 1) * gat_stat_slots(heads, f) * 2);
+    c.take<float>(std::max<int64_t>(n_partials, 1) * gat_stat_slots(heads, f) * 2);
     if (!concat && heads > 1) c.take<float>(n * heads * f);
     return c.bytes();
 }
@@ -1040,7 +1040,18 @@ void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ld
 }
 
 size_t gat_workspace(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat) {
-    return gat_ws(p, n, heads, f, concat);
+    return gat_ws_partials(p.n_partials, n, heads, f, concat);
+}
+
+int64_t blocked_max_partials(const BlockedCSR& bk) {
+    int64_t m = 0;
+    for (const auto& p : bk.plans) m = std::max(m, p->n_partials);
+    return m;
+}
+
+size_t gat_workspace_blocked(const BlockedCSR& bk, int64_t n, int64_t heads, int64_t f,
+                             int concat) {
+    return gat_ws_partials(blocked_max_partials(bk), n, heads, f, concat);
 }
 
 void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
@@ -1061,7 +1072,7 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
         require(ftot <= p.max_f, "GATLayer: heads * f exceeds the plan's max_f");
     DeviceBuffer own;
     if (work == nullptr) {
-        own.resize(gat_ws(p, n, heads, f, concat));
+        own.resize(gat_ws_partials(p.n_partials, n, heads, f, concat));
         work = own.get();
         work_bytes = own.size();
     }
@@ -1118,13 +1129,14 @@ bool gat_blocked_ok(int64_t heads, int64_t f, int concat) {
     return heads == 1 || f % 32 == 0;            // 32-column tiles inside one head
 }
 
-void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
+void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int64_t n,
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
                            float* rmax, float* rinv, void* work, size_t work_bytes,
                            hipStream_t s, bool exact) {
-    require(bk.n == n && p.m == n, "GATLayer: blocked structure or plan rows differ from n");
+    require(bk.n == n && (plan == nullptr || plan->m == n),
+            "GATLayer: blocked structure or plan rows differ from n");
     require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
     require(heads * f < (int64_t(1) << 31), "GATLayer: heads * f too large");
     if (n == 0) return;
@@ -1145,7 +1157,7 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
         P.dst = dst;
         P.m_state = rmax;
         P.s_state = rinv;
-        P.pstats = cw.take<float>(std::max<int64_t>(p.n_partials, 1) * groups * 2);
+        P.pstats = cw.take<float>(std::max<int64_t>(blocked_max_partials(bk), 1) * groups * 2);
         P.bias = bias;
         P.heads = static_cast<int>(heads);
         P.head_cols = static_cast<int>(f);
@@ -1154,13 +1166,16 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_
         P.post = post;
         P.vec_io = ftot % 4 == 0 && ldo % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
                    (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
-        const int64_t maxp = std::max<int64_t>(p.n_partials, 1);
+        // partial slots: the block plans' (work holds gat_workspace_blocked)
+        const int64_t maxp = std::max<int64_t>(blocked_max_partials(bk), 1);
         if (gc == 64)
             gat_online_passes<16>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
         else
             gat_online_passes<8>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
         return;
     }
+    require(plan != nullptr, "GATLayer: the statistics need the unblocked plan");
+    const tg_spmm_plan_s& p = *plan;
     const bool vec4 = heads % 4 == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
     const unsigned grid = static_cast<unsigned>(ceil_div(p.n_chunks, 4));
     if (exact) {

@@ -59,6 +59,10 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
 void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,
                 const float* al, const float* ar, float* src, float* dst, hipStream_t s);
 size_t gat_workspace(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f, int concat);
+// The workspace of a blocked GAT aggregation in fast precision (the
+// softmax carried across the passes), sized by the block plans.
+size_t gat_workspace_blocked(const BlockedCSR& bk, int64_t n, int64_t heads, int64_t f,
+                             int concat);
 int64_t gat_stat_slots(int64_t heads, int64_t f);
 void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
                    const int32_t* ci, const float* wh, int64_t ldwh, const float* src,
@@ -68,16 +72,19 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
 // Column-blocked GAT aggregation: whether a layer's layout
 // allows it (concatenated or single head, heads of whole 32-column tiles),
 // and the aggregation itself over the blocked
-// form of the structure (p, ci: the unblocked structure's plan and columns,
-// for the softmax statistics; rmax, rinv: n x max(heads, ceil(heads*f/32))
+// form of the structure (plan, ci: the unblocked structure's plan and
+// columns, for the softmax statistics of the exact path and of layers whose
+// heads are not whole lane groups; null where fast precision carries the
+// softmax across the passes; rmax, rinv: n x max(heads, ceil(heads*f/32))
 // scratch, the row statistics or, in fast precision, the softmax state the
 // passes carry per (row, column group); the passes compute each entry's
-// attention weight and store none; work: at least gat_workspace(p, ...)
+// attention weight and store none; work: at least gat_workspace(*plan, ...),
+// or gat_workspace_blocked(bk, ...) without a plan
 // bytes; exact: the reference's
 // operation order, for a plan that splits no row and a blocked structure in
 // block order).
 bool gat_blocked_ok(int64_t heads, int64_t f, int concat);
-void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s& p, int64_t n,
+void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int64_t n,
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,

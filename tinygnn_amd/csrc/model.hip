@@ -324,7 +324,8 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
 // GCN runs on the block plans alone (config-E reference-semantics GCN: one
 // plan build and its synchronisation fewer per call).
 void ensure_plan_sl(tg_model_s& m, int64_t n, int64_t nnz, hipStream_t s) {
-    const bool needed = m.need_sl() || (m.need_norm() && !m.blk_sl);
+    // (a blocked copy split from A directly serves every reader of A + I)
+    const bool needed = !m.blk_sl_direct && (m.need_sl() || (m.need_norm() && !m.blk_sl));
     if (!needed || m.plan_sl_built) return;
     const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
     build_plan(*m.plan_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.max_wide(), chunk, s);
@@ -337,8 +338,9 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                       m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision &&
                       m.built_layers_gen == m.layers_gen;
     // a new blocking setting keeps the cached state, unless A + I's values
-    // were skipped for the factored path (an unblocked GCN needs them)
-    const bool values_ok = m.sl_values || !m.need_norm();
+    // were skipped for the factored path (an unblocked GCN needs them), or
+    // A + I's blocked copy came straight from A (A + I was not written)
+    const bool values_ok = (m.sl_values || !m.need_norm()) && !m.blk_sl_direct;
     if (mode == TG_FORWARD_CACHED && same && (values_ok || m.built_block_rows == m.block_rows)) {
         // a cached call after a reference-mode one (or a new blocking
         // setting) adds the blocked copies to the state it reuses
@@ -397,26 +399,39 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         }
         // A + I's values: GAT reads the structure alone; GCN needs the
         // normalised values unless its aggregation will run factored
-        if (m.direct_split && unit_v && will_block && !m.need_sl()) {
-            // Only the factored blocked GCN reads A + I: its blocked copy is
-            // split from A directly, each row's diagonal placed where
-            // add_self_loops inserts it, and dis comes from the row lengths;
-            // A + I itself is never written (config-E reference-semantics GCN
-            // 10.3 -> 9.x ms).  Valid for sorted rows of A without a
-            // diagonal, which the build checks; otherwise the path below.
-            m.dis.reserve(n * sizeof(float));
-            fill_i32(m.flag.as<int32_t>(), 1, 0, s);
-            unit_self_loop_dis(n, rp, m.dis.as<float>(), m.flag.as<int32_t>(), s);
-            TG_HIP(hipMemcpyAsync(host + 1, m.flag.as<int32_t>(), sizeof(int32_t),
-                                  hipMemcpyDeviceToHost, s));
+        // GAT layers in fast precision whose softmax rides along the blocked
+        // passes read A + I's structure only through its blocked copy
+        bool gat_online = m.precision != TG_PRECISION_EXACT && !m.need_norm();
+        for (auto& l : m.layers)
+            if (l.type == LType::GAT && !gat_blocked_ok(l.heads, l.out, l.concat))
+                gat_online = false;
+        const bool gcn_direct = unit_v && !m.need_sl();
+        const bool gat_direct = m.need_sl() && gat_online;
+        if (m.direct_split && will_block && (gcn_direct || gat_direct)) {
+            // Only blocked passes without values read A + I (the factored
+            // GCN, or GAT carrying its softmax): the blocked copy is split
+            // from A directly, each row's diagonal placed where
+            // add_self_loops inserts it, and the GCN's dis comes from the
+            // row lengths; A + I itself is never written (config-E
+            // reference-semantics GCN 10.30 -> 9.80 ms).  Valid for sorted
+            // rows of A without a diagonal, which the build checks;
+            // otherwise the path below.
+            host[1] = 0;
+            if (gcn_direct) {
+                m.dis.reserve(n * sizeof(float));
+                fill_i32(m.flag.as<int32_t>(), 1, 0, s);
+                unit_self_loop_dis(n, rp, m.dis.as<float>(), m.flag.as<int32_t>(), s);
+                TG_HIP(hipMemcpyAsync(host + 1, m.flag.as<int32_t>(), sizeof(int32_t),
+                                      hipMemcpyDeviceToHost, s));
+            }
             if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
             // (synchronises s: host[1] is current after the call)
             const bool built =
                 build_blocked_self_loops(*m.blk_sl, n, nnz, rp, ci, r_unit, maxf, s, chunk);
             if (built && host[1] == 0) {
-                m.blk_sl->group_cols = 32;
+                m.blk_sl->group_cols = gcn_direct ? 32 : 64;
                 m.blk_sl_direct = true;
-                m.unit_sl = true;
+                m.unit_sl = gcn_direct;
             }
         }
         if (!m.blk_sl_direct) {
@@ -516,7 +531,9 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
         if (l.type == LType::SAGE)
             ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, dataflow, nnz));
         if (l.type == LType::GAT)
-            ws = std::max(ws, gat_workspace(*m.plan_sl, n, l.heads, l.out, l.concat));
+            ws = std::max(ws, m.blk_sl_direct
+                                  ? gat_workspace_blocked(*m.blk_sl, n, l.heads, l.out, l.concat)
+                                  : gat_workspace(*m.plan_sl, n, l.heads, l.out, l.concat));
     }
     m.act[0].reserve(n * wmax * sizeof(float));
     m.act[1].reserve(n * wmax * sizeof(float));
@@ -601,7 +618,8 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             if (blocked) {
                 float* rmax = dst + n * l.heads;
                 float* rinv = rmax + n * gat_stat_slots(l.heads, l.out);
-                gat_aggregate_blocked(*m.blk_sl, *m.plan_sl, n, l.heads, l.out,
+                gat_aggregate_blocked(*m.blk_sl, m.blk_sl_direct ? nullptr : m.plan_sl.get(), n,
+                                      l.heads, l.out,
                                       m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
                                       l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
                                       l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s,
