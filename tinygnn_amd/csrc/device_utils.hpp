@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace tg {
 
@@ -67,6 +68,41 @@ __device__ __forceinline__ T block_exclusive_scan(T v, T* lds, T* total) {
     __syncthreads();
     *total = tot;
     return wave_off + inc - v;
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Lane SRC of the caller's group of LPR consecutive lanes (groups aligned to
+// LPR), to every lane of the group.  16- and 4-lane groups use one DPP
+// move (row broadcast within a 16-lane row, quad permute), with no LDS
+// traffic: the config-E GAT passes (16-lane groups) ran 1.5% faster than
+// with ds_bpermute.  Other widths keep the shuffle: two DPP moves and a
+// select for 8 lanes were no faster, and readlane for 32 lanes made the
+// F=128 SpMM 0.8% slower.  Every lane of the caller's group must be
+// active; lanes of other groups may not be.
+template <int LPR, int SRC>
+__device__ __forceinline__ int group_bcast(int v) {
+    static_assert(SRC >= 0 && SRC < LPR, "source lane outside the group");
+    if constexpr (LPR == 16) {
+        return __builtin_amdgcn_update_dpp(0, v, 0x150 + SRC, 0xF, 0xF, false);  // row_newbcast
+    } else if constexpr (LPR == 4) {
+        return __builtin_amdgcn_update_dpp(0, v, SRC | (SRC << 2) | (SRC << 4) | (SRC << 6), 0xF,
+                                           0xF, false);  // quad_perm
+    } else {
+        return __shfl(v, SRC, LPR);
+    }
+}
+
+template <int LPR, int SRC>
+__device__ __forceinline__ float group_bcast(float v) {
+    return __int_as_float(group_bcast<LPR, SRC>(__float_as_int(v)));
 }
 
 // Non-temporal (streaming) loads for data read exactly once.

@@ -850,12 +850,14 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
         }
         const int cnt = e - base < BE ? e - base : BE;
         float bv[U][4];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int col = __shfl(cl[u % CPL], u / CPL, LPR);
+        // entry u of the batch is slot u % CPL of lane u / CPL: compile-time
+        // lanes, broadcast without LDS (group_bcast)
+        static_for<0, U>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const int col = group_bcast<LPR, u / CPL>(cl[u % CPL]);
             const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
             ldv<4>(reinterpret_cast<const float*>(bl + off), bv[u]);
-        }
+        });
         fetch(base + BE);
         // the batch's scores, the group's maximum, the rescaled carry
         float ev[CPL];
@@ -883,16 +885,16 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
             wl[j] = base + l * CPL + j < e ? expf(ev[j] - m) : 0.0f;
             s += wl[j];
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const float w = __shfl(wl[u % CPL], u / CPL, LPR);
+        static_for<0, U>([&](auto uc) {
+            constexpr int u = decltype(uc)::value;
+            const float w = group_bcast<LPR, u / CPL>(wl[u % CPL]);
             const bool valid = u < cnt;  // a select, not a branch
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float nx = __builtin_fmaf(w, bv[u][k], acc[k]);
                 acc[k] = valid ? nx : acc[k];
             }
-        }
+        });
     }
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, LPR);

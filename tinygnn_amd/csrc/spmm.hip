@@ -646,11 +646,6 @@ struct Unroll {
     static constexpr int value = VPL == 1 ? 16 : VPL == 2 ? 8 : 4;
 };
 
-// Shuffle of an edge entry held by lane `src` of the caller's lane group.
-__device__ __forceinline__ int shfl_i(int v, int src, int width) { return __shfl(v, src, width); }
-__device__ __forceinline__ float shfl_f(float v, int src, int width) {
-    return __shfl(v, src, width);
-}
 
 template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
@@ -768,70 +763,146 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
         // U gathers in flight per step; in the chunk's last, partial batch
         // the slots past its end gather row 0 (in bounds: cl is 0 there) and
         // are not accumulated.
-        const int cnt = e - base < BE ? e - base : BE;
+        if constexpr (LPR <= 16) {
+            const int cnt = e - base < BE ? e - base : BE;
+            // slot s0 + u of the batch is entry (s0 + u) % CPL of lane (s0 + u) / CPL:
+            // compile-time lanes, broadcast without LDS (group_bcast)
+            static_for<0, BE / U>([&](auto sc) {
+                constexpr int s0 = decltype(sc)::value * U;
+                if (s0 < cnt) {  // uniform across the group: no early exit in the unrolled body
+                    int col[U];
+                    float w[U];
+                    static_for<0, U>([&](auto uc) {
+                        constexpr int u = decltype(uc)::value;
+                        col[u] = group_bcast<LPR, (s0 + u) / CPL>(cl[(s0 + u) % CPL]);
+                        w[u] = 1.0f;
+                        if constexpr (MODE == kAggWeighted)
+                            w[u] = group_bcast<LPR, (s0 + u) / CPL>(wl[(s0 + u) % CPL]);
+                    });
+                    float bv[U][VPL][VEC];
 #pragma unroll
-        for (int s0 = 0; s0 < BE; s0 += U) {
-            if (s0 < cnt) {  // uniform across the group: no early exit in the unrolled body
-                int col[U];
-                float w[U];
+                    for (int u = 0; u < U; ++u) {
+                        const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    col[u] = shfl_i(cl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
-                    w[u] = 1.0f;
-                    if constexpr (MODE == kAggWeighted)
-                        w[u] = shfl_f(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
-                }
-                float bv[U][VPL][VEC];
+                        for (int v = 0; v < VPL; ++v)
+                            load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                    }
+                    if (s0 == 0) fetch(base + BE);
+                    if constexpr (MODE == kAggAttn) {
+                        // alpha_ij = exp(LeakyReLU(s_i + d_j) - max_i) * (1/sum_i)
+                        // (layers.cpp:1068-1090), once per entry and head
+                        if (s0 == 0) {
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
-#pragma unroll
-                    for (int v = 0; v < VPL; ++v)
-                        load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
-                }
-                if (s0 == 0) fetch(base + BE);
-                if constexpr (MODE == kAggAttn) {
-                    // alpha_ij = exp(LeakyReLU(s_i + d_j) - max_i) * (1/sum_i)
-                    // (layers.cpp:1068-1090), once per entry and head
-                    if (s0 == 0) {
-#pragma unroll
-                        for (int j = 0; j < CPL; ++j) {
-                            const float x = att_s + dl[j];
-                            const float t = ((x >= 0.0f) ? x : epi.att_slope * x) - att_m;
-                            wl[j] = (epi.exact_exp ? exp_rn(t) : expf(t)) * att_r;
+                            for (int j = 0; j < CPL; ++j) {
+                                const float x = att_s + dl[j];
+                                const float t = ((x >= 0.0f) ? x : epi.att_slope * x) - att_m;
+                                wl[j] = (epi.exact_exp ? exp_rn(t) : expf(t)) * att_r;
+                            }
                         }
                     }
-                }
-                // the weight of slot u: attention weights are broadcast at
-                // their fma (not all U held at once: fewer live registers)
-                auto wt = [&](int u) {
-                    if constexpr (MODE == kAggAttn)
-                        return shfl_f(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
-                    else
-                        return w[u];
-                };
-                if (cnt == BE) {  // a full batch: every slot is an entry
+                    // the weight of slot u: attention weights are broadcast at
+                    // their fma (not all U held at once: fewer live registers)
+                    auto wt = [&](auto uc) {
+                        constexpr int u = decltype(uc)::value;
+                        if constexpr (MODE == kAggAttn)
+                            return group_bcast<LPR, (s0 + u) / CPL>(wl[(s0 + u) % CPL]);
+                        else
+                            return w[u];
+                    };
+                    if (cnt == BE) {  // a full batch: every slot is an entry
+                        static_for<0, U>([&](auto uc) {
+                            constexpr int u = decltype(uc)::value;
+                            const float wu = wt(uc);
 #pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        const float wu = wt(u);
+                            for (int v = 0; v < VPL; ++v)
 #pragma unroll
-                        for (int v = 0; v < VPL; ++v)
+                                for (int k = 0; k < VEC; ++k)
+                                    acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                        });
+                    } else {
+                        static_for<0, U>([&](auto uc) {
+                            constexpr int u = decltype(uc)::value;
+                            const bool valid = s0 + u < cnt;  // a select, not a branch
+                            const float wu = wt(uc);
 #pragma unroll
-                            for (int k = 0; k < VEC; ++k)
-                                acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                                for (int k = 0; k < VEC; ++k) {
+                                    const float nx = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                                    acc[v][k] = valid ? nx : acc[v][k];
+                                }
+                        });
                     }
-                } else {
+                }
+            });
+        } else {
+            // 32- and 64-lane groups: runtime-lane shuffles (the compile-time
+            // form measured 2-3% slower for the F=128 / F=512 SpMM)
+            const int cnt = e - base < BE ? e - base : BE;
+#pragma unroll
+            for (int s0 = 0; s0 < BE; s0 += U) {
+                if (s0 < cnt) {  // uniform across the group: no early exit in the unrolled body
+                    int col[U];
+                    float w[U];
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
-                        const bool valid = s0 + u < cnt;  // a select, not a branch
-                        const float wu = wt(u);
+                        col[u] = __shfl(cl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+                        w[u] = 1.0f;
+                        if constexpr (MODE == kAggWeighted)
+                            w[u] = __shfl(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+                    }
+                    float bv[U][VPL][VEC];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
 #pragma unroll
                         for (int v = 0; v < VPL; ++v)
+                            load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                    }
+                    if (s0 == 0) fetch(base + BE);
+                    if constexpr (MODE == kAggAttn) {
+                        // alpha_ij = exp(LeakyReLU(s_i + d_j) - max_i) * (1/sum_i)
+                        // (layers.cpp:1068-1090), once per entry and head
+                        if (s0 == 0) {
 #pragma unroll
-                            for (int k = 0; k < VEC; ++k) {
-                                const float nx = combine<MODE>(acc[v][k], bv[u][v][k], wu);
-                                acc[v][k] = valid ? nx : acc[v][k];
+                            for (int j = 0; j < CPL; ++j) {
+                                const float x = att_s + dl[j];
+                                const float t = ((x >= 0.0f) ? x : epi.att_slope * x) - att_m;
+                                wl[j] = (epi.exact_exp ? exp_rn(t) : expf(t)) * att_r;
                             }
+                        }
+                    }
+                    // the weight of slot u: attention weights are broadcast at
+                    // their fma (not all U held at once: fewer live registers)
+                    auto wt = [&](int u) {
+                        if constexpr (MODE == kAggAttn)
+                            return __shfl(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
+                        else
+                            return w[u];
+                    };
+                    if (cnt == BE) {  // a full batch: every slot is an entry
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const float wu = wt(u);
+#pragma unroll
+                            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                                for (int k = 0; k < VEC; ++k)
+                                    acc[v][k] = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                        }
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const bool valid = s0 + u < cnt;  // a select, not a branch
+                            const float wu = wt(u);
+#pragma unroll
+                            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                                for (int k = 0; k < VEC; ++k) {
+                                    const float nx = combine<MODE>(acc[v][k], bv[u][v][k], wu);
+                                    acc[v][k] = valid ? nx : acc[v][k];
+                                }
+                        }
                     }
                 }
             }
