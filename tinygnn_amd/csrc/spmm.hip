@@ -763,7 +763,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
         // U gathers in flight per step; in the chunk's last, partial batch
         // the slots past its end gather row 0 (in bounds: cl is 0 there) and
         // are not accumulated.
-        if constexpr (LPR <= 16) {
+        if constexpr (LPR == 16 || LPR == 4) {
             const int cnt = e - base < BE ? e - base : BE;
             // slot s0 + u of the batch is entry (s0 + u) % CPL of lane (s0 + u) / CPL:
             // compile-time lanes, broadcast without LDS (group_bcast)
@@ -836,8 +836,8 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                 }
             });
         } else {
-            // 32- and 64-lane groups: runtime-lane shuffles (the compile-time
-            // form measured 2-3% slower for the F=128 / F=512 SpMM)
+            // other group widths: runtime-lane shuffles (the compile-time form
+            // measured 2-3% slower for the F=128 / F=512 SpMM, no faster at 8)
             const int cnt = e - base < BE ? e - base : BE;
 #pragma unroll
             for (int s0 = 0; s0 < BE; s0 += U) {
