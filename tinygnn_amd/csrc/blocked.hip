@@ -179,228 +179,237 @@ __global__ __launch_bounds__(256) void block_split_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Sorted-row split.  When every row's columns are non-decreasing (every CSR
-// edge_list_to_csr builds), a block's entries in a row form one contiguous
-// run, so the split reduces to the runs' starts: entry j starts the runs of
-// blocks (block(c[j-1]), block(c[j])], with block(c[-1]) = -1; blocks past
-// the last entry's start at the row's end.  G lanes share a row (16, 64 or a
-// 256-thread workgroup by row length), lane l taking entries l, l + G, ...
-// with kSortedU of them loaded per step and the next step's loaded ahead;
-// the starts collect in LDS.  The count pass writes each block's count and
-// start, the scatter pass copies every entry to its block's row segment at
-// its rank in the run.  Its purpose is vdiag: every row i also holds a
-// virtual entry (column i, no value) at its sorted position, before its
-// first column > i, which gives A + I's blocked copy straight from A (the
-// general kernel above handles any order, without that entry).  A row found
-// out of order sets flags[0], one with a diagonal flags[1]; it then counts
-// its whole length in block 0 (the totals stay those of a valid split), the
-// scatter pass writes nothing and the caller takes another path.
+// Flat split, for rows whose entries are in block order (sorted rows: every
+// CSR edge_list_to_csr builds).  A block's entries in a row are then one
+// run, and the split reduces to each run's start: entry k starts the runs of
+// blocks (block(c[k-1]), block(c[k])] of its row (all blocks up to block(c[k])
+// when k starts the row).  Instead of a group of lanes per row (bound by the
+// row-level latency of dependent loads: config E's count + scatter 0.63 ms
+// with the general kernel, a read-only pass one wave per row 0.13 ms), both
+// passes stream col_ind one entry per thread, coalesced, and find an
+// entry's row from a bitmap of row starts: with rank = the number of row
+// starts at or before k (a scan over 64-entry slices plus a popcount within
+// the slice), the row is the rank-th non-empty row.  The count pass writes
+// the run starts (every start preset to the row's length, for the blocks
+// past its last entry); counts, their scan and the output bases follow per
+// (block, row); the scatter pass writes every entry at its base plus its
+// position.  An entry that steps back to an earlier block sets flags[0] (the
+// caller then runs the general split).  With vdiag every row i also holds a
+// virtual entry (column i, no value) before its first column > i: the
+// diagonal of A + I for an A without one; a diagonal in A sets flags[1].
 // ---------------------------------------------------------------------------
-constexpr int kShortSplit = 512;
-constexpr int kLongSplit = 4096;
-
-struct SortedSplit {
+struct FlatSplit {
     const int32_t* rp;
     const int32_t* ci;
-    const float* v;           // scatter: values to copy, or null
-    int64_t n;
+    const float* v;             // scatter: values to copy, or null
+    int64_t n, nnz;
     int rows_per_block;
     double inv_rows;
     int nb;
     int vdiag;
-    const int32_t* long_list;  // rows longer than kLongSplit, *long_count of them
-    const int32_t* long_count;
-    int32_t* cnt;              // count pass: [nb * n] entries per block and row
-    const int32_t* brp;        // scatter pass: the scanned counts
-    int32_t* starts;           // [nb * n] each block's first position in the row
-    int32_t* ins;              // [n] (vdiag) the virtual entry's position in the row
+    const uint64_t* bits;       // bit k: entry k starts a (non-empty) row
+    const int32_t* slice_rank;  // row starts before each 64-entry slice
+    const int32_t* nz_rows;     // the non-empty rows in order
+    int32_t* starts;            // [nb * n] each block's first position in the row
+    int32_t* ins;               // [n] (vdiag) the virtual entry's position
+    const int32_t* obase;       // scatter: [nb * n] brp - starts - rp[row]
     int32_t* bci;
     uint16_t* bci16;
     float* bv;
-    int32_t* flags;            // [0] a row out of order, [1] (vdiag) a row with a diagonal
+    int32_t* flags;             // [0] an entry out of block order, [1] (vdiag) a diagonal
 };
 
-template <int G>
-__device__ __forceinline__ void group_sync() {
-    if constexpr (G == 256)
-        __syncthreads();
-    else
-        __builtin_amdgcn_wave_barrier();  // the group's lanes are in one wave
-}
-
-__device__ __forceinline__ int block_of(int c, const SortedSplit& a) {
+__device__ __forceinline__ int block_of(int c, const FlatSplit& a) {
     const int b = div_by(c < 0 ? 0 : c, a.rows_per_block, a.inv_rows);
     return b < a.nb ? b : a.nb - 1;  // in bounds whatever the column
 }
 
-// Entries of one step: lane l of the group takes entries j0 + u*G + l,
-// u < kSortedU (coalesced across the group), the next step's loaded before
-// the current one is placed.
-constexpr int kSortedU = 8;
+// Bit rp[r] for every non-empty row r, the non-empty flags; the row's
+// length as every block's start (blocks past its last entry), and as the
+// virtual entry's position (a row whose columns are all < i).
+__global__ __launch_bounds__(256) void flat_marks_kernel(FlatSplit a, uint32_t* __restrict__ bits32,
+                                                         int32_t* __restrict__ nonempty) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= a.n) return;
+    const int s = a.rp[r], e = a.rp[r + 1];
+    nonempty[r] = e > s ? 1 : 0;
+    if (e > s && s >= 0 && s < a.nnz) atomicOr(&bits32[s >> 5], 1u << (s & 31));
+    for (int b = 0; b < a.nb; ++b) a.starts[static_cast<int64_t>(b) * a.n + r] = e - s;
+    if (a.vdiag) a.ins[r] = e - s;
+}
 
-struct SortedStep {
-    int c[kSortedU];
-    int pc[kSortedU];  // the previous entries, loaded where no shuffle reaches them
-    float x[kSortedU];
+__global__ __launch_bounds__(256) void flat_nzrows_kernel(const int32_t* __restrict__ rp, int64_t n,
+                                                          const int32_t* __restrict__ nzrank,
+                                                          int32_t* __restrict__ nz_rows) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r < n && rp[r + 1] > rp[r]) nz_rows[nzrank[r]] = static_cast<int32_t>(r);
+}
+
+__global__ __launch_bounds__(256) void flat_popc_kernel(const uint64_t* __restrict__ bits,
+                                                        int64_t slices, int32_t* __restrict__ popc) {
+    const int64_t w = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (w < slices) popc[w] = __popcll(bits[w]);
+}
+
+// Each wave takes kFlatSU consecutive 64-entry slices (lane l: entry l of
+// each), with every slice's loads issued before the dependent ones: an
+// entry's row is a chain of loads (bitmap and slice rank, then the
+// non-empty row, then its row pointer), and one slice per wave left that
+// chain's latency exposed (config-E count and scatter passes 0.45 ms each).
+constexpr int kFlatSU = 8;
+
+struct FlatRows {
+    int c[kFlatSU];     // the entries' columns
+    int row[kFlatSU];   // their rows (valid entries)
+    int pos[kFlatSU];   // their positions in the row
+    bool first[kFlatSU];  // an entry that starts its row
+    bool valid[kFlatSU];
 };
 
-// W: the shuffle width (the group, or one wave of a workgroup-wide group);
-// the first lane of each W-lane span loads its entries' predecessors.
-template <int G, bool VALUES, bool PREV>
-__device__ __forceinline__ void load_step(const SortedSplit& a, int s, int len, int j0, int lane,
-                                          SortedStep& t) {
-    constexpr int W = G < 64 ? G : 64;
+// The wave's slices w0 .. w0 + kFlatSU - 1 (w0 < slices): columns, rows and
+// positions; an entry whose rank finds no row sets flags[0].
+__device__ __forceinline__ void flat_rows(const FlatSplit& a, int64_t w0, int lane, FlatRows& f) {
+    const int64_t slices = (a.nnz + 63) >> 6;
+    const uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+    uint64_t word[kFlatSU];
+    int srank[kFlatSU];
 #pragma unroll
-    for (int u = 0; u < kSortedU; ++u) {
-        const int j = j0 + u * G + lane;
-        t.c[u] = j < len ? a.ci[s + j] : 0;
-        if (VALUES) t.x[u] = j < len ? a.v[s + j] : 0.0f;
-        if (PREV) t.pc[u] = (lane % W == 0 && j > 0 && j <= len) ? a.ci[s + j - 1] : -1;
+    for (int u = 0; u < kFlatSU; ++u) {
+        const int64_t w = w0 + u;
+        const int64_t k = w * 64 + lane;
+        f.valid[u] = k < a.nnz;
+        f.c[u] = f.valid[u] ? a.ci[k] : 0;
+        word[u] = w < slices ? a.bits[w] : 0ull;
+        srank[u] = w < slices ? a.slice_rank[w] : 0;
     }
+    int rank[kFlatSU];
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) {
+        rank[u] = srank[u] + __popcll(word[u] & upto);
+        f.first[u] = (word[u] >> lane) & 1;
+        if (f.valid[u] && rank[u] < 1) {
+            atomicOr(&a.flags[0], 1);
+            f.valid[u] = false;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) f.row[u] = f.valid[u] ? a.nz_rows[rank[u] - 1] : 0;
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u)
+        f.pos[u] = static_cast<int>((w0 + u) * 64 + lane - a.rp[f.row[u]]);
 }
 
-template <int G, bool SCATTER>
-__device__ __forceinline__ void split_sorted_row(const SortedSplit& a, int64_t row, int lane,
-                                                 int32_t* slot, int32_t* misc) {
-    constexpr int W = G < 64 ? G : 64;
-    constexpr int STEP = G * kSortedU;
-    const int64_t n = a.n;
-    const int nb = a.nb;
-    const int s = a.rp[row], e = a.rp[row + 1], len = e - s;
-    const int i = static_cast<int>(row);
-    if constexpr (!SCATTER) {
-        for (int b = lane; b < nb; b += G) slot[b] = len;
+__global__ __launch_bounds__(256) void flat_count_kernel(FlatSplit a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t w0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kFlatSU;
+    if (w0 * 64 >= a.nnz) return;  // uniform per wave
+    FlatRows f;
+    flat_rows(a, w0, lane, f);
+    // each entry's predecessor: the lane below, or the previous slice's last
+    // lane, or (the wave's first entry) a load
+    const int pc0 = (lane == 0 && w0 > 0) ? a.ci[w0 * 64 - 1] : 0;
+    int blk[kFlatSU], last[kFlatSU], lastb[kFlatSU];
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) {
+        blk[u] = block_of(f.c[u], a);
+        last[u] = __shfl(f.c[u], 63, 64);
+        lastb[u] = __shfl(blk[u], 63, 64);
+    }
+    const int pb0 = block_of(pc0, a);
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) {
+        int pc = __shfl_up(f.c[u], 1, 64);
+        int pbk = __shfl_up(blk[u], 1, 64);
         if (lane == 0) {
-            misc[0] = len;  // the virtual entry's position: before the first column > i
-            misc[1] = 0;
+            pc = u == 0 ? pc0 : last[u > 0 ? u - 1 : 0];
+            pbk = u == 0 ? pb0 : lastb[u > 0 ? u - 1 : 0];
         }
-        group_sync<G>();
-        int bad = 0;
-        SortedStep cur, nxt;
-        load_step<G, false, true>(a, s, len, 0, lane, cur);
-        for (int j0 = 0; j0 < len; j0 += STEP) {
-            if (j0 + STEP < len) load_step<G, false, true>(a, s, len, j0 + STEP, lane, nxt);
-#pragma unroll
-            for (int u = 0; u < kSortedU; ++u) {
-                const int j = j0 + u * G + lane;
-                // the previous entry: the lane below's, or the loaded one
-                const int up = __shfl_up(cur.c[u], 1, W);
-                const int pc = lane % W != 0 ? up : cur.pc[u];
-                if (j < len) {
-                    const int c = cur.c[u];
-                    const int cb = block_of(c, a);
-                    const int pb = j > 0 ? block_of(pc, a) : -1;
-                    bad |= (j > 0 && pc > c) ? 1 : 0;
-                    if (a.vdiag) {
-                        bad |= c == i ? 2 : 0;
-                        if ((j == 0 || pc < i) && c > i) misc[0] = j;
-                    }
-                    for (int b = pb + 1; b <= cb; ++b) slot[b] = j;
-                }
-            }
-            cur = nxt;
+        if (!f.valid[u]) continue;
+        const int c = f.c[u], row = f.row[u], pos = f.pos[u];
+        const int b = blk[u];
+        const int pb = f.first[u] ? -1 : pbk;
+        if (pb > b) atomicOr(&a.flags[0], 1);
+        for (int x = pb + 1; x <= b; ++x) a.starts[static_cast<int64_t>(x) * a.n + row] = pos;
+        if (a.vdiag) {
+            if (c == row) atomicOr(&a.flags[1], 1);
+            if ((f.first[u] || pc < row) && c > row) a.ins[row] = pos;
         }
-        if (bad) atomicOr(&misc[1], bad);
-        group_sync<G>();
-        const int flag = misc[1];
-        const int d = a.vdiag ? block_of(i, a) : nb;  // the virtual entry's block
-        if (lane == 0 && (flag & 1)) atomicOr(&a.flags[0], 1);
-        if (lane == 0 && (flag & 2)) atomicOr(&a.flags[1], 1);
-        for (int b = lane; b < nb; b += G) {
-            const int st = slot[b] + (b > d ? 1 : 0);
-            const int nx = (b + 1 < nb ? slot[b + 1] : len) + (b + 1 > d ? 1 : 0);
-            const int64_t o = static_cast<int64_t>(b) * n + row;
-            a.cnt[o] = flag ? (b == 0 ? len + a.vdiag : 0) : nx - st;
-            a.starts[o] = flag ? 0 : st;
-        }
-        if (a.vdiag && lane == 0) a.ins[row] = misc[0];
-        group_sync<G>();  // the slots are reused by the group's next row
-    } else {
-        // out position of the entry at (virtual) row position jv in block b:
-        // brp[b*n + row] + jv - starts[b*n + row]
-        for (int b = lane; b < nb; b += G) {
-            const int64_t o = static_cast<int64_t>(b) * n + row;
-            slot[b] = a.brp[o] - a.starts[o];
-        }
-        group_sync<G>();
-        const int R = a.rows_per_block;
-        SortedStep cur, nxt;
-        const bool vals = a.bv != nullptr;
-        if (vals)
-            load_step<G, true, false>(a, s, len, 0, lane, cur);
-        else
-            load_step<G, false, false>(a, s, len, 0, lane, cur);
-        for (int j0 = 0; j0 < len; j0 += STEP) {
-            if (j0 + STEP < len) {
-                if (vals)
-                    load_step<G, true, false>(a, s, len, j0 + STEP, lane, nxt);
-                else
-                    load_step<G, false, false>(a, s, len, j0 + STEP, lane, nxt);
-            }
-#pragma unroll
-            for (int u = 0; u < kSortedU; ++u) {
-                const int j = j0 + u * G + lane;
-                if (j >= len) continue;
-                const int c = cur.c[u];
-                const int cb = block_of(c, a);
-                const int out = slot[cb] + j + (a.vdiag && c > i ? 1 : 0);
-                if (a.bci16)
-                    a.bci16[out] = static_cast<uint16_t>(c - cb * R);
-                else
-                    a.bci[out] = c;
-                if (vals) a.bv[out] = cur.x[u];
-            }
-            cur = nxt;
-        }
-        if (a.vdiag && lane == 0) {
-            const int d = block_of(i, a);
-            const int out = slot[d] + a.ins[row];
-            if (a.bci16)
-                a.bci16[out] = static_cast<uint16_t>(i - d * R);
-            else
-                a.bci[out] = i;
-        }
-        group_sync<G>();
     }
 }
 
-// Rows by length class: G = 16 lanes for rows of at most kShortSplit
-// entries, a wave (G = 64) up to kLongSplit, so no row takes more than eight
-// steps of its group (config-E count + scatter: 0.75 ms with 16-lane groups
-// and 4 entries per lane up to kLongSplit, 0.65 ms so); longer rows:
-// split_sorted_long_kernel.
-template <int G, bool SCATTER>
-__global__ __launch_bounds__(256) void split_sorted_kernel(SortedSplit a) {
-    constexpr int NG = 256 / G;
-    __shared__ int32_t slots[NG][kMaxBlocks];
-    __shared__ int32_t misc[NG][2];
-    if (SCATTER && (a.flags[0] | a.flags[1])) return;  // the general split runs instead
-    const int grp = threadIdx.x / G;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * NG + grp;
-    if (row >= a.n) return;
-    const int len = a.rp[row + 1] - a.rp[row];
-    if (G == 16 ? len > kShortSplit : (len <= kShortSplit || len > kLongSplit)) return;
-    split_sorted_row<G, SCATTER>(a, row, threadIdx.x % G, slots[grp], misc[grp]);
+// Per (block, row): the count (the virtual entry in its block), or, after
+// a flagged count pass, the row's whole length in block 0.
+__global__ __launch_bounds__(256) void flat_counts_kernel(FlatSplit a, int32_t* __restrict__ cnt) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= a.n * a.nb) return;
+    const int b = static_cast<int>(t / a.n);
+    const int64_t r = t - static_cast<int64_t>(b) * a.n;
+    const int len = a.rp[r + 1] - a.rp[r];
+    if (a.flags[0] | a.flags[1]) {
+        cnt[t] = b == 0 ? len + a.vdiag : 0;
+        return;
+    }
+    const int st = a.starts[t];
+    const int nx = b + 1 < a.nb ? a.starts[t + a.n] : len;
+    const int d = a.vdiag ? block_of(static_cast<int>(r), a) : -1;
+    cnt[t] = nx - st + (b == d ? 1 : 0);
 }
 
-// The listed longer rows: one workgroup each, grid-stride over the list.
-template <bool SCATTER>
-__global__ __launch_bounds__(256) void split_sorted_long_kernel(SortedSplit a) {
-    __shared__ int32_t slot[kMaxBlocks];
-    __shared__ int32_t misc[2];
-    if (SCATTER && (a.flags[0] | a.flags[1])) return;
-    const int64_t count = *a.long_count;
-    for (int64_t t = blockIdx.x; t < count; t += gridDim.x)
-        split_sorted_row<256, SCATTER>(a, a.long_list[t], static_cast<int>(threadIdx.x), slot,
-                                       misc);
+// obase = brp - start - rp[row] (in place of the counts, which the scan has
+// consumed): entry k of the block's run goes to obase + k (+1 past the
+// virtual entry in its block).
+__global__ __launch_bounds__(256) void flat_bases_kernel(FlatSplit a, const int32_t* __restrict__ brp,
+                                                         int32_t* __restrict__ obase) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= a.n * a.nb) return;
+    const int b = static_cast<int>(t / a.n);
+    const int64_t r = t - static_cast<int64_t>(b) * a.n;
+    obase[t] = brp[t] - a.starts[t] - a.rp[r];
 }
 
-__global__ __launch_bounds__(256) void split_long_rows_kernel(const int32_t* __restrict__ rp,
-                                                              int64_t n,
-                                                              int32_t* __restrict__ list,
-                                                              int32_t* __restrict__ count) {
+__global__ __launch_bounds__(256) void flat_scatter_kernel(FlatSplit a) {
+    if (a.flags[0] | a.flags[1]) return;  // the caller runs another split
+    const int lane = threadIdx.x & 63;
+    const int64_t w0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kFlatSU;
+    if (w0 * 64 >= a.nnz) return;
+    FlatRows f;
+    flat_rows(a, w0, lane, f);
+    float x[kFlatSU];
+    int out[kFlatSU], b[kFlatSU];
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) {
+        const int64_t k = (w0 + u) * 64 + lane;
+        x[u] = (a.bv && f.valid[u]) ? a.v[k] : 0.0f;
+        b[u] = block_of(f.c[u], a);
+        out[u] = f.valid[u] ? a.obase[static_cast<int64_t>(b[u]) * a.n + f.row[u]] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kFlatSU; ++u) {
+        if (!f.valid[u]) continue;
+        const int c = f.c[u], row = f.row[u];
+        int o = out[u] + static_cast<int>((w0 + u) * 64 + lane);
+        if (a.vdiag && c > row && b[u] == block_of(row, a)) ++o;
+        if (a.bci16)
+            a.bci16[o] = static_cast<uint16_t>(c - b[u] * a.rows_per_block);
+        else
+            a.bci[o] = c;
+        if (a.bv) a.bv[o] = x[u];
+    }
+}
+
+// vdiag: each row's virtual entry.
+__global__ __launch_bounds__(256) void flat_diag_kernel(FlatSplit a, const int32_t* __restrict__ brp) {
+    if (a.flags[0] | a.flags[1]) return;
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (r < n && rp[r + 1] - rp[r] > kLongSplit) list[atomicAdd(count, 1)] = static_cast<int32_t>(r);
+    if (r >= a.n) return;
+    const int i = static_cast<int>(r);
+    const int d = block_of(i, a);
+    const int64_t t = static_cast<int64_t>(d) * a.n + r;
+    const int out = brp[t] + a.ins[r] - a.starts[t];
+    if (a.bci16)
+        a.bci16[out] = static_cast<uint16_t>(i - d * a.rows_per_block);
+    else
+        a.bci[out] = i;
 }
 
 }  // namespace
@@ -418,30 +427,37 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_
 
 namespace {
 
-// The split's temporaries: counts, the scan's temp, flags ([0] a row out of
-// order, [1] a diagonal (vdiag), [2] the general split's disorder, [3] the
-// long-row count), the sorted split's starts, virtual positions and
-// long-row list.
+// The split's temporaries: counts (then the flat split's output bases),
+// the scans' temp, flags ([0] out of block order, [1] a diagonal (vdiag),
+// [2] the general split's disorder), and the flat split's row-start bitmap,
+// slice ranks, non-empty rows, run starts and virtual-entry positions.
 struct SplitTemps {
-    int32_t *cnt, *flags, *starts, *ins, *long_list;
+    int32_t *cnt, *flags, *starts, *ins, *nonempty, *nzrank, *nz_rows, *popc, *slice_rank;
+    uint64_t* bits;
     int64_t* scan_tmp;
 };
 
-SplitTemps carve_split(Carver& c, int64_t n, int64_t nb) {
+SplitTemps carve_split(Carver& c, int64_t n, int64_t nnz_src, int64_t nb) {
+    const int64_t slices = ceil_div(std::max<int64_t>(nnz_src, 1), 64);
     SplitTemps t;
+    t.bits = c.take<uint64_t>(slices);
     t.cnt = c.take<int32_t>(nb * n);
-    t.scan_tmp = c.take<int64_t>(scan_temp_elems(nb * n));
+    t.scan_tmp = c.take<int64_t>(scan_temp_elems(std::max(nb * n, slices)));
     t.flags = c.take<int32_t>(4);
     t.starts = c.take<int32_t>(nb * n);
     t.ins = c.take<int32_t>(n);
-    t.long_list = c.take<int32_t>(n);
+    t.nonempty = c.take<int32_t>(n);
+    t.nzrank = c.take<int32_t>(n + 1);
+    t.nz_rows = c.take<int32_t>(n);
+    t.popc = c.take<int32_t>(slices);
+    t.slice_rank = c.take<int32_t>(slices + 1);
     return t;
 }
 
 // Shapes the blocked copy for n rows and nnz entries and returns its
 // temporaries.
-SplitTemps setup_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
-                         bool weighted, int64_t rows_per_block) {
+SplitTemps setup_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, int64_t nnz_src,
+                         const int32_t* rp, bool weighted, int64_t rows_per_block) {
     require(n > 0 && rows_per_block > 0, "blocked CSR: empty structure or block");
     require(nnz >= 0 && nnz < (int64_t(1) << 31), "blocked CSR: nnz must be < 2^31");
     const int64_t nb = ceil_div(n, rows_per_block);
@@ -460,7 +476,7 @@ SplitTemps setup_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* 
                    (bk.idx16 ? sizeof(uint16_t) : sizeof(int32_t)));
     if (weighted) bk.bv.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
     Carver cv(nullptr, 0);
-    carve_split(cv, n, nb);
+    carve_split(cv, n, nnz_src, nb);
     bk.scratch.reserve(cv.bytes());
     Carver c(bk.scratch.get(), bk.scratch.size());
     // host results: the plans' totals (4 per block), then the flags
@@ -468,7 +484,7 @@ SplitTemps setup_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* 
     bk.plans.resize(static_cast<size_t>(nb));
     for (auto& p : bk.plans)
         if (!p) p = std::make_unique<tg_spmm_plan_s>();
-    return carve_split(c, n, nb);
+    return carve_split(c, n, nnz_src, nb);
 }
 
 // One plan per block, all built by one launch per step and one
@@ -483,55 +499,65 @@ void build_block_plans(BlockedCSR& bk, int64_t max_f, int64_t chunk, hipStream_t
                       bk.host.as<int64_t>(), s);
 }
 
-// The sorted-row split (with or without the virtual diagonal); false when
-// some row is out of order or, with vdiag, has a diagonal (the copy is then
-// incomplete and the caller takes another path).
-bool split_sorted(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const int32_t* ci,
-                  const float* v, int64_t nnz_src, bool vdiag, int64_t max_f, int64_t chunk,
-                  hipStream_t s) {
+// The flat split (with or without the virtual diagonal); false when some
+// row is out of block order or, with vdiag, has a diagonal (the copy is
+// then incomplete and the caller takes another path).
+bool split_flat(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const int32_t* ci,
+                const float* v, int64_t nnz_src, bool vdiag, int64_t max_f, int64_t chunk,
+                hipStream_t s) {
     const int64_t n = bk.n, nb = bk.n_blocks;
+    const int64_t slices = ceil_div(std::max<int64_t>(nnz_src, 1), 64);
+    auto grid = [](int64_t x) { return static_cast<unsigned>(ceil_div(std::max<int64_t>(x, 1), 256)); };
     fill_i32(t.flags, 4, 0, s);
-    split_long_rows_kernel<<<static_cast<unsigned>(ceil_div(n, 256)), 256, 0, s>>>(
-        rp, n, t.long_list, t.flags + 3);
-    TG_LAUNCH_CHECK();
-    SortedSplit a{};
+    fill_i32(reinterpret_cast<int32_t*>(t.bits), 2 * slices, 0, s);
+    FlatSplit a{};
     a.rp = rp;
     a.ci = ci;
     a.v = v;
     a.n = n;
+    a.nnz = nnz_src;
     a.rows_per_block = static_cast<int>(bk.rows_per_block);
     a.inv_rows = 1.0 / static_cast<double>(bk.rows_per_block);
     a.nb = static_cast<int>(nb);
     a.vdiag = vdiag ? 1 : 0;
-    a.long_list = t.long_list;
-    a.long_count = t.flags + 3;
-    a.cnt = t.cnt;
+    a.bits = t.bits;
+    a.slice_rank = t.slice_rank;
+    a.nz_rows = t.nz_rows;
     a.starts = t.starts;
     a.ins = t.ins;
     a.flags = t.flags;
-    // grid-stride over at most nnz / (kLongSplit + 1) long rows
-    const unsigned long_grid =
-        static_cast<unsigned>(std::min<int64_t>(nnz_src / (kLongSplit + 1) + 1, 1024));
-    const unsigned grid16 = static_cast<unsigned>(ceil_div(n, 16));
-    const unsigned grid64 = static_cast<unsigned>(ceil_div(n, 4));
-    split_sorted_kernel<16, false><<<grid16, 256, 0, s>>>(a);
+    flat_marks_kernel<<<grid(n), 256, 0, s>>>(a, reinterpret_cast<uint32_t*>(t.bits), t.nonempty);
     TG_LAUNCH_CHECK();
-    split_sorted_kernel<64, false><<<grid64, 256, 0, s>>>(a);
+    exclusive_scan_i32(t.nonempty, t.nzrank, n, t.scan_tmp, s);
+    flat_nzrows_kernel<<<grid(n), 256, 0, s>>>(rp, n, t.nzrank, t.nz_rows);
     TG_LAUNCH_CHECK();
-    split_sorted_long_kernel<false><<<long_grid, 256, 0, s>>>(a);
+    flat_popc_kernel<<<grid(slices), 256, 0, s>>>(t.bits, slices, t.popc);
+    TG_LAUNCH_CHECK();
+    exclusive_scan_i32(t.popc, t.slice_rank, slices, t.scan_tmp, s);
+    // waves of kFlatSU slices, four per workgroup
+    const unsigned egrid = static_cast<unsigned>(ceil_div(slices, 4 * kFlatSU));
+    if (nnz_src > 0) {
+        flat_count_kernel<<<egrid, 256, 0, s>>>(a);
+        TG_LAUNCH_CHECK();
+    }
+    flat_counts_kernel<<<grid(n * nb), 256, 0, s>>>(a, t.cnt);
     TG_LAUNCH_CHECK();
     int32_t* brp = bk.brp.as<int32_t>();
     exclusive_scan_i32(t.cnt, brp, nb * n, t.scan_tmp, s);
-    a.brp = brp;
+    flat_bases_kernel<<<grid(n * nb), 256, 0, s>>>(a, brp, t.cnt);
+    TG_LAUNCH_CHECK();
+    a.obase = t.cnt;
     a.bci = bk.idx16 ? nullptr : bk.bci.as<int32_t>();
     a.bci16 = bk.idx16 ? bk.bci.as<uint16_t>() : nullptr;
     a.bv = v ? bk.bv.as<float>() : nullptr;
-    split_sorted_kernel<16, true><<<grid16, 256, 0, s>>>(a);
-    TG_LAUNCH_CHECK();
-    split_sorted_kernel<64, true><<<grid64, 256, 0, s>>>(a);
-    TG_LAUNCH_CHECK();
-    split_sorted_long_kernel<true><<<long_grid, 256, 0, s>>>(a);
-    TG_LAUNCH_CHECK();
+    if (nnz_src > 0) {
+        flat_scatter_kernel<<<egrid, 256, 0, s>>>(a);
+        TG_LAUNCH_CHECK();
+    }
+    if (vdiag) {
+        flat_diag_kernel<<<grid(n), 256, 0, s>>>(a, brp);
+        TG_LAUNCH_CHECK();
+    }
     int32_t* hf = reinterpret_cast<int32_t*>(bk.host.as<int64_t>() + 4 * nb);
     TG_HIP(hipMemcpyAsync(hf, t.flags, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, s));
     build_block_plans(bk, max_f, chunk, s);
@@ -571,10 +597,14 @@ void split_general(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const
 void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    const int32_t* ci, const float* v, int64_t rows_per_block, int64_t max_f,
                    hipStream_t s, int64_t chunk) {
-    const SplitTemps t = setup_blocked(bk, n, nnz, rp, v != nullptr, rows_per_block);
+    const SplitTemps t = setup_blocked(bk, n, nnz, nnz, rp, v != nullptr, rows_per_block);
     require(nnz == 0 || ci != nullptr, "blocked CSR: null structure");
-    // (the sorted-row split is no faster here: config-E count + scatter
-    // 0.65 ms against 0.63 ms; it serves the virtual diagonal below)
+    // rows in block order (sorted rows) take the flat split; the general
+    // one runs when some row is not
+    if (split_flat(bk, t, rp, ci, v, nnz, false, max_f, chunk, s)) {
+        bk.in_order = true;
+        return;
+    }
     split_general(bk, t, rp, ci, v, max_f, chunk, s);
 }
 
@@ -582,9 +612,9 @@ bool build_blocked_self_loops(BlockedCSR& bk, int64_t n, int64_t nnz, const int3
                               const int32_t* ci, int64_t rows_per_block, int64_t max_f,
                               hipStream_t s, int64_t chunk) {
     require(nnz + n < (int64_t(1) << 31), "blocked CSR: nnz + n must be < 2^31");
-    const SplitTemps t = setup_blocked(bk, n, nnz + n, rp, false, rows_per_block);
+    const SplitTemps t = setup_blocked(bk, n, nnz + n, nnz, rp, false, rows_per_block);
     require(nnz == 0 || ci != nullptr, "blocked CSR: null structure");
-    if (!split_sorted(bk, t, rp, ci, nullptr, nnz, true, max_f, chunk, s)) return false;
+    if (!split_flat(bk, t, rp, ci, nullptr, nnz, true, max_f, chunk, s)) return false;
     bk.in_order = true;
     return true;
 }
