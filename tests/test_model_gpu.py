@@ -189,9 +189,9 @@ def test_zero_weights_default(gpu):
 
 
 @pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
-                                  "sage_concat", "sage_transform_first", "sage_split_rows",
-                                  "gat", "gat_split_rows", "gat_negative_slope",
-                                  "gat_wide_heads"])
+                                  "gcn_wide_tail", "sage_concat", "sage_transform_first",
+                                  "sage_split_rows", "sage_wide_tail", "gat", "gat_split_rows",
+                                  "gat_negative_slope", "gat_wide_heads"])
 def test_blocked_aggregation(gpu, restate, case):
     """Column-blocked GCN / SAGE-mean / GAT aggregation (forced on small
     graphs with few rows per block): against the oracle at the
@@ -201,7 +201,8 @@ def test_blocked_aggregation(gpu, restate, case):
     32-column ones), a narrow last layer, three 32-column GAT heads (kept in
     32-column groups), two 64-column heads (one weight plane per 64-column
     group), empty rows, unsorted rows and rows of more than one plan chunk
-    inside a block."""
+    inside a block.  Last tiles of 12, 7 and 10 valid columns, and of 28,
+    25 (the wide_tail cases)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(31)
     split = case.endswith("split_rows")
@@ -215,7 +216,7 @@ def test_blocked_aggregation(gpu, restate, case):
         # positive edge weights: signed ones put row degrees near 0, whose
         # 1/sqrt(deg) blows up the normalised weights and the cancellation
         a.val[:] = np.abs(a.val) + 0.01
-        spec = synth.spec_gcn(48, 300, 7)
+        spec = synth.spec_gcn(48, 60, 25) if case == "gcn_wide_tail" else synth.spec_gcn(48, 300, 7)
     elif case == "gat_wide_heads":  # heads of 64 columns: one weight plane per 64-column group
         spec = synth.spec_gat(48, 64, 2, 7)
     elif case.startswith("gat"):
@@ -223,6 +224,8 @@ def test_blocked_aggregation(gpu, restate, case):
         if case == "gat_negative_slope":  # LeakyReLU not monotone: per-entry score maxima
             for layer in spec:
                 layer["slope"] = -0.3
+    elif case == "sage_wide_tail":
+        spec = synth.spec_sage(96, 60, 25)
     else:
         spec = synth.spec_sage(96, 300, 10)
     w = synth.model_weights(spec, seed=3)

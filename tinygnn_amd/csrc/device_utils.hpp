@@ -105,6 +105,42 @@ __device__ __forceinline__ float group_bcast(float v) {
     return __int_as_float(group_bcast<LPR, SRC>(__float_as_int(v)));
 }
 
+// The value of the partner lane that differs in lane bit K (K = 8, 4, 2, 1)
+// within a 16-lane row, and in no higher bit: row_mirror (lane i <-> 15 - i)
+// for 8, row_half_mirror (i <-> 7 - i within each eight) for 4, quad_perm
+// [2,3,0,1] and [1,0,3,2] for 2 and 1.  The partner must be active.
+template <int K>
+__device__ __forceinline__ float dpp_flip(float v) {
+    static_assert(K == 8 || K == 4 || K == 2 || K == 1, "partner bit");
+    constexpr int ctrl = K == 8 ? 0x140 : K == 4 ? 0x141 : K == 2 ? 0x4E : 0xB1;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
+}
+
+template <int K, int N>
+__device__ __forceinline__ void transpose_sum_step(float* x, int lane) {
+    // x[0, N) -> x[0, N / 2): the half that lane bit K selects, plus the
+    // partner's copy of it (the partner keeps the other half)
+    const bool hi = (lane & K) != 0;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        const float a = x[i], b = x[i + N / 2];
+        const float send = hi ? a : b;
+        const float keep = hi ? b : a;
+        x[i] = keep + dpp_flip<K>(send);
+    }
+    if constexpr (K > 1) transpose_sum_step<K / 2, N / 2>(x, lane);
+}
+
+// Sums x[u] over the LPR lanes of a group (LPR 8 or 16, groups aligned to
+// LPR lanes, all active): on return x[j], j < N / LPR, of lane l holds the
+// total of entry l * (N / LPR) + j.  log2(LPR) halving steps, N - N / LPR
+// adds per lane, no LDS; each total is one fixed tree of adds.
+template <int LPR, int N>
+__device__ __forceinline__ void group_transpose_sum(float (&x)[N], int lane) {
+    static_assert((LPR == 8 || LPR == 16) && N % LPR == 0, "group shape");
+    transpose_sum_step<LPR / 2, N>(x, lane);
+}
+
 // Non-temporal (streaming) loads for data read exactly once.
 template <typename T>
 __device__ __forceinline__ T ld_stream(const T* p) {

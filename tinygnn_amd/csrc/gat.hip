@@ -736,6 +736,10 @@ __global__ __launch_bounds__(256) void gat_stats_merge_kernel(const int4* __rest
 struct GatPass {
     const float* src;  // [n x heads] a_l . Wh_i
     const float* dst;  // [n x heads] a_r . Wh_j
+    // [heads x head_cols] a_r: the passes that hold a whole head per lane
+    // group compute a_r . Wh_j from the gathered row instead of gathering dst
+    const float* att_r;
+    int tail_mask;     // those passes: the head's width is not a multiple of 4
     float* m_state;    // [n x G] running max per row and column group
     float* s_state;    // [n x G] running sum
     float* pstats;     // [partial slots x G x 2] (m, s) of split rows' chunks
@@ -789,7 +793,7 @@ __device__ __forceinline__ void out_store(float* row, int64_t fo, int64_t f, boo
     }
 }
 
-template <int LPR>
+template <int LPR, bool DIN>
 __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
     const uint16_t* __restrict__ ci16, const float* __restrict__ B, int64_t ldb,
@@ -818,6 +822,18 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     const bool ok = fo < f;
     const int64_t fl = ok ? fo : fbase;  // lanes past f gather the tile's first vector
     float* crow = C + static_cast<int64_t>(ch.x) * ldc;
+    // DIN (the group's columns are one whole head): a_r at the lane's
+    // columns, 0 past the head; nv of the lane's four gathered floats are
+    // Wh columns (the rest may be row padding, masked when tail_mask)
+    float ar[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int nv = 0;
+    if constexpr (DIN) {
+        const int64_t hc = fo - static_cast<int64_t>(h) * P.head_cols;  // column in the head
+        nv = ok ? static_cast<int>(P.head_cols - hc < 4 ? P.head_cols - hc : 4) : 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            ar[k] = k < nv ? P.att_r[static_cast<int64_t>(h) * P.head_cols + hc + k] : 0.0f;
+    }
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, s = 0.0f;  // s: this lane's share of the running sum
@@ -846,7 +862,8 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             cl[j] = ncl[j];
-            d[j] = dh[static_cast<int64_t>(cl[j]) * stride];  // before the row gathers
+            // before the row gathers (DIN: from them, below)
+            if constexpr (!DIN) d[j] = dh[static_cast<int64_t>(cl[j]) * stride];
         }
         const int cnt = e - base < BE ? e - base : BE;
         float bv[U][4];
@@ -859,6 +876,28 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
             ldv<4>(reinterpret_cast<const float*>(bl + off), bv[u]);
         });
         fetch(base + BE);
+        if constexpr (DIN) {
+            // a_r . Wh_j of the batch's entries: the lane's four-column
+            // share of each, summed over the group, entry l * CPL + j's
+            // total landing in lane l (group_transpose_sum)
+            float pd[U];
+            static_for<0, U>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                float b1 = bv[u][1], b2 = bv[u][2], b3 = bv[u][3];
+                if (P.tail_mask) {  // uniform
+                    b1 = nv > 1 ? b1 : 0.0f;
+                    b2 = nv > 2 ? b2 : 0.0f;
+                    b3 = nv > 3 ? b3 : 0.0f;
+                }
+                float t = ar[0] * bv[u][0];
+                t = __builtin_fmaf(ar[1], b1, t);
+                t = __builtin_fmaf(ar[2], b2, t);
+                pd[u] = __builtin_fmaf(ar[3], b3, t);
+            });
+            group_transpose_sum<LPR>(pd, l);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) d[j] = pd[j];
+        }
         // the batch's scores, the group's maximum, the rescaled carry
         float ev[CPL];
         float bm = -INFINITY;
@@ -986,7 +1025,7 @@ __global__ __launch_bounds__(256) void gat_online_reduce_kernel(
     }
 }
 
-template <int LPR>
+template <int LPR, bool DIN>
 void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t ldwh,
                        float* out, int64_t ldo, const GatPass& base, int64_t max_partials,
                        hipStream_t s) {
@@ -1005,7 +1044,7 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
             GatPass Q = P;
             Q.dst = P.dst + r0 * P.heads;
             dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)), ytiles);
-            gat_online_chunk_kernel<LPR><<<grid, 256, 0, s>>>(
+            gat_online_chunk_kernel<LPR, DIN><<<grid, 256, 0, s>>>(
                 p.chunks.as<int4>(), p.n_chunks, bk.idx16 ? nullptr : bk.bci.as<int32_t>(),
                 bk.idx16 ? bk.bci.as<uint16_t>() : nullptr, wh + r0 * ldwh, ldwh, out, ldo,
                 p.partials.as<float>(), ldp, f, Q);
@@ -1136,7 +1175,7 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
                            float* rmax, float* rinv, void* work, size_t work_bytes,
-                           hipStream_t s, bool exact) {
+                           hipStream_t s, bool exact, const float* ar) {
     require(bk.n == n && (plan == nullptr || plan->m == n),
             "GATLayer: blocked structure or plan rows differ from n");
     require(gat_blocked_ok(heads, f, 1), "GATLayer: layout not supported blocked");
@@ -1157,6 +1196,8 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int
         GatPass P{};
         P.src = src;
         P.dst = dst;
+        P.att_r = ar;
+        P.tail_mask = f % 4 != 0 ? 1 : 0;
         P.m_state = rmax;
         P.s_state = rinv;
         P.pstats = cw.take<float>(std::max<int64_t>(blocked_max_partials(bk), 1) * groups * 2);
@@ -1170,10 +1211,20 @@ void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int
                    (bias == nullptr || reinterpret_cast<uintptr_t>(bias) % 16 == 0);
         // partial slots: the block plans' (work holds gat_workspace_blocked)
         const int64_t maxp = std::max<int64_t>(blocked_max_partials(bk), 1);
-        if (gc == 64)
-            gat_online_passes<16>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
-        else
-            gat_online_passes<8>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+        // a whole head per lane group: a_r . Wh_j from the gathered rows (a
+        // gather of dst per entry cost 2 ms of the config-E GAT forward's 11.8)
+        const bool din = ar != nullptr && (heads == 1 ? f <= gc : f == gc);
+        if (gc == 64) {
+            if (din)
+                gat_online_passes<16, true>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+            else
+                gat_online_passes<16, false>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+        } else {
+            if (din)
+                gat_online_passes<8, true>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+            else
+                gat_online_passes<8, false>(bk, ftot, wh, ldwh, out, ldo, P, maxp, s);
+        }
         return;
     }
     require(plan != nullptr, "GATLayer: the statistics need the unblocked plan");

@@ -82,13 +82,15 @@ void gat_aggregate(const tg_spmm_plan_s& p, int64_t n, int64_t heads, int64_t f,
 // or gat_workspace_blocked(bk, ...) without a plan
 // bytes; exact: the reference's
 // operation order, for a plan that splits no row and a blocked structure in
-// block order).
+// block order; ar: the attention vector a_r [heads x f] behind dst, or null:
+// fast-precision passes whose lane groups hold whole heads then compute
+// a_r . Wh_j from the gathered rows instead of reading dst).
 bool gat_blocked_ok(int64_t heads, int64_t f, int concat);
 void gat_aggregate_blocked(const BlockedCSR& bk, const tg_spmm_plan_s* plan, int64_t n,
                            int64_t heads, int64_t f, const int32_t* ci, const float* wh,
                            int64_t ldwh, const float* src, const float* dst, float slope,
                            const float* bias, int act, int post, float* out, int64_t ldo,
                            float* rmax, float* rinv, void* work, size_t work_bytes,
-                           hipStream_t s, bool exact = false);
+                           hipStream_t s, bool exact = false, const float* ar = nullptr);
 
 }  // namespace tg

@@ -623,7 +623,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
                                       m.sl_ci.as<int32_t>(), wh, ldwh, src, dst, l.slope,
                                       l.bias ? l.b.as<float>() : nullptr, l.act, l.post, y,
                                       l.out_cols(), rmax, rinv, m.work.get(), m.work.size(), s,
-                                      exact);
+                                      exact, l.ar.as<float>());
             } else {
                 gat_aggregate(*m.plan_sl, n, l.heads, l.out, m.sl_ci.as<int32_t>(), wh, ldwh,
                               src, dst, l.slope, l.bias ? l.b.as<float>() : nullptr, l.act,
