@@ -30,8 +30,14 @@ def _plan(da, max_f, chunk=0):
 
 
 @pytest.mark.parametrize("agg", [0, 1])
-@pytest.mark.parametrize("f_in,f_out", [(5, 3), (13, 11), (64, 7), (100, 16), (33, 64)])
+@pytest.mark.parametrize("f_in,f_out", [(5, 3), (13, 11), (64, 7), (100, 16), (33, 64),
+                                        (37, 41), (20, 130)])
 def test_sage_concat_bitexact(gpu, restate, agg, f_in, f_out):
+    """The reference's dataflow, bit for bit: the aggregation in nonzero
+    order, then the in-order dual GEMM (one output per thread up to 32
+    columns; in 64-column slabs beyond, with scalar-tail columns from
+    f_out rounded down to 8 -- 40 of 41, 128 of 130 -- and k not a multiple
+    of the GEMM's k-tile)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(agg * 1000 + f_in * 10 + f_out)
     n = 400

@@ -245,6 +245,125 @@ __global__ __launch_bounds__(256) void gemm_inorder_small_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// In-order GEMM for small products in 64-column slabs (bit-exact; the
+// Cora-scale dual n x 1433 x 64 SAGE transform): a wavefront computes TM
+// rows x 64 columns, one column per lane.  The rows are wave-uniform, so
+// their A values come through scalar loads (s_load_dwordx16, no LDS); the
+// workgroup's four wavefronts share each k-tile of kRKT rows of B through
+// LDS (two buffers, the next tile loaded into registers while the current
+// one is consumed).  Every output is one fma chain over k ascending from
+// 0, never over padded k; DUAL interleaves the pairs per k and applies the
+// reference's scalar tail, as gemm_inorder_kernel.  A tile's A values (TM x
+// kRKT per pair) must fit the scalar registers.  Measured on the dual
+// 2708 x 1433 x 64 product (Cora-synth SAGE forward, 204 us with
+// gemm_inorder_small_kernel): TM 1 / kRKT 32 145 us, kRKT 16 154 us, kRKT
+// 64 200 us (scalar spills), TM 2 169 us, TM 4 255 us; the single product
+// (GAT) is no faster than gemm_inorder_small_kernel and stays there.
+// ---------------------------------------------------------------------------
+template <int TM, int kRKT, bool DUAL>
+__global__ __launch_bounds__(256) void gemm_inorder_rows_kernel(GemmArgs g) {
+    constexpr int NP = DUAL ? 2 : 1;
+    constexpr int LB = kRKT * 64 / 256;  // B values per thread per tile and pair
+    __shared__ float Bs[2][NP][kRKT][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int64_t M = g.m, N = g.n, K = g.k1;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int64_t m0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * TM;
+    const int64_t nt = (K + kRKT - 1) / kRKT;
+    // the wave's rows of A (clamped for the loads; rows >= M are not stored)
+    const float* ar[NP][TM];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int r = 0; r < TM; ++r) {
+            const int64_t row = m0 + r < M ? m0 + r : M - 1;
+            ar[p][r] = p ? g.a2 + row * g.lda2 : g.a1 + row * g.lda1;
+        }
+    const bool tail = DUAL && g.tail_from >= 0 && (n0 + lane) >= g.tail_from;
+
+    float rb[NP][LB];
+    auto fetch = [&](int64_t kt) {
+        const int64_t k0 = kt * kRKT;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float* B = p ? g.b2 : g.b1;
+            const int64_t ldb = p ? g.ldb2 : g.ldb1;
+#pragma unroll
+            for (int t = 0; t < LB; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                const int64_t gk = k0 + e / 64, gn = n0 + e % 64;
+                rb[p][t] = (gk < K && gn < N) ? B[gk * ldb + gn] : 0.0f;
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int t = 0; t < LB; ++t) {
+                const int e = threadIdx.x + 256 * t;
+                Bs[buf][p][e / 64][e % 64] = rb[p][t];
+            }
+    };
+
+    float acc[TM];
+#pragma unroll
+    for (int r = 0; r < TM; ++r) acc[r] = 0.0f;
+    // one k step of every row: plain (tail = false) or the scalar tail form
+    auto step = [&](int cb, int64_t k, int kk, bool tl) {
+        const float b1 = Bs[cb][0][kk][lane];
+        const float b2 = Bs[cb][NP - 1][kk][lane];
+#pragma unroll
+        for (int r = 0; r < TM; ++r) {
+            const float a1 = ar[0][r][k];
+            if constexpr (DUAL) {
+                const float a2 = ar[NP - 1][r][k];
+                acc[r] = tl ? acc[r] + __builtin_fmaf(a1, b1, a2 * b2)
+                            : __builtin_fmaf(a2, b2, __builtin_fmaf(a1, b1, acc[r]));
+            } else {
+                acc[r] = __builtin_fmaf(a1, b1, acc[r]);
+            }
+        }
+    };
+    if (nt > 0) {
+        fetch(0);
+        stage(0);
+    }
+    __syncthreads();
+    for (int64_t kt = 0; kt < nt; ++kt) {
+        const int cb = static_cast<int>(kt & 1);
+        if (kt + 1 < nt) fetch(kt + 1);
+        const int64_t k0 = kt * kRKT;
+        const int kmax = static_cast<int>(K - k0 < kRKT ? K - k0 : kRKT);
+        // the dual form is chosen outside the k loop
+        if (kmax == kRKT) {
+            if (DUAL && tail) {
+#pragma unroll
+                for (int kk = 0; kk < kRKT; ++kk) step(cb, k0 + kk, kk, true);
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < kRKT; ++kk) step(cb, k0 + kk, kk, false);
+            }
+        } else {
+            if (DUAL && tail) {
+                for (int kk = 0; kk < kmax; ++kk) step(cb, k0 + kk, kk, true);
+            } else {
+                for (int kk = 0; kk < kmax; ++kk) step(cb, k0 + kk, kk, false);
+            }
+        }
+        if (kt + 1 < nt) stage(cb ^ 1);
+        __syncthreads();
+    }
+    const int64_t gn = n0 + lane;
+#pragma unroll
+    for (int r = 0; r < TM; ++r) {
+        const int64_t gm = m0 + r;
+        if (gm < M && gn < N) g.c[c_index(g, gm, gn)] = epi_out(g, acc[r], gm, gn);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Wide in-order GEMM (bit-exact, n > 32): 128x128 workgroup tile, an 8x8
 // register micro-tile per thread, BK = 8, two LDS buffers with register
 // prefetch.  Each output is still one fma chain over k ascending from 0 (the
@@ -833,6 +952,13 @@ void launch_inorder_small(const GemmArgs& g, hipStream_t s) {
     TG_LAUNCH_CHECK();
 }
 
+template <int TM, int KT, bool DUAL>
+void launch_inorder_rows(const GemmArgs& g, hipStream_t s) {
+    dim3 grid(static_cast<unsigned>(ceil_div(g.m, 4 * TM)), static_cast<unsigned>(ceil_div(g.n, 64)));
+    gemm_inorder_rows_kernel<TM, KT, DUAL><<<grid, 256, 0, s>>>(g);
+    TG_LAUNCH_CHECK();
+}
+
 template <bool DUAL>
 void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
     // Small products (m n <= 2^21): one output per thread, many workgroups
@@ -842,6 +968,7 @@ void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
         if (g.n <= 8) return launch_inorder_small<8, DUAL>(g, s);
         if (g.n <= 16) return launch_inorder_small<16, DUAL>(g, s);
         if (g.n <= 32) return launch_inorder_small<32, DUAL>(g, s);
+        if constexpr (DUAL) return launch_inorder_rows<1, 32, DUAL>(g, s);
         return launch_inorder_small<64, DUAL>(g, s);
     }
     if (g.n > 32) {
