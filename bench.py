@@ -356,11 +356,15 @@ def _blocked_cost(n, nnz, f, nb, gc, values=False, self_term=False, score_heads=
         8 x 4 n f (with f padded to whole 32-column tiles);
       * the output read and written once per block after the first:
         4 n f (2 nb - 1);
-      * a self term (SAGE) and score arrays (GAT) once: 4 n f, 8 x 4 n heads;
-      * GAT's online softmax state (max, sum) per row and column group, read
-        and written once per block after the first: 8 n g (2 nb - 1).
+      * a self term (SAGE) once: 4 n f;
+      * GAT: the row's source score per column group and pass, 4 n g nb (the
+        destination scores a_r . Wh_j are computed in the pass from the
+        gathered rows), and the online softmax state (max, sum) per row and
+        column group, read and written once per block after the first:
+        8 n g (2 nb - 1).
     The gathers themselves (4 f bytes per entry) are served by L2 and are not
-    counted; they are what the passes spend their time on."""
+    counted here (gather_lines); they are what the passes spend their time
+    on."""
     g = -(-f // gc)
     fpad = -(-f // 32) * 32
     idx = 2 if -(-n // nb) <= 65536 else 4
@@ -369,30 +373,45 @@ def _blocked_cost(n, nnz, f, nb, gc, values=False, self_term=False, score_heads=
     if self_term:
         b += 4 * n * f
     if score_heads:
-        b += 8 * 4 * n * score_heads + 8 * n * g * (2 * nb - 1)
+        b += 4 * n * g * nb + 8 * n * g * (2 * nb - 1)
     return b
 
 
-def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
+def gather_lines(f, gc):
+    """128-byte lines one entry's gather touches in a blocked aggregation of
+    width f in lane groups of gc columns: one per 32-column tile (tile-major,
+    gc = 32); a 64-column group's row-major 256-byte span covers
+    ceil(4 c / 128) lines for its c valid columns."""
+    if gc == 32:
+        return -(-f // 32)
+    return sum(-(-4 * min(gc, f - c0) // 128) for c0 in range(0, f, gc))
+
+
+def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info, l2_gbs=None):
     """T_roof of the config-E cached forward in fast precision, over the
     kernels of the dataflow the library ran (info = Model.blocking_info()):
     sum over kernels of max(bytes / 8 TB/s, flops / 157.3 TFLOP/s), bytes as
     _gemm_cost / _blocked_cost (the reference's SpMM cost model,
-    ops.cpp:186-191, where a pass is unblocked).  Returns (ms, per-kernel
-    list)."""
+    ops.cpp:186-191, where a pass is unblocked).  With l2_gbs (the measured
+    rate of the aggregation kernel gathering L2-resident rows), a second sum
+    adds the blocked passes' gathers as a third bound, gathered lines x 128
+    bytes / l2_gbs.  Returns (ms, ms with the gather bound or None,
+    per-kernel list)."""
     nnz_s = nnz_a + n
     ks = []
 
     def gemm(label, m, k, nn):
         b, fl = _gemm_cost(m, k, nn)
-        ks.append((label, b, fl))
+        ks.append((label, b, fl, 0))
 
     def agg(label, nnz, f, nb, gc, **kw):
         if nb > 0:
-            ks.append((label, _blocked_cost(n, nnz, f, nb, gc, **kw), 2 * nnz * f))
-        else:  # unblocked: the reference's cost model
+            ks.append((label, _blocked_cost(n, nnz, f, nb, gc, **kw), 2 * nnz * f,
+                       128 * nnz * gather_lines(f, gc)))
+        else:  # unblocked: the reference's cost model (gathers from HBM)
             v = 0 if kw.get("values") is False else 4 * nnz
-            ks.append((label, 4 * (n + 1) + 4 * nnz + v + 4 * f * nnz + 4 * f * n, 2 * nnz * f))
+            ks.append((label, 4 * (n + 1) + 4 * nnz + v + 4 * f * nnz + 4 * f * n, 2 * nnz * f,
+                       0))
 
     if name == "gcn":
         nb, gc = info["blocks_sl"], info["cols_sl"]
@@ -414,17 +433,23 @@ def forward_roofline(name, n, nnz_a, f_in, hidden, classes, heads, info):
         nb, gc = info["blocks_sl"], info["cols_sl"]
         for li, (fi, fo, h) in enumerate(((f_in, hidden, heads), (hidden * heads, classes, 1))):
             gemm(f"L{li + 1} transform", n, fi, fo * h)
-            ks.append((f"L{li + 1} scores", 4 * n * fo * h + 8 * n * h, 4 * n * fo * h))
+            ks.append((f"L{li + 1} scores", 4 * n * fo * h + 8 * n * h, 4 * n * fo * h, 0))
             agg(f"L{li + 1} attention aggregation", nnz_s, fo * h, nb, gc, values=False,
                 score_heads=h)
-    out, tot = [], 0.0
-    for label, b, fl in ks:
+    out, tot, tot_l2 = [], 0.0, 0.0
+    for label, b, fl, gb in ks:
         t = max(b / (HBM_PEAK_GBS * 1e6), fl / (MFMA_PEAK_TFS * 1e9))
         tot += t
-        out.append(dict(kernel=label, bytes=int(b), flops=int(fl), t_roof_ms=round(t, 4),
-                        bound="hbm" if b / (HBM_PEAK_GBS * 1e6) >= fl / (MFMA_PEAK_TFS * 1e9)
-                        else "mfma"))
-    return tot, out
+        k = dict(kernel=label, bytes=int(b), flops=int(fl), t_roof_ms=round(t, 4),
+                 bound="hbm" if b / (HBM_PEAK_GBS * 1e6) >= fl / (MFMA_PEAK_TFS * 1e9)
+                 else "mfma")
+        if gb:
+            k["gathered_bytes"] = int(gb)
+            if l2_gbs:
+                k["t_gather_ms"] = round(gb / (l2_gbs * 1e6), 4)
+        tot_l2 += max(t, gb / (l2_gbs * 1e6)) if l2_gbs else t
+        out.append(k)
+    return tot, (tot_l2 if l2_gbs else None), out
 
 
 def run_forward_e(args, torch, tg):
@@ -437,6 +462,8 @@ def run_forward_e(args, torch, tg):
     stream = torch.cuda.current_stream()
     n = synth.E_NODES
     t0 = time.time()
+    l2 = measure_l2_gather(torch, tg)
+    l2_rate = l2["rate_gbs"]
     adj, csr_ms = build_graph_gpu(torch, tg, n, synth.E_EDGES, args.seed + 10, dev)
     rng = np.random.default_rng(args.seed + 11)
     x_h = rng.standard_normal((n, synth.E_FEATURES), dtype=np.float32)
@@ -513,8 +540,9 @@ def run_forward_e(args, torch, tg):
         raw_x = y.cpu().numpy()
         logits_x = tg.log_softmax_(y.clone()).cpu().numpy()
         model.set_precision(tg.PRECISION_FAST)
-        troof, kern = forward_roofline(name, n, adj.nnz, synth.E_FEATURES, 256 if name != "gat"
-                                       else 64, synth.E_CLASSES, 4, blocking)
+        troof, troof_l2, kern = forward_roofline(name, n, adj.nnz, synth.E_FEATURES,
+                                                 256 if name != "gat" else 64, synth.E_CLASSES,
+                                                 4, blocking, l2_rate)
         r = dict(gpu_ms=round(cached, 3), gpu_ms_reference_semantics=round(refsem, 3),
                  cpp_api=cpp,
                  gpu_ms_exact=round(exact_ms, 3), blocking=blocking,
@@ -522,9 +550,15 @@ def run_forward_e(args, torch, tg):
                  roofline_kernels=kern,
                  roofline_note="T_roof = sum over the dataflow's kernels of max(compulsory "
                                "bytes / 8 TB/s, flops / 157.3 TF/s); blocked passes count "
-                               "their compulsory L2 fills, not the L2-served gathers")
+                               "their compulsory L2 fills, not the L2-served gathers",
+                 gather_bound_ms=round(troof_l2, 4) if troof_l2 else None,
+                 gather_bound_frac=round(troof_l2 / cached, 4) if troof_l2 else None,
+                 gather_bound_note="the same sum with each blocked pass bounded also by its "
+                                   "gathered lines x 128 B at the aggregation kernel's measured "
+                                   "rate on L2-resident rows (l2_gather)")
         log(f"{name}: cached {cached:.2f} ms, reference semantics {refsem:.2f} ms, "
-            f"exact {exact_ms:.2f} ms")
+            f"exact {exact_ms:.2f} ms; roofline {troof:.3f} ms, gather bound "
+            f"{troof_l2 or 0:.3f} ms ({(troof_l2 or 0) / cached:.3f})")
         if ref is not None:
             rm = ref.model(spec, w)
             t1 = time.perf_counter()
@@ -551,7 +585,43 @@ def run_forward_e(args, torch, tg):
         del raw, raw_r
         out[name] = r
         del model, y
-    return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), models=out)
+    return dict(n=n, nnz=adj.nnz, csr_build_ms=round(csr_ms, 2), l2_gather=l2, models=out)
+
+
+def measure_l2_gather(torch, tg, rows: int = 500_000, deg: int = 64, cols: int = 16384,
+                      f: int = 32, reps: int = 50):
+    """The aggregation kernel's gather rate when every gathered row is
+    L2-resident: a SAGE-mean aggregation (unweighted, as the factored GCN
+    and SAGE passes) of `rows` rows with `deg` sorted random columns each
+    in [0, cols), B = cols x f floats (2 MB at the defaults: every line stays
+    in each XCD's 4 MB L2).  Rate = gathered bytes (one 128-byte line per
+    entry at f = 32) / HIP-event time per call, the mean over `reps` calls."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    rp = (torch.arange(rows + 1, device=dev, dtype=torch.int64) * deg).to(torch.int32)
+    ci = torch.randint(0, cols, (rows, deg), generator=g, device=dev, dtype=torch.int32)
+    ci = torch.sort(ci, dim=1)[0].reshape(-1).contiguous()
+    a = tg.DeviceCSR(rows, cols, rp, ci, torch.ones(rows * deg, device=dev))
+    b = torch.randn(cols, f, generator=g, device=dev)
+    plan = tg.SpmmPlan(rp, rows, rows * deg, f)
+    for _ in range(20):
+        tg.sage_aggregate(plan, a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        tg.sage_aggregate(plan, a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    gathered = rows * deg * 128 * (-(-f // 32))
+    del a, b, plan, ci, rp
+    torch.cuda.empty_cache()
+    r = dict(rate_gbs=round(gathered / ms / 1e6, 1), ms=round(ms, 4), rows=rows, entries=rows * deg,
+             cols=cols, f=f, gathered_bytes=gathered)
+    log(f"L2-resident gather rate: {r['rate_gbs']} GB/s ({r})")
+    return r
 
 
 def run_calib_gather(torch, tg, rows: int = 1 << 23):
