@@ -774,11 +774,25 @@ __global__ __launch_bounds__(512) void gemm_mfma_thin_lds_kernel(GemmArgs g) {
     };
     if (active && nt > 0) fetch(0, a0);
     if (active && nt > 1) fetch(1, a1);
-    // stage B, zero-padded to nt * 32 rows and BN columns
+    // stage B, zero-padded to nt * 32 rows and BN columns: eight loads in
+    // flight per thread before their stores (a load-store loop waited out
+    // one load latency per element)
     const int64_t kp = nt * kTK;
-    for (int64_t e = threadIdx.x; e < kp * BN; e += blockDim.x) {
-        const int64_t k = e / BN, c = e % BN;
-        Bs[((k >> 3) * BN + c) * 8 + (k & 7)] = (k < K && c < N) ? g.b1[k * g.ldb1 + c] : 0.0f;
+    const int64_t total = kp * BN;
+    for (int64_t e0 = threadIdx.x; e0 < total; e0 += 8 * static_cast<int64_t>(blockDim.x)) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t e = e0 + u * static_cast<int64_t>(blockDim.x);
+            const int64_t k = e / BN, c = e % BN;
+            v[u] = (e < total && k < K && c < N) ? g.b1[k * g.ldb1 + c] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t e = e0 + u * static_cast<int64_t>(blockDim.x);
+            const int64_t k = e / BN, c = e % BN;
+            if (e < total) Bs[((k >> 3) * BN + c) * 8 + (k & 7)] = v[u];
+        }
     }
     __syncthreads();
     if (!active) return;
