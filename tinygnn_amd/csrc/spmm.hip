@@ -761,8 +761,8 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                 dl[j] = att_d[static_cast<int64_t>(cl[j]) * att_stride];
         }
         // U gathers in flight per step; in the chunk's last, partial batch
-        // the slots past its end gather row 0 (in bounds: cl is 0 there) and
-        // are not accumulated.
+        // the slots past its end are not accumulated (and gather row 0, in
+        // bounds since cl is 0 there, or nothing; see below).
         if constexpr (LPR == 16 || LPR == 4) {
             const int cnt = e - base < BE ? e - base : BE;
             // slot s0 + u of the batch is entry (s0 + u) % CPL of lane (s0 + u) / CPL:
@@ -779,13 +779,26 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                         if constexpr (MODE == kAggWeighted)
                             w[u] = group_bcast<LPR, (s0 + u) / CPL>(wl[(s0 + u) % CPL]);
                     });
+                    // plain sums (the column-blocked GCN and SAGE passes, long
+                    // chunks): slots past the chunk's end gather nothing, their
+                    // lanes masked off (config-E GCN / SAGE forwards 1% faster);
+                    // the other modes gather row 0 there (the per-slot branches
+                    // cost more than they save on config D's short rows and in
+                    // the GAT passes)
                     float bv[U][VPL][VEC];
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
+                        if (MODE != kAggSum || s0 + u < cnt) {
 #pragma unroll
-                        for (int v = 0; v < VPL; ++v)
-                            load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                            for (int v = 0; v < VPL; ++v)
+                                load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                        } else {
+#pragma unroll
+                            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                                for (int k = 0; k < VEC; ++k) bv[u][v][k] = 0.0f;
+                        }
                     }
                     if (s0 == 0) fetch(base + BE);
                     if constexpr (MODE == kAggAttn) {
@@ -851,13 +864,26 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                         if constexpr (MODE == kAggWeighted)
                             w[u] = __shfl(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
                     }
+                    // plain sums (the column-blocked GCN and SAGE passes, long
+                    // chunks): slots past the chunk's end gather nothing, their
+                    // lanes masked off (config-E GCN / SAGE forwards 1% faster);
+                    // the other modes gather row 0 there (the per-slot branches
+                    // cost more than they save on config D's short rows and in
+                    // the GAT passes)
                     float bv[U][VPL][VEC];
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
+                        if (MODE != kAggSum || s0 + u < cnt) {
 #pragma unroll
-                        for (int v = 0; v < VPL; ++v)
-                            load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                            for (int v = 0; v < VPL; ++v)
+                                load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
+                        } else {
+#pragma unroll
+                            for (int v = 0; v < VPL; ++v)
+#pragma unroll
+                                for (int k = 0; k < VEC; ++k) bv[u][v][k] = 0.0f;
+                        }
                     }
                     if (s0 == 0) fetch(base + BE);
                     if constexpr (MODE == kAggAttn) {
