@@ -199,8 +199,8 @@ def test_blocked_aggregation(gpu, restate, case):
     the unblocked path within the same tolerance.  Covers wide layers (300
     columns: ten tiles; A + I passes in 64-column lane groups, SAGE's in
     32-column ones), a narrow last layer, three 32-column GAT heads (kept in
-    32-column groups), two 64-column heads (one weight plane per 64-column
-    group), empty rows, unsorted rows and rows of more than one plan chunk
+    32-column groups), two 64-column heads (one per 64-column lane group,
+    destination scores computed from the gathered rows), empty rows, unsorted rows and rows of more than one plan chunk
     inside a block.  Last tiles of 12, 7 and 10 valid columns, and of 28,
     25 (the wide_tail cases)."""
     import tinygnn_amd as tg
@@ -217,7 +217,7 @@ def test_blocked_aggregation(gpu, restate, case):
         # 1/sqrt(deg) blows up the normalised weights and the cancellation
         a.val[:] = np.abs(a.val) + 0.01
         spec = synth.spec_gcn(48, 60, 25) if case == "gcn_wide_tail" else synth.spec_gcn(48, 300, 7)
-    elif case == "gat_wide_heads":  # heads of 64 columns: one weight plane per 64-column group
+    elif case == "gat_wide_heads":  # heads of 64 columns: one per 64-column lane group
         spec = synth.spec_gat(48, 64, 2, 7)
     elif case.startswith("gat"):
         spec = synth.spec_gat(48, 32, 3, 7)
@@ -550,7 +550,7 @@ def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
 @pytest.mark.parametrize("precision", ["fast", "exact"])
 def test_blocked_mixed_stack(gpu, restate, precision):
     """A stack that shares one blocked A + I between GCN (values) and GAT
-    (attention-weight planes), plus SAGE-mean over blocked A, forced to 40
+    (attention weights computed in the passes), plus SAGE-mean over blocked A, forced to 40
     blocks: within the fast tolerance of the oracle, and in exact precision
     bit-identical to the unblocked exact forward (GCN / SAGE layers keep the
     reference's order; GAT matches the unblocked exact kernel)."""
