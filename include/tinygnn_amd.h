@@ -352,15 +352,17 @@ int tg_model_invalidate(tg_model_t model);
  * directly (below).  Filled by the last forward; any pointer may be null. */
 int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
                            int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct);
-/* How a fast-precision GCN-only model gets the blocked A + I its factored
- * passes read (no counterpart in the reference; for tests and measurement).
- * direct = 1 (the default): when A's values are all 1, its rows sorted and
+/* How a fast-precision model whose blocked A + I is read only by the
+ * factored GCN passes (A's values all 1) or by GAT passes that carry their
+ * softmax gets that copy (no counterpart in the reference; for tests and
+ * measurement).  direct = 1 (the default): when A's rows are sorted and
  * without a diagonal, the blocked copy is split from A directly, each row's
- * diagonal placed where add_self_loops would insert it, and gcn_norm's
- * degrees come from the row lengths; A + I itself is never written.  The
- * build checks those conditions and otherwise takes the path of direct = 0:
- * gcn_norm writes A + I's structure, which is then split.  Both give the same
- * blocked copy and the same outputs bit for bit.  Drops the cached state. */
+ * diagonal placed where add_self_loops would insert it (and, for GCN,
+ * gcn_norm's degrees come from the row lengths); A + I itself is never
+ * written.  The build checks those conditions and otherwise takes the path
+ * of direct = 0: gcn_norm / add_self_loops write A + I's structure, which is
+ * then split.  Both give the same blocked copy and the same outputs bit for
+ * bit.  Drops the cached state. */
 int tg_model_set_self_loop_split(tg_model_t model, int direct);
 
 /* ------------------------------------------------------------------------

@@ -463,7 +463,7 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
 
 
 @pytest.mark.parametrize("model", ["gcn", "gat"])
-@pytest.mark.parametrize("order", ["sorted", "unsorted"])
+@pytest.mark.parametrize("order", ["sorted", "unsorted", "unsorted_in_block"])
 def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
     """The blocked A + I split straight from A (rows of up to 9,000 entries:
     the workgroup-per-row kernels past 4,096) equals the copy split from the
@@ -471,7 +471,9 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
     and the oracle within tolerance: the factored GCN (32-column groups) and a
     GAT carrying its softmax across the passes (64-column groups).  A row
     out of order makes the direct split decline (sl_direct False) and the
-    forward take the written A + I."""
+    forward take the written A + I; so does a row out of order inside one
+    block (two adjacent columns around the diagonal swapped), where the
+    block order holds but the diagonal's place would not be unique."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(91)
     n = 3000
@@ -483,6 +485,19 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
     if order == "unsorted":  # one long row reversed
         i = int(np.argmax(np.diff(g.row_ptr)))
         g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]] = g.col_ind[g.row_ptr[i]:g.row_ptr[i + 1]][::-1]
+    elif order == "unsorted_in_block":  # c_p < i < c_p+1 in i's block (500 rows), swapped
+        done = False
+        for i in range(n):
+            s0, e0 = int(g.row_ptr[i]), int(g.row_ptr[i + 1])
+            for p in range(s0, e0 - 1):
+                c1, c2 = int(g.col_ind[p]), int(g.col_ind[p + 1])
+                if c1 < i < c2 and c1 // 500 == i // 500 == c2 // 500:
+                    g.col_ind[p], g.col_ind[p + 1] = c2, c1
+                    done = True
+                    break
+            if done:
+                break
+        assert done
     spec = synth.spec_gcn(16, 64, 5) if model == "gcn" else synth.spec_gat(16, 64, 2, 5)
     w = synth.model_weights(spec, seed=9)
     x = rng.standard_normal((n, 16)).astype(np.float32)

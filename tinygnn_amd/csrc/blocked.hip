@@ -196,7 +196,8 @@ __global__ __launch_bounds__(256) void block_split_kernel(
 // position.  An entry that steps back to an earlier block sets flags[0] (the
 // caller then runs the general split).  With vdiag every row i also holds a
 // virtual entry (column i, no value) before its first column > i: the
-// diagonal of A + I for an A without one; a diagonal in A sets flags[1].
+// diagonal of A + I for an A without one; a diagonal in A sets flags[1], a
+// row out of order anywhere flags[0].
 // ---------------------------------------------------------------------------
 struct FlatSplit {
     const int32_t* rp;
@@ -332,6 +333,10 @@ __global__ __launch_bounds__(256) void flat_count_kernel(FlatSplit a) {
         for (int x = pb + 1; x <= b; ++x) a.starts[static_cast<int64_t>(x) * a.n + row] = pos;
         if (a.vdiag) {
             if (c == row) atomicOr(&a.flags[1], 1);
+            // the virtual entry goes before the row's first column > i: one
+            // such position only in a sorted row (out of order within a
+            // block, decline as for block order)
+            if (!f.first[u] && pc > c) atomicOr(&a.flags[0], 1);
             if ((f.first[u] || pc < row) && c > row) a.ins[row] = pos;
         }
     }

@@ -19,12 +19,16 @@
 //   * rows longer than one chunk: every chunk stores its unnormalised sum
 //     with its own (max, sum); gat_reduce_kernel merges them in chunk order
 //     (max of maxima, sums rescaled by exp(m_c - M)).
-//   * column-blocked form (large, dense graphs): gat_stats_kernel first
-//     finds each row's max score and 1/sum per head; then the blocked passes
-//     (blocked.hip) aggregate alpha_ij Wh_j block by block, each pass
-//     computing alpha_ij = exp(e_ij - max_i) * (1/sum_i) per entry and head
-//     from the [n x heads] scores and statistics (the attention mode of the
-//     aggregation kernel): the attention matrix is never stored here either.
+//   * column-blocked form (large, dense graphs), fast precision: the online
+//     softmax carried across the block passes (gat_online_chunk_kernel, a
+//     running max and sum per row and column group), where a lane group
+//     holding a whole head computes dst_j = a_r . Wh_j from the rows it
+//     gathers instead of reading it; exact precision and the other layouts:
+//     a statistics sweep (gat_exact_stats_kernel / gat_stats_kernel: each
+//     row's max score and 1/sum per head), then passes (blocked.hip) that
+//     compute alpha_ij = exp(e_ij - max_i) * (1/sum_i) per entry and head from
+//     the [n x heads] scores and statistics (the attention mode of the
+//     aggregation kernel).  The attention matrix is never stored here either.
 #include "aggregate.hpp"
 #include "common.hpp"
 #include "device_utils.hpp"
