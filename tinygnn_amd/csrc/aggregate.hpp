@@ -39,6 +39,10 @@ struct AggEpilogue {
     int64_t scale_ld = 0;
     int scale_cols = 1;
     int exact_exp = 0;  // ELU's exp evaluated as exp_rn (the exact GAT path)
+    // plain sums (no values, not max or attention): a chunk's last, partial
+    // batch gathers nothing for the slots past its end (worth it for the
+    // fast blocked passes' chunks, not for long unsplit ones)
+    int mask_tail = 0;
     // B's layout (tile_cols = 32 only): > 0 = tile-major, 32-column tile t
     // of row j at B + t * b_tile_stride + j * ldb (ldb = 32); 0 = row-major
     int64_t b_tile_stride = 0;

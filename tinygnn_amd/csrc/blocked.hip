@@ -655,6 +655,7 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         e.b_tile_stride = epi.b_tile_stride;
         e.w_head_cols = epi.w_head_cols;
         e.exact_exp = epi.exact_exp;
+        e.mask_tail = epi.mask_tail;
         e.att_src = epi.att_src;
         e.att_dst = epi.att_dst;
         e.att_max = epi.att_max;

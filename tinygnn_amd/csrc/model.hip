@@ -578,6 +578,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
                 epi.row_scale = m.dis.as<float>();
                 epi.scale_ld = 1;
                 epi.scale_cols = static_cast<int>(l.out);
+                epi.mask_tail = 1;
             }
             epi.bias = l.bias ? l.b.as<float>() : nullptr;
             epi.act = l.act;

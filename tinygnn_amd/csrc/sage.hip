@@ -176,6 +176,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         epi.post = post;
         if (tiled) {
             epi.b_tile_stride = n * 32;
+            epi.mask_tail = 1;
             run_aggregate_blocked(*blocked, f_out, t + (fp / 32) * n * 32, 32, out, f_out, epi, s);
         } else if (blocked) {
             run_aggregate_blocked(*blocked, f_out, t + fp, 2 * fp, out, f_out, epi, s);

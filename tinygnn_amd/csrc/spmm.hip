@@ -624,7 +624,9 @@ __device__ __forceinline__ void finish_store(float (&x)[VEC], int row, int deg, 
 
 // kAggAttn: GAT's attention weights, computed per entry inside the pass
 // (AggEpilogue.att_*), then accumulated as kAggWeighted's.
-enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2, kAggAttn = 3 };
+// kAggSumTail: kAggSum whose chunks' last, partial batches gather nothing
+// for the slots past the chunk's end (AggEpilogue.mask_tail).
+enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2, kAggAttn = 3, kAggSumTail = 4 };
 
 // One step of a row's reduction: fma with the edge weight (SpMM's value,
 // ops.cpp:266-287, or a GAT attention weight), a plain add (SAGE mean,
@@ -633,7 +635,7 @@ enum { kAggWeighted = 0, kAggSum = 1, kAggMax = 2, kAggAttn = 3 };
 template <int MODE>
 __device__ __forceinline__ float combine(float acc, float x, float w) {
     if constexpr (MODE == kAggWeighted || MODE == kAggAttn) return __builtin_fmaf(w, x, acc);
-    if constexpr (MODE == kAggSum) return acc + x;
+    if constexpr (MODE == kAggSum || MODE == kAggSumTail) return acc + x;
     return (acc < x) ? x : acc;
 }
 
@@ -779,17 +781,17 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                         if constexpr (MODE == kAggWeighted)
                             w[u] = group_bcast<LPR, (s0 + u) / CPL>(wl[(s0 + u) % CPL]);
                     });
-                    // plain sums (the column-blocked GCN and SAGE passes, long
-                    // chunks): slots past the chunk's end gather nothing, their
-                    // lanes masked off (config-E GCN / SAGE forwards 1% faster);
-                    // the other modes gather row 0 there (the per-slot branches
-                    // cost more than they save on config D's short rows and in
-                    // the GAT passes)
+                    // kAggSumTail (the fast column-blocked GCN and SAGE passes):
+                    // slots past the chunk's end gather nothing, their lanes
+                    // masked off (config-E GCN / SAGE forwards 1% faster); the
+                    // other modes gather row 0 there (the per-slot branches cost
+                    // more than they save on config D's short rows, in the GAT
+                    // passes and on exact SAGE's long chunks, 4%)
                     float bv[U][VPL][VEC];
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
-                        if (MODE != kAggSum || s0 + u < cnt) {
+                        if (MODE != kAggSumTail || s0 + u < cnt) {
 #pragma unroll
                             for (int v = 0; v < VPL; ++v)
                                 load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
@@ -864,17 +866,17 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
                         if constexpr (MODE == kAggWeighted)
                             w[u] = __shfl(wl[(s0 + u) % CPL], (s0 + u) / CPL, LPR);
                     }
-                    // plain sums (the column-blocked GCN and SAGE passes, long
-                    // chunks): slots past the chunk's end gather nothing, their
-                    // lanes masked off (config-E GCN / SAGE forwards 1% faster);
-                    // the other modes gather row 0 there (the per-slot branches
-                    // cost more than they save on config D's short rows and in
-                    // the GAT passes)
+                    // kAggSumTail (the fast column-blocked GCN and SAGE passes):
+                    // slots past the chunk's end gather nothing, their lanes
+                    // masked off (config-E GCN / SAGE forwards 1% faster); the
+                    // other modes gather row 0 there (the per-slot branches cost
+                    // more than they save on config D's short rows, in the GAT
+                    // passes and on exact SAGE's long chunks, 4%)
                     float bv[U][VPL][VEC];
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pitch;
-                        if (MODE != kAggSum || s0 + u < cnt) {
+                        if (MODE != kAggSumTail || s0 + u < cnt) {
 #pragma unroll
                             for (int v = 0; v < VPL; ++v)
                                 load_vec<VEC>(reinterpret_cast<const float*>(bl[v] + off), bv[u][v]);
@@ -1085,6 +1087,8 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
     if (av) {
         TG_AGG_MODE(kAggWeighted)
     }
+    if (epi.mask_tail && vec == 4 && L.lpr == 8 && L.vpl == 1)  // the 32-column passes only
+        return launch_agg<4, 8, 1, kAggSumTail>(p, L, f, ci, av, B, ldb, C, ldc, e, s);
     TG_AGG_MODE(kAggSum)
 #undef TG_AGG_MODE
 }
