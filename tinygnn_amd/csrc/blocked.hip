@@ -477,8 +477,11 @@ SplitTemps setup_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, int64_t nnz_src
     bk.weighted = weighted;
     bk.brp.reserve(static_cast<size_t>(nb * n + 1) * sizeof(int32_t));
     bk.idx16 = rows_per_block <= 65536;
+    // 64 bytes past the indices: the 16-bit passes' scalar loads read whole
+    // 16-entry batches, up to 15 entries past a chunk's end
     bk.bci.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) *
-                   (bk.idx16 ? sizeof(uint16_t) : sizeof(int32_t)));
+                       (bk.idx16 ? sizeof(uint16_t) : sizeof(int32_t)) +
+                   64);
     if (weighted) bk.bv.reserve(static_cast<size_t>(std::max<int64_t>(nnz, 1)) * sizeof(float));
     Carver cv(nullptr, 0);
     carve_split(cv, n, nnz_src, nb);

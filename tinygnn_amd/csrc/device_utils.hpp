@@ -141,6 +141,15 @@ __device__ __forceinline__ void group_transpose_sum(float (&x)[N], int lane) {
     transpose_sum_step<LPR / 2, N>(x, lane);
 }
 
+// v with lane LANE replaced by the wave-uniform value s (v_writelane_b32;
+// this compiler has no builtin for it).
+template <int LANE>
+__device__ __forceinline__ uint32_t write_lane(uint32_t s, uint32_t v) {
+    static_assert(LANE >= 0 && LANE < kWave, "lane");
+    asm("v_writelane_b32 %0, %1, %2" : "=v"(v) : "s"(s), "i"(LANE), "0"(v));
+    return v;
+}
+
 // Non-temporal (streaming) loads for data read exactly once.
 template <typename T>
 __device__ __forceinline__ T ld_stream(const T* p) {

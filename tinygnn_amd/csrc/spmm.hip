@@ -956,6 +956,158 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     }
 }
 
+// The fast column-blocked passes' kernel (kAggSumTail over 16-bit block
+// indices, 8-lane groups of 32 columns): agg_chunk_kernel<4, 8, 1,
+// kAggSumTail>'s arithmetic, with the index stream read through scalar loads.
+//
+// Vector loads of a compute unit return in issue order, so an index load
+// that misses to the MALL or HBM holds back the L2-resident gathers issued
+// after it, by any wavefront of that unit.  Scalar loads return through the
+// scalar cache instead: a gather probe at a 4 MB block (32,768 rows of
+// 128 B) with a 537 MB index stream moved 25.8 TB/s with scalar index loads
+// against 22.0 with vector ones (a producer wavefront streaming the indices
+// into LDS through vector loads: 22.9).
+//
+// The wavefront walks its eight chunks in a uniform loop of 16-entry batches
+// over dword-aligned positions (a chunk starting at an odd entry masks its
+// first slot).  Each batch, one scalar load per group brings 8 dwords (16
+// indices) and v_writelane spreads them as the vector path holds them (lane
+// p of a group: entries 2p, 2p + 1), for the same shuffles; the next batch's
+// scalar loads are issued after the current gathers.  A finished group
+// reloads its last batch (unused), so every load stays within the chunk's
+// batches, at most 15 entries past its end (the blocked copy keeps 64 bytes
+// of padding after its indices).
+__device__ __forceinline__ uint32_t put_group(const uint32_t (&d)[8], int gg, uint32_t v) {
+    switch (gg) {  // gg is a compile-time constant after unrolling
+#define TG_PUT(G)                                                                      \
+    case G:                                                                            \
+        v = write_lane<8 * G + 0>(d[0], v);                                            \
+        v = write_lane<8 * G + 1>(d[1], v);                                            \
+        v = write_lane<8 * G + 2>(d[2], v);                                            \
+        v = write_lane<8 * G + 3>(d[3], v);                                            \
+        v = write_lane<8 * G + 4>(d[4], v);                                            \
+        v = write_lane<8 * G + 5>(d[5], v);                                            \
+        v = write_lane<8 * G + 6>(d[6], v);                                            \
+        v = write_lane<8 * G + 7>(d[7], v);                                            \
+        break;
+        TG_PUT(0) TG_PUT(1) TG_PUT(2) TG_PUT(3) TG_PUT(4) TG_PUT(5) TG_PUT(6) TG_PUT(7)
+#undef TG_PUT
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
+    const int4* __restrict__ chunks, int64_t n_chunks, const int64_t* __restrict__ n_chunks_dev,
+    const float* __restrict__ B, int64_t ldb, float* __restrict__ C, int64_t ldc,
+    float* __restrict__ partials, int64_t ldp, int64_t f, AggEpilogue epi) {
+    constexpr int LPR = 8, VEC = 4, U = 16;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int64_t cid = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + g;
+    const int64_t nch = n_chunks_dev ? *n_chunks_dev : n_chunks;
+    // groups past the plan's end, and empty chunks of a middle pass, take
+    // part in the wavefront's loop with no entries and store nothing
+    int4 ch = make_int4(0, 0, 0, -1);
+    bool active = cid < nch;
+    if (active) ch = chunks[cid];
+    if (active && epi.skip_empty && ch.z == ch.y) active = false;
+    if (!active) ch = make_int4(0, 0, 0, -1);
+    if (__builtin_amdgcn_readfirstlane(__ballot(active) == 0 ? 1 : 0)) return;
+
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * (LPR * VEC);
+    const int64_t fo = fbase + static_cast<int64_t>(l) * VEC;
+    const bool ok = fo < f;
+    const int64_t fl = ok ? fo : fbase;
+    float acc[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+    if (active && epi.acc && ch.w < 0 && ok) {
+        // continue the row's chain from the earlier passes' value
+        const float* prev = C + static_cast<int64_t>(ch.x) * ldc + fo;
+        if (epi.vec_io) {
+            load_vec_nt<VEC>(prev, acc);
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) acc[k] = fo + k < f ? prev[k] : 0.0f;
+        }
+    }
+    const char* bl = reinterpret_cast<const char*>(
+        epi.b_tile_stride > 0 ? B + (fl >> 5) * epi.b_tile_stride + (fl & 31) : B + fl);
+    const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
+
+    // the group's batches: 16 entries each from the dword-aligned start
+    const int a = ch.y & ~1;
+    const int nb = ch.z > ch.y ? (ch.z - a + 15) >> 4 : 0;
+    int nmax = 0;
+#pragma unroll
+    for (int gg = 0; gg < kWave / LPR; ++gg) {
+        const int x = __builtin_amdgcn_readlane(nb, gg * LPR);
+        nmax = x > nmax ? x : nmax;
+    }
+    const uint32_t* cw = reinterpret_cast<const uint32_t*>(epi.ci16);
+    // dword offset of batch t of the lane's group (its last batch once done;
+    // 0 for a group with none)
+    auto batch_off = [&](int t) { return nb > 0 ? (a >> 1) + 8 * (t < nb ? t : nb - 1) : 0; };
+    auto load_batch = [&](int t, uint32_t (&d)[kWave / LPR][8]) {
+        const int o = batch_off(t);
+#pragma unroll
+        for (int gg = 0; gg < kWave / LPR; ++gg) {
+            const int og = __builtin_amdgcn_readlane(o, gg * LPR);
+#pragma unroll
+            for (int p = 0; p < 8; ++p) d[gg][p] = cw[og + p];
+        }
+    };
+    uint32_t d[kWave / LPR][8];
+    uint32_t packed = 0;
+    load_batch(0, d);
+#pragma unroll
+    for (int gg = 0; gg < kWave / LPR; ++gg) packed = put_group(d[gg], gg, packed);
+    (void)lane;
+
+    for (int t = 0; t < nmax; ++t) {
+        // slots [lo, cnt) of this batch are the group's entries
+        const int base = a + 16 * t;
+        const int lo = ch.y - base, cnt = ch.z - base;
+        const int c0 = static_cast<int>(packed & 0xFFFFu), c1 = static_cast<int>(packed >> 16);
+        float bv[U][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int col = __shfl((u & 1) ? c1 : c0, u >> 1, LPR);
+            if (u >= lo && u < cnt) {
+                const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
+                load_vec<VEC>(reinterpret_cast<const float*>(bl + off), bv[u]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) bv[u][k] = 0.0f;
+            }
+        }
+        // the next batch's indices, behind this batch's gathers
+        __builtin_amdgcn_sched_barrier(0);
+        load_batch(t + 1, d);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool valid = u >= lo && u < cnt;  // a select, not a branch
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                const float nx = acc[k] + bv[u][k];
+                acc[k] = valid ? nx : acc[k];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int gg = 0; gg < kWave / LPR; ++gg) packed = put_group(d[gg], gg, packed);
+    }
+
+    if (!active || !ok) return;
+    if (ch.w < 0) {
+        finish_store<VEC>(acc, ch.x, ch.z - ch.y, fo, f, C, ldc, epi, false);
+    } else {
+        store_vec<VEC>(partials + static_cast<int64_t>(ch.w) * ldp + fo, acc);
+    }
+}
+
 // Finishes split rows: partials of a row are combined in chunk order.
 template <int VEC, int LPR, int VPL, int MODE>
 __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict__ split,
@@ -1010,6 +1162,29 @@ void launch_agg(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_reduce_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
+            p.split, p.n_split, dc ? dc + 1 : nullptr, p.partials, ldp, C, ldc, f, epi);
+        TG_LAUNCH_CHECK();
+    }
+}
+
+// The fast column-blocked passes over 16-bit indices (agg_sidx_kernel), then
+// split rows as launch_agg<4, 8, 1, kAggSumTail>'s.
+void launch_agg_sidx(const PlanView& p, const LaneLayout& L, int64_t f, const float* B,
+                     int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi, hipStream_t s) {
+    constexpr int GPB = 256 / 8;
+    const int64_t ldp = round_up(f, 4);
+    const int64_t* dc = p.dev_counts;
+    if (p.n_chunks > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        agg_sidx_kernel<<<grid, 256, 0, s>>>(p.chunks, p.n_chunks, dc, B, ldb, C, ldc,
+                                             p.partials, ldp, f, epi);
+        TG_LAUNCH_CHECK();
+    }
+    if (p.n_split > 0) {
+        dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
+                  static_cast<unsigned>(L.n_tiles));
+        agg_reduce_kernel<4, 8, 1, kAggSumTail><<<grid, 256, 0, s>>>(
             p.split, p.n_split, dc ? dc + 1 : nullptr, p.partials, ldp, C, ldc, f, epi);
         TG_LAUNCH_CHECK();
     }
@@ -1087,8 +1262,11 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
     if (av) {
         TG_AGG_MODE(kAggWeighted)
     }
-    if (epi.mask_tail && vec == 4 && L.lpr == 8 && L.vpl == 1)  // the 32-column passes only
+    if (epi.mask_tail && vec == 4 && L.lpr == 8 && L.vpl == 1) {  // the 32-column passes only
+        // 16-bit indices are a blocked copy's, padded for the scalar loads
+        if (epi.ci16) return launch_agg_sidx(p, L, f, B, ldb, C, ldc, e, s);
         return launch_agg<4, 8, 1, kAggSumTail>(p, L, f, ci, av, B, ldb, C, ldc, e, s);
+    }
     TG_AGG_MODE(kAggSum)
 #undef TG_AGG_MODE
 }
