@@ -90,11 +90,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 template <int LPR, int SRC>
 __device__ __forceinline__ int group_bcast(int v) {
     static_assert(SRC >= 0 && SRC < LPR, "source lane outside the group");
+    // every lane of the row or quad is written: no old value (mov_dpp)
     if constexpr (LPR == 16) {
-        return __builtin_amdgcn_update_dpp(0, v, 0x150 + SRC, 0xF, 0xF, false);  // row_newbcast
+        return __builtin_amdgcn_mov_dpp(v, 0x150 + SRC, 0xF, 0xF, false);  // row_newbcast
     } else if constexpr (LPR == 4) {
-        return __builtin_amdgcn_update_dpp(0, v, SRC | (SRC << 2) | (SRC << 4) | (SRC << 6), 0xF,
-                                           0xF, false);  // quad_perm
+        return __builtin_amdgcn_mov_dpp(v, SRC | (SRC << 2) | (SRC << 4) | (SRC << 6), 0xF, 0xF,
+                                        false);  // quad_perm
     } else {
         return __shfl(v, SRC, LPR);
     }
@@ -108,7 +109,8 @@ __device__ __forceinline__ float group_bcast(float v) {
 // The value of the partner lane that differs in lane bit K (K = 8, 4, 2, 1)
 // within a 16-lane row, and in no higher bit: row_mirror (lane i <-> 15 - i)
 // for 8, row_half_mirror (i <-> 7 - i within each eight) for 4, quad_perm
-// [2,3,0,1] and [1,0,3,2] for 2 and 1.  The partner must be active.
+// [2,3,0,1] and [1,0,3,2] for 2 and 1.  The partner must be active.  (With
+// an old value the compiler folds the move into a following add, v_add_dpp.)
 template <int K>
 __device__ __forceinline__ float dpp_flip(float v) {
     static_assert(K == 8 || K == 4 || K == 2 || K == 1, "partner bit");

@@ -797,7 +797,30 @@ __device__ __forceinline__ void out_store(float* row, int64_t fo, int64_t f, boo
     }
 }
 
-template <int LPR, bool DIN>
+// The maximum over an aligned group of LPR (8 or 16) lanes with DPP moves,
+// no LDS: max is exact, so the butterfly's order gives the same value as any.
+template <int LPR>
+__device__ __forceinline__ float group_max_dpp(float x) {
+    static_assert(LPR == 8 || LPR == 16, "group width");
+    float o;
+    if constexpr (LPR == 16) {
+        o = dpp_flip<8>(x);
+        x = (x < o) ? o : x;
+    }
+    o = dpp_flip<4>(x);
+    x = (x < o) ? o : x;
+    o = dpp_flip<2>(x);
+    x = (x < o) ? o : x;
+    o = dpp_flip<1>(x);
+    return (x < o) ? o : x;
+}
+
+// TMASK: the head's last lane holds fewer than four Wh columns (a_r . Wh_j
+// masks the row padding).  OFF32: every gather's byte offset from B fits 32
+// bits, and its column and the row pitch 24 (the host checks), so gathers
+// take B as a scalar base and a 32-bit lane offset (one 24-bit multiply-add
+// per gather instead of a 64-bit one).
+template <int LPR, bool DIN, bool TMASK, bool OFF32>
 __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int32_t* __restrict__ ci,
     const uint16_t* __restrict__ ci16, const float* __restrict__ B, int64_t ldb,
@@ -849,6 +872,8 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
     }
 
     const char* bl = reinterpret_cast<const char*>(B + fl);
+    const char* bs = reinterpret_cast<const char*>(B);
+    const uint32_t loff = static_cast<uint32_t>(fl) * 4u;
     const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
     const int stride = P.heads;
     int ncl[CPL];
@@ -876,8 +901,13 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
         static_for<0, U>([&](auto uc) {
             constexpr int u = decltype(uc)::value;
             const int col = group_bcast<LPR, u / CPL>(cl[u % CPL]);
-            const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
-            ldv<4>(reinterpret_cast<const float*>(bl + off), bv[u]);
+            if constexpr (OFF32) {  // col and pitch below 2^24
+                const uint32_t off = __umul24(static_cast<uint32_t>(col), pitch) + loff;
+                ldv<4>(reinterpret_cast<const float*>(bs + off), bv[u]);
+            } else {
+                const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
+                ldv<4>(reinterpret_cast<const float*>(bl + off), bv[u]);
+            }
         });
         fetch(base + BE);
         if constexpr (DIN) {
@@ -888,7 +918,7 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
             static_for<0, U>([&](auto uc) {
                 constexpr int u = decltype(uc)::value;
                 float b1 = bv[u][1], b2 = bv[u][2], b3 = bv[u][3];
-                if (P.tail_mask) {  // uniform
+                if constexpr (TMASK) {
                     b1 = nv > 1 ? b1 : 0.0f;
                     b2 = nv > 2 ? b2 : 0.0f;
                     b3 = nv > 3 ? b3 : 0.0f;
@@ -910,11 +940,7 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
             ev[j] = lrelu(si + d[j], P.slope);
             if (base + l * CPL + j < e) bm = (bm < ev[j]) ? ev[j] : bm;
         }
-#pragma unroll
-        for (int off = LPR / 2; off >= 1; off >>= 1) {
-            const float o = __shfl_xor(bm, off, LPR);
-            bm = (bm < o) ? o : bm;
-        }
+        bm = group_max_dpp<LPR>(bm);
         if (m < bm) {  // uniform in the group
             const float fct = expf(m - bm);  // 0 when nothing was carried (m = -inf)
 #pragma unroll
@@ -928,16 +954,25 @@ __global__ __launch_bounds__(256, 4) void gat_online_chunk_kernel(
             wl[j] = base + l * CPL + j < e ? expf(ev[j] - m) : 0.0f;
             s += wl[j];
         }
-        static_for<0, U>([&](auto uc) {
-            constexpr int u = decltype(uc)::value;
-            const float w = group_bcast<LPR, u / CPL>(wl[u % CPL]);
-            const bool valid = u < cnt;  // a select, not a branch
+        if (cnt == BE) {  // a full batch: every slot is an entry (no selects)
+            static_for<0, U>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                const float w = group_bcast<LPR, u / CPL>(wl[u % CPL]);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float nx = __builtin_fmaf(w, bv[u][k], acc[k]);
-                acc[k] = valid ? nx : acc[k];
-            }
-        });
+                for (int k = 0; k < 4; ++k) acc[k] = __builtin_fmaf(w, bv[u][k], acc[k]);
+            });
+        } else {
+            static_for<0, U>([&](auto uc) {
+                constexpr int u = decltype(uc)::value;
+                const float w = group_bcast<LPR, u / CPL>(wl[u % CPL]);
+                const bool valid = u < cnt;  // a select, not a branch
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float nx = __builtin_fmaf(w, bv[u][k], acc[k]);
+                    acc[k] = valid ? nx : acc[k];
+                }
+            });
+        }
     }
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, LPR);
@@ -1036,6 +1071,11 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
     constexpr int GPB = 256 / LPR;
     const int64_t ldp = round_up(f, 4);
     const unsigned ytiles = static_cast<unsigned>(ceil_div(f, LPR * 4));
+    // gather offsets from a block's first row: (column within the block) x
+    // row pitch + column offset, all in 32 bits when they fit
+    const int64_t rows_in = bk.idx16 ? bk.rows_per_block : bk.n;
+    const bool off32 = rows_in * ldwh * 4 + ldwh * 4 < (int64_t(1) << 32) &&
+                       rows_in < (int64_t(1) << 24) && ldwh * 4 < (int64_t(1) << 24);
     for (int64_t blk = 0; blk < bk.n_blocks; ++blk) {
         const tg_spmm_plan_s& p = *bk.plans[blk];
         require(p.n_partials <= max_partials, "GATLayer: block plan has more partial slots");
@@ -1048,10 +1088,19 @@ void gat_online_passes(const BlockedCSR& bk, int64_t f, const float* wh, int64_t
             GatPass Q = P;
             Q.dst = P.dst + r0 * P.heads;
             dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)), ytiles);
-            gat_online_chunk_kernel<LPR, DIN><<<grid, 256, 0, s>>>(
-                p.chunks.as<int4>(), p.n_chunks, bk.idx16 ? nullptr : bk.bci.as<int32_t>(),
-                bk.idx16 ? bk.bci.as<uint16_t>() : nullptr, wh + r0 * ldwh, ldwh, out, ldo,
-                p.partials.as<float>(), ldp, f, Q);
+            const int32_t* ci = bk.idx16 ? nullptr : bk.bci.as<int32_t>();
+            const uint16_t* ci16 = bk.idx16 ? bk.bci.as<uint16_t>() : nullptr;
+            const float* bb = wh + r0 * ldwh;
+            float* pp = p.partials.as<float>();
+#define TG_GAT_ONLINE(TM_, O32_)                                                         \
+    gat_online_chunk_kernel<LPR, DIN, TM_, O32_><<<grid, 256, 0, s>>>(                  \
+        p.chunks.as<int4>(), p.n_chunks, ci, ci16, bb, ldwh, out, ldo, pp, ldp, f, Q)
+            if (Q.tail_mask) {
+                if (off32) TG_GAT_ONLINE(true, true); else TG_GAT_ONLINE(true, false);
+            } else {
+                if (off32) TG_GAT_ONLINE(false, true); else TG_GAT_ONLINE(false, false);
+            }
+#undef TG_GAT_ONLINE
             TG_LAUNCH_CHECK();
         }
         if (p.n_split > 0) {
