@@ -548,9 +548,17 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     const int wave = threadIdx.x >> 6;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int q = lane >> 4, r = lane & 15;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kMBM;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * kMBN;
     const int64_t M = g.m, N = g.n;
+    // Workgroup i runs on XCD i % 8 (round-robin dispatch).  XCD x takes the
+    // row tiles m = x (mod 8), and for each of them its column tiles one
+    // after another, so the second and later reads of the row tile's A
+    // find it in that XCD's L2.  Ids past an XCD's tiles exit.
+    const int64_t mt = (M + kMBM - 1) / kMBM, ntl = (N + kMBN - 1) / kMBN;
+    const int64_t xj = blockIdx.x / 8;
+    const int64_t mtile = (xj / ntl) * 8 + blockIdx.x % 8;
+    if (mtile >= mt) return;  // before any barrier: the whole workgroup
+    const int64_t m0 = mtile * kMBM;
+    const int64_t n0 = (xj % ntl) * kMBN;
     const int64_t t1 = (g.k1 + kMBK - 1) / kMBK;
     const int64_t nt = t1 + (g.a2 ? (g.k2 + kMBK - 1) / kMBK : 0);
 
@@ -1105,8 +1113,10 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
 #undef TG_THIN_CASE
     }
     if (algo == TG_GEMM_MFMA) {
-        dim3 grid(static_cast<unsigned>(ceil_div(g.m, kMBM)),
-                  static_cast<unsigned>(ceil_div(g.n, kMBN)));
+        // eight XCDs, each over its row tiles (gemm_mfma_kernel's mapping)
+        const int64_t wgs = 8 * ceil_div(ceil_div(g.m, kMBM), 8) * ceil_div(g.n, kMBN);
+        require(wgs < (int64_t(1) << 31), "matmul: too many row tiles");
+        dim3 grid(static_cast<unsigned>(wgs));
         auto width = [](std::initializer_list<int64_t> lds, std::initializer_list<const void*> ps) {
             for (int v : {4, 2}) {
                 bool ok = true;
