@@ -1001,7 +1001,6 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
     const float* __restrict__ B, int64_t ldb, float* __restrict__ C, int64_t ldc,
     float* __restrict__ partials, int64_t ldp, int64_t f, AggEpilogue epi) {
     constexpr int LPR = 8, VEC = 4, U = 16;
-    const int lane = threadIdx.x & (kWave - 1);
     const int g = threadIdx.x / LPR;
     const int l = threadIdx.x % LPR;
     const int64_t cid = static_cast<int64_t>(blockIdx.x) * (256 / LPR) + g;
@@ -1063,7 +1062,6 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
     load_batch(0, d);
 #pragma unroll
     for (int gg = 0; gg < kWave / LPR; ++gg) packed = put_group(d[gg], gg, packed);
-    (void)lane;
 
     for (int t = 0; t < nmax; ++t) {
         // slots [lo, cnt) of this batch are the group's entries
