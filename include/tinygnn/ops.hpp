@@ -14,8 +14,16 @@ namespace tinygnn {
 /// MFMA (within 1e-4 relative).
 Tensor matmul(const Tensor& A, const Tensor& B);
 
-/// C = A * B, A SparseCSR, B Dense (ops.cpp:198-297).
+/// C = A * B, A SparseCSR, B Dense (ops.cpp:198-297).  Every row is one
+/// fma chain in nonzero order, as in the reference: bit-identical.
 Tensor spmm(const Tensor& A, const Tensor& B);
+
+/// Summation order of spmm (an addition of this build: the reference has
+/// one order).  Exact is the reference's and spmm(A, B)'s; Fast sums rows
+/// longer than 1,024 nonzeros from per-chunk partials (a regrouped sum,
+/// within the fp32 summation bound of the exact one).
+enum class SpmmOrder : uint8_t { Exact = 0, Fast = 1 };
+Tensor spmm(const Tensor& A, const Tensor& B, SpmmOrder order);
 
 void relu_inplace(Tensor& X);
 void leaky_relu_inplace(Tensor& X, float alpha = 0.01f);

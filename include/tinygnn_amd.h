@@ -49,6 +49,11 @@ enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1 };
 enum { TG_POST_NONE = 0, TG_POST_RELU = 1, TG_POST_ELU = 2 };
 /* SAGE aggregator (layers.hpp:250-253 {Mean=0, Max=1}). */
 enum { TG_AGG_MEAN = 0, TG_AGG_MAX = 1 };
+/* Summation order of SpMM plans and Model forwards (no counterpart in the
+ * reference, which has one order): TG_PRECISION_EXACT keeps the reference's
+ * order bit for bit; TG_PRECISION_FAST may regroup sums (see the entry
+ * points that take it). */
+enum { TG_PRECISION_FAST = 0, TG_PRECISION_EXACT = 1 };
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* tg_last_error(void);
@@ -117,14 +122,17 @@ int tg_gcn_norm(int64_t n, int64_t nnz, const int32_t* row_ptr,
  * C[m x f] = A[m x k] * B[k x f].
  *
  * A plan holds the degree-binned row schedule of one CSR structure
- * (row_ptr): rows are cut into chunks of at most `chunk_nnz` nonzeros
- * (0 = default), chunks are ordered longest first, and rows of more than
- * one chunk are finished by an in-order reduction of per-chunk partials.
- * Rows of at most chunk_nnz nonzeros are bit-identical to the reference
- * (one lane per output element, fma in nonzero order); longer rows differ
- * only by the regrouping of their sum.  `nnz_bound` >= the actual nnz
- * (row_ptr[m]); `max_f` bounds the feature width of later executes.
- * Plan creation allocates device memory and synchronises `stream` once.
+ * (row_ptr): rows of at most `chunk_nnz` nonzeros (0 = default, 1,024) are
+ * chunks of their own, ordered longest first, each summed by one lane per
+ * output element with fma in nonzero order -- the reference's chain, bit
+ * for bit.  Longer rows ("split rows", listed longest first) are summed,
+ * by default (TG_PRECISION_EXACT), as the same single chain, one workgroup
+ * per row: the whole output is bit-identical to the reference.  Under
+ * TG_PRECISION_FAST they are cut into chunks whose per-chunk partials are
+ * added in chunk order (deterministic, a regrouped sum).  `nnz_bound` >=
+ * the actual nnz (row_ptr[m]); `max_f` bounds the feature width of later
+ * executes.  Plan creation allocates device memory and synchronises
+ * `stream` once.
  * ------------------------------------------------------------------------ */
 typedef struct tg_spmm_plan_s* tg_spmm_plan_t;
 int tg_spmm_plan_create(int64_t m, int64_t nnz_bound, const int32_t* row_ptr,
@@ -138,7 +146,19 @@ int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f,
                     const int32_t* row_ptr, const int32_t* col_ind, const float* val,
                     const float* b, int64_t ldb, float* c, int64_t ldc,
                     tg_stream_t stream);
-/* One-shot form: builds a plan, executes, frees it (allocates; synchronises). */
+/* Summation order of the plan's later executes and of tg_sage_aggregate /
+ * tg_sage_forward over it (TG_PRECISION_EXACT by default).  EXACT sums
+ * every row, split rows included, as one chain in nonzero order from 0 --
+ * the reference's order (src/ops.cpp:252-294) -- so the whole output is
+ * bit-identical to the reference: a row longer than the plan's chunk runs
+ * on one workgroup, its gathers spread over the workgroup, its chains
+ * walked in order from LDS.  FAST: split rows from per-chunk partials. */
+int tg_spmm_plan_set_precision(tg_spmm_plan_t plan, int precision);
+/* One-shot form: builds a plan, executes, frees it (allocates; synchronises).
+ * tg_spmm is tg_spmm_ex with TG_PRECISION_EXACT (bit-identical). */
+int tg_spmm_ex(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+               const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
+               float* c, int64_t ldc, int precision, tg_stream_t stream);
 int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
             const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
             float* c, int64_t ldc, tg_stream_t stream);
@@ -218,7 +238,8 @@ int tg_edge_softmax(int64_t n_rows, const int32_t* row_ptr, const float* val,
  *   TG_SAGE_AUTO takes transform-first for the mean aggregator when
  *     f_out < f_in and nnz * f_in >= 2^26, else concat.
  * With concat and the in-order GEMM (small products) the result is
- * bit-identical to the reference for rows of at most one plan chunk.
+ * bit-identical to the reference (every row under a plan of
+ * TG_PRECISION_EXACT, the default; rows of at most one chunk under FAST).
  * `nnz` of the workspace query is the adjacency's nonzero count.
  * ------------------------------------------------------------------------ */
 enum { TG_SAGE_AUTO = 0, TG_SAGE_CONCAT = 1, TG_SAGE_TRANSFORM_FIRST = 2 };
@@ -321,7 +342,6 @@ int tg_model_set_sage_dataflow(tg_model_t model, int dataflow);
  *     evaluated in double and rounded.  GCN and SAGE outputs are
  *     bit-identical to the reference; GAT differs only where the reference's
  *     libm expf is not correctly rounded. */
-enum { TG_PRECISION_FAST = 0, TG_PRECISION_EXACT = 1 };
 int tg_model_set_precision(tg_model_t model, int precision);
 /* Column blocking of the model's GCN, SAGE-mean and GAT aggregations
  * (both forward modes; GAT layers with concatenated or single heads of

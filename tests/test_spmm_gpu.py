@@ -1,8 +1,15 @@
 """CSR SpMM on the GPU vs the oracle (reference src/ops.cpp:198-297).
 
-Bar: rows processed as one chunk (<= chunk_nnz nonzeros) are bit-identical
-to the reference's fma chain; split rows (regrouped sum) and the whole
-output are within |got-want| <= 1e-5 + 1e-4*|want|.
+Bar, default plans (TG_PRECISION_EXACT): every row, rows longer than the
+plan's chunk included, is bit-identical to the reference's fma chain.
+
+Bar, TG_PRECISION_FAST plans: rows of at most one chunk (<= chunk_nnz
+nonzeros) are bit-identical; rows split into chunks (a regrouped sum of
+per-chunk partials) are held to the fp32 summation error bound
+n 2^-24 sum|terms| around the float64 product, the bound the reference's own
+sequential sum obeys.  (The two sums can differ by more than
+1e-5 + 1e-4 |want| where a long row cancels; the exact plans are the
+reference-order path.)
 """
 import numpy as np
 import pytest
@@ -12,12 +19,17 @@ from helpers import bits, random_csr
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, a, b, chunk=0, plan=True):
+def _run(gpu, a, b, chunk=0, plan=True, precision=None):
     import tinygnn_amd as tg
     da = tg.DeviceCSR.from_numpy(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, a.val)
     db = gpu.from_numpy(b).cuda()
     p = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, b.shape[1], chunk) if plan else None
-    out = tg.spmm(da, db, plan=p)
+    if p is not None and precision is not None:
+        p.set_precision(precision)
+    if p is None and precision is not None:
+        out = tg.spmm(da, db, precision=precision)
+    else:
+        out = tg.spmm(da, db, plan=p)
     gpu.cuda.synchronize()
     info = p.info() if p else None
     return out.cpu().numpy(), info
@@ -35,13 +47,53 @@ def test_spmm_widths_bitexact(gpu, restate, f):
 
 
 @pytest.mark.parametrize("chunk", [1, 7, 64, 256])
-@pytest.mark.parametrize("f", [4, 41, 128, 512])
-def test_spmm_split_rows(gpu, restate, f, chunk):
-    rng = np.random.default_rng(7 * f + chunk)
+@pytest.mark.parametrize("f", [2, 3, 4, 41, 128, 512])
+def test_spmm_split_rows_exact(gpu, restate, f, chunk):
+    """Default plans: rows longer than the chunk run one workgroup each
+    (gathers spread over the workgroup, the chain walked in order), so every
+    row is bit-identical.  Widths cover 1-, 2- and 4-float gathers and the
+    32-, 64- and 128-column tiles of that kernel (f = 512: four tiles)."""
+    rng = np.random.default_rng(7 * f + chunk + 1)
     a = random_csr(rng, 400, 300, avg_deg=20, max_deg=2000, empty_frac=0.1)
     b = rng.standard_normal((300, f)).astype(np.float32)
     want = restate.spmm(a, b)
     got, info = _run(gpu, a, b, chunk=chunk)
+    deg = np.diff(a.row_ptr)
+    assert info["n_split_rows"] == int((deg > chunk).sum())
+    np.testing.assert_array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("f", [1, 32, 41, 128, 300])
+def test_spmm_long_rows_exact(gpu, restate, f):
+    """Rows of 1,025 to 30,000 nonzeros (many LDS batches, odd and even
+    batch counts, a partial last batch) under the default 1,024-entry chunk,
+    against the reference's chain; empty and short rows around them."""
+    import oracle
+    rng = np.random.default_rng(900 + f)
+    n_cols = 4000
+    deg = np.concatenate([rng.integers(1025, 30001, 12), [1025, 1088, 2048, 8192 + 1],
+                          rng.integers(0, 50, 200)]).astype(np.int64)
+    rng.shuffle(deg)
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = np.concatenate([np.sort(rng.integers(0, n_cols, d)) for d in deg]).astype(np.int32)
+    val = (1.0 - rng.random(int(rp[-1]))).astype(np.float32)
+    a = oracle.CSR(len(deg), n_cols, rp, ci, val)
+    b = rng.standard_normal((n_cols, f)).astype(np.float32)
+    got, info = _run(gpu, a, b)
+    assert info["n_split_rows"] == int((deg > 1024).sum())
+    np.testing.assert_array_equal(bits(got), bits(restate.spmm(a, b)))
+
+
+@pytest.mark.parametrize("chunk", [1, 7, 64, 256])
+@pytest.mark.parametrize("f", [4, 41, 128, 512])
+def test_spmm_split_rows(gpu, restate, f, chunk):
+    """TG_PRECISION_FAST plans: split rows summed from per-chunk partials."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(7 * f + chunk)
+    a = random_csr(rng, 400, 300, avg_deg=20, max_deg=2000, empty_frac=0.1)
+    b = rng.standard_normal((300, f)).astype(np.float32)
+    want = restate.spmm(a, b)
+    got, info = _run(gpu, a, b, chunk=chunk, precision=tg.PRECISION_FAST)
     deg = np.diff(a.row_ptr)
     single = deg <= chunk
     np.testing.assert_array_equal(bits(got[single]), bits(want[single]))
@@ -83,20 +135,30 @@ def test_spmm_padded_rows(gpu, restate, f, pad, chunk):
     bp[:, :f] = b
     da = tg.DeviceCSR.from_numpy(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, a.val)
     dbp = gpu.from_numpy(bp).cuda()
-    p = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, f, chunk)
-    got = tg.spmm(da, dbp[:, :f], plan=p).cpu().numpy()
     want = restate.spmm(a, b)
     deg = np.diff(a.row_ptr)
     single = deg <= chunk
-    assert np.isfinite(got).all()
-    np.testing.assert_array_equal(bits(got[single]), bits(want[single]))
-    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+    for precision in (tg.PRECISION_EXACT, tg.PRECISION_FAST):
+        p = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, f, chunk, precision=precision)
+        got = tg.spmm(da, dbp[:, :f], plan=p).cpu().numpy()
+        assert np.isfinite(got).all()
+        if precision == tg.PRECISION_EXACT:
+            np.testing.assert_array_equal(bits(got), bits(want))
+        else:
+            np.testing.assert_array_equal(bits(got[single]), bits(want[single]))
+            np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
 
 
 def test_spmm_one_shot_and_empty(gpu, restate):
     rng = np.random.default_rng(3)
     a = random_csr(rng, 300, 200, avg_deg=5, empty_frac=0.3)
     b = rng.standard_normal((200, 24)).astype(np.float32)
+    got, _ = _run(gpu, a, b, plan=False)
+    np.testing.assert_array_equal(bits(got), bits(restate.spmm(a, b)))
+    # the one-shot form with long rows: exact by default
+    a = random_csr(rng, 200, 300, avg_deg=40, max_deg=3000, empty_frac=0.1)
+    b = rng.standard_normal((300, 24)).astype(np.float32)
+    assert np.diff(a.row_ptr).max() > 1024
     got, _ = _run(gpu, a, b, plan=False)
     np.testing.assert_array_equal(bits(got), bits(restate.spmm(a, b)))
     import oracle

@@ -81,13 +81,21 @@ class SpmmPlan:
     """Degree-binned row schedule of one CSR structure (tg_spmm_plan_*)."""
 
     def __init__(self, row_ptr, n_rows: int, nnz_bound: int, max_f: int, chunk_nnz: int = 0,
-                 stream=None):
+                 stream=None, precision: int = PRECISION_EXACT):
         h = C.c_void_p()
         lib.check(lib.tg_spmm_plan_create(n_rows, nnz_bound, dptr(row_ptr), max_f, chunk_nnz,
                                           stream_handle(stream), C.byref(h)))
         self.h = h
         self.row_ptr = row_ptr
         self.n_rows = n_rows
+        if precision != PRECISION_EXACT:
+            self.set_precision(precision)
+
+    def set_precision(self, precision: int) -> None:
+        """PRECISION_EXACT: every row one fma chain in nonzero order (the
+        reference's order, bit-identical output); PRECISION_FAST: rows longer
+        than the chunk summed from per-chunk partials."""
+        lib.check(lib.tg_spmm_plan_set_precision(self.h, precision))
 
     @property
     def handle(self):
@@ -118,8 +126,13 @@ def _check_spmm_shapes(a: DeviceCSR, b):
                                  f"Required: A.cols() == B.rows() ({a.n_cols} vs {b.shape[0]}).")
 
 
-def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None):
-    """C = A * B (reference ops.cpp:198-297)."""
+def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None,
+         precision: int = PRECISION_EXACT):
+    """C = A * B (reference ops.cpp:198-297).  With a plan, the plan's
+    precision applies; without one, `precision`: PRECISION_EXACT (the
+    default) is the reference's summation order, bit-identical;
+    PRECISION_FAST sums rows longer than 1,024 nonzeros from per-chunk
+    partials."""
     torch = _torch()
     _check_spmm_shapes(a, b)
     f = b.shape[1]
@@ -127,8 +140,9 @@ def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None):
         out = torch.empty((a.n_rows, f), dtype=torch.float32, device=b.device)
     s = stream_handle(stream)
     if plan is None:
-        lib.check(lib.tg_spmm(a.n_rows, a.n_cols, f, a.nnz, dptr(a.row_ptr), dptr(a.col_ind),
-                              dptr(a.val), dptr(b), b.stride(0), dptr(out), out.stride(0), s))
+        lib.check(lib.tg_spmm_ex(a.n_rows, a.n_cols, f, a.nnz, dptr(a.row_ptr), dptr(a.col_ind),
+                                 dptr(a.val), dptr(b), b.stride(0), dptr(out), out.stride(0),
+                                 precision, s))
     else:
         lib.check(lib.tg_spmm_execute(plan.h, a.n_cols, f, dptr(a.row_ptr), dptr(a.col_ind),
                                       dptr(a.val), dptr(b), b.stride(0), dptr(out),

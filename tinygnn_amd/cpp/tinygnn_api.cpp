@@ -451,7 +451,9 @@ Tensor matmul(const Tensor& A, const Tensor& B) {
     return C;
 }
 
-Tensor spmm(const Tensor& A, const Tensor& B) {
+Tensor spmm(const Tensor& A, const Tensor& B) { return spmm(A, B, SpmmOrder::Exact); }
+
+Tensor spmm(const Tensor& A, const Tensor& B, SpmmOrder order) {
     // ops.cpp:200-236
     if (A.format() != StorageFormat::SparseCSR)
         throw std::invalid_argument(
@@ -471,6 +473,8 @@ Tensor spmm(const Tensor& A, const Tensor& B) {
     if (A.rows() == 0 || B.cols() == 0 || A.nnz() == 0) return Tensor::dense(A.rows(), B.cols());
     Tensor C = Tensor::device_dense(A.rows(), B.cols());
     tg_spmm_plan_t plan = detail::plan_for(A, i64(B.cols()));
+    check(tg_spmm_plan_set_precision(
+        plan, order == SpmmOrder::Exact ? TG_PRECISION_EXACT : TG_PRECISION_FAST));
     check(tg_spmm_execute(plan, i64(A.cols()), i64(B.cols()), A.device_row_ptr(),
                           A.device_col_ind(), A.device_data(), B.device_data(), i64(B.cols()),
                           C.device_data_mutable(), i64(B.cols()), nullptr));

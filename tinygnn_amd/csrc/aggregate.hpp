@@ -43,6 +43,10 @@ struct AggEpilogue {
     // batch gathers nothing for the slots past its end (worth it for the
     // fast blocked passes' chunks, not for long unsplit ones)
     int mask_tail = 0;
+    // rows of more than one plan chunk ("split rows") summed as one chain in
+    // nonzero order, one workgroup per row (agg_long_kernel), instead of from
+    // per-chunk partials: every row then sums in the reference's order
+    int long_rows = 0;
     // B's layout (tile_cols = 32 only): > 0 = tile-major, 32-column tile t
     // of row j at B + t * b_tile_stride + j * ldb (ldb = 32); 0 = row-major
     int64_t b_tile_stride = 0;

@@ -360,6 +360,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     if (m.need_raw()) {
         if (!m.plan_raw) m.plan_raw = std::make_unique<tg_spmm_plan_s>();
         build_plan(*m.plan_raw, n, nnz, rp, maxf, chunk, s);
+        m.plan_raw->precision = m.precision;
     } else {
         m.plan_raw.reset();
     }

@@ -54,10 +54,12 @@ void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* 
     AggEpilogue epi;
     epi.mean = agg == TG_AGG_MEAN;
     epi.max = agg == TG_AGG_MAX;
-    if (blocked && agg == TG_AGG_MEAN)
+    if (blocked && agg == TG_AGG_MEAN) {
         run_aggregate_blocked(*blocked, f, h, ldh, out, ldo, epi, s);
-    else
+    } else {
+        epi.long_rows = p.precision == TG_PRECISION_EXACT;  // split rows as in-order chains
         run_aggregate(p, f, ci, nullptr, h, ldh, out, ldo, epi, s);
+    }
 }
 
 size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
@@ -181,6 +183,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         } else if (blocked) {
             run_aggregate_blocked(*blocked, f_out, t + fp, 2 * fp, out, f_out, epi, s);
         } else {
+            epi.long_rows = p.precision == TG_PRECISION_EXACT;
             run_aggregate(p, f_out, ci, nullptr, t + fp, 2 * fp, out, f_out, epi, s);
         }
     }

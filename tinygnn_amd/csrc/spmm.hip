@@ -35,13 +35,15 @@ __device__ __forceinline__ int chunk_bin(int len) {
     return b < kPlanBins ? b : kPlanBins - 1;
 }
 
+// bin_count holds 2 x kPlanBins counters: the chunks' length bins, then the
+// split rows' degree bins (split rows are listed longest first too).
 __global__ __launch_bounds__(256) void plan_count_kernel(const int32_t* __restrict__ row_ptr,
                                                          int64_t m, int chunk,
                                                          int32_t* __restrict__ split_cnt,
                                                          int32_t* __restrict__ is_split,
                                                          int32_t* __restrict__ bin_count) {
-    __shared__ int32_t hist[kPlanBins];
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __shared__ int32_t hist[2 * kPlanBins];
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (r < m) {
@@ -55,10 +57,11 @@ __global__ __launch_bounds__(256) void plan_count_kernel(const int32_t* __restri
             const int full = deg / chunk, rem = deg - full * chunk;
             atomicAdd(&hist[chunk_bin(chunk)], full);
             if (rem) atomicAdd(&hist[chunk_bin(rem)], 1);
+            atomicAdd(&hist[kPlanBins + chunk_bin(deg)], 1);
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x)
         if (hist[i]) atomicAdd(&bin_count[i], hist[i]);
 }
 
@@ -78,6 +81,11 @@ __global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
             bin_cursor[b] = static_cast<int32_t>(acc);
             acc += bin_count[b];
         }
+        int64_t sacc = 0;  // split rows, longest degree bin first
+        for (int b = kPlanBins - 1; b >= 0; --b) {
+            bin_cursor[kPlanBins + b] = static_cast<int32_t>(sacc);
+            sacc += bin_count[kPlanBins + b];
+        }
         const int64_t n_split = split_pos[m], n_part = slot_base[m];
         const bool over = acc > cap_chunks || n_split > cap_split || n_part > cap_partials;
         totals[0] = over ? 0 : acc;      // chunks
@@ -93,15 +101,14 @@ __global__ void plan_bins_kernel(const int32_t* __restrict__ bin_count,
 // ranges.
 __global__ __launch_bounds__(256) void plan_scatter_kernel(
     const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
-    const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
-    int32_t* __restrict__ bin_cursor, int4* __restrict__ chunks, int4* __restrict__ split,
-    int64_t cap_chunks, int64_t cap_split) {
-    __shared__ int hist[kPlanBins], gbase[kPlanBins];
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    const int32_t* __restrict__ slot_base, int32_t* __restrict__ bin_cursor,
+    int4* __restrict__ chunks, int4* __restrict__ split, int64_t cap_chunks, int64_t cap_split) {
+    __shared__ int hist[2 * kPlanBins], gbase[2 * kPlanBins];
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     int b = 0, e = 0, deg = 0, full = 0, rem = 0;
-    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0;
+    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0, bin_s = 0, pos_s = 0;
     if (r < m) {
         b = row_ptr[r];
         e = row_ptr[r + 1];
@@ -119,10 +126,12 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
                 bin_r = chunk_bin(rem);
                 pos_r = atomicAdd(&hist[bin_r], 1);
             }
+            bin_s = kPlanBins + chunk_bin(deg);
+            pos_s = atomicAdd(&hist[bin_s], 1);
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x)
         if (hist[i] > 0) gbase[i] = atomicAdd(&bin_cursor[i], hist[i]);
     __syncthreads();
     if (r >= m) return;
@@ -144,8 +153,9 @@ __global__ __launch_bounds__(256) void plan_scatter_kernel(
         const int64_t at = static_cast<int64_t>(gbase[bin_r]) + pos_r;
         if (at < cap_chunks) chunks[at] = make_int4(row, b + full * chunk, e, slot0 + full);
     }
-    if (split_pos[r] < cap_split)
-        split[split_pos[r]] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
+    // split rows in degree bins, longest first (agg_long_kernel's order)
+    const int64_t at = static_cast<int64_t>(gbase[bin_s]) + pos_s;
+    if (at < cap_split) split[at] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
 }
 
 }  // namespace
@@ -154,7 +164,7 @@ namespace {
 
 // The plan build's temporaries, carved from the plan's scratch in the same
 // layout by both phases: split_cnt[m], is_split[m], slot_base[m+1],
-// split_pos[m+1], bin_count[64], bin_cursor[64], totals[4], scan temp.
+// split_pos[m+1], bin_count[128], bin_cursor[128], totals[4], scan temp.
 struct PlanTemps {
     int32_t *split_cnt, *is_split, *slot_base, *split_pos, *bin_count, *bin_cursor;
     int64_t *totals, *scan_tmp;
@@ -166,8 +176,8 @@ PlanTemps carve_temps(Carver& c, int64_t m) {
     t.is_split = c.take<int32_t>(m);
     t.slot_base = c.take<int32_t>(m + 1);
     t.split_pos = c.take<int32_t>(m + 1);
-    t.bin_count = c.take<int32_t>(kPlanBins);
-    t.bin_cursor = c.take<int32_t>(kPlanBins);
+    t.bin_count = c.take<int32_t>(2 * kPlanBins);  // chunk bins, then split-row bins
+    t.bin_cursor = c.take<int32_t>(2 * kPlanBins);
     t.totals = c.take<int64_t>(4);
     t.scan_tmp = c.take<int64_t>(scan_temp_elems(m));
     return t;
@@ -203,7 +213,7 @@ void build_plan_count(tg_spmm_plan_s& p, int64_t m, int64_t nnz_bound, const int
     if (m == 0) return;
     require(row_ptr != nullptr, "spmm plan: row_ptr is null");
     const PlanTemps t = carve_plan_temps(p, m);
-    fill_i32(t.bin_count, kPlanBins, 0, s);
+    fill_i32(t.bin_count, 2 * kPlanBins, 0, s);
     const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
     plan_count_kernel<<<nblk, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk), t.split_cnt,
                                            t.is_split, t.bin_count);
@@ -231,7 +241,7 @@ void build_plan_finish(tg_spmm_plan_s& p, const int64_t* host_totals, hipStream_
                            static_cast<size_t>(round_up(p.max_f, 4)) * sizeof(float));
     const unsigned nblk = static_cast<unsigned>(ceil_div(p.m, 256));
     plan_scatter_kernel<<<nblk, 256, 0, s>>>(p.row_ptr, p.m, static_cast<int>(p.chunk),
-                                             t.slot_base, t.split_pos, t.bin_cursor,
+                                             t.slot_base, t.bin_cursor,
                                              p.chunks.as<int4>(), p.split.as<int4>(),
                                              p.n_chunks, p.n_split);
     TG_LAUNCH_CHECK();
@@ -257,8 +267,8 @@ namespace {
 __global__ __launch_bounds__(256) void plan_count_multi_kernel(
     const int32_t* __restrict__ row_ptr, int64_t m, int chunk, int32_t* __restrict__ split_cnt,
     int32_t* __restrict__ is_split, int32_t* __restrict__ bin_count) {
-    __shared__ int32_t hist[kPlanBins];
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    __shared__ int32_t hist[2 * kPlanBins];
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (r < m) {
@@ -273,11 +283,12 @@ __global__ __launch_bounds__(256) void plan_count_multi_kernel(
             const int full = deg / chunk, rem = deg - full * chunk;
             atomicAdd(&hist[chunk_bin(chunk)], full);
             if (rem) atomicAdd(&hist[chunk_bin(rem)], 1);
+            atomicAdd(&hist[kPlanBins + chunk_bin(deg)], 1);
         }
     }
     __syncthreads();
-    int32_t* bc = bin_count + static_cast<int64_t>(blockIdx.y) * kPlanBins;
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+    int32_t* bc = bin_count + static_cast<int64_t>(blockIdx.y) * 2 * kPlanBins;
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x)
         if (hist[i]) atomicAdd(&bc[i], hist[i]);
 }
 
@@ -290,10 +301,14 @@ __global__ void plan_bins_multi_kernel(const int32_t* __restrict__ bin_count,
                                        int nplans, int64_t* __restrict__ totals) {
     const int b = threadIdx.x;
     if (b >= nplans) return;
-    int64_t acc = 0;
+    const int32_t* bc = bin_count + b * 2 * kPlanBins;
+    int32_t* cur = bin_cursor + b * 2 * kPlanBins;
+    int64_t acc = 0, sacc = 0;
     for (int k = kPlanBins - 1; k >= 0; --k) {
-        bin_cursor[b * kPlanBins + k] = static_cast<int32_t>(acc);
-        acc += bin_count[b * kPlanBins + k];
+        cur[k] = static_cast<int32_t>(acc);
+        acc += bc[k];
+        cur[kPlanBins + k] = static_cast<int32_t>(sacc);  // split rows, longest first
+        sacc += bc[kPlanBins + k];
     }
     const int64_t lo = static_cast<int64_t>(b) * m, hi = lo + m;
     totals[4 * b + 0] = acc;
@@ -309,15 +324,14 @@ struct MultiPlanOut {
 
 __global__ __launch_bounds__(256) void plan_scatter_multi_kernel(
     const int32_t* __restrict__ row_ptr, int64_t m, int chunk,
-    const int32_t* __restrict__ slot_base, const int32_t* __restrict__ split_pos,
-    int32_t* __restrict__ bin_cursor, MultiPlanOut out) {
-    __shared__ int hist[kPlanBins], gbase[kPlanBins];
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x) hist[i] = 0;
+    const int32_t* __restrict__ slot_base, int32_t* __restrict__ bin_cursor, MultiPlanOut out) {
+    __shared__ int hist[2 * kPlanBins], gbase[2 * kPlanBins];
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x) hist[i] = 0;
     __syncthreads();
     const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t lo = static_cast<int64_t>(blockIdx.y) * m;
     int b = 0, e = 0, deg = 0, full = 0, rem = 0;
-    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0;
+    int bin_f = 0, pos_f = 0, bin_r = 0, pos_r = 0, bin_s = 0, pos_s = 0;
     if (r < m) {
         b = row_ptr[lo + r];
         e = row_ptr[lo + r + 1];
@@ -335,11 +349,13 @@ __global__ __launch_bounds__(256) void plan_scatter_multi_kernel(
                 bin_r = chunk_bin(rem);
                 pos_r = atomicAdd(&hist[bin_r], 1);
             }
+            bin_s = kPlanBins + chunk_bin(deg);
+            pos_s = atomicAdd(&hist[bin_s], 1);
         }
     }
     __syncthreads();
-    int32_t* cur = bin_cursor + static_cast<int64_t>(blockIdx.y) * kPlanBins;
-    for (int i = threadIdx.x; i < kPlanBins; i += blockDim.x)
+    int32_t* cur = bin_cursor + static_cast<int64_t>(blockIdx.y) * 2 * kPlanBins;
+    for (int i = threadIdx.x; i < 2 * kPlanBins; i += blockDim.x)
         if (hist[i] > 0) gbase[i] = atomicAdd(&cur[i], hist[i]);
     __syncthreads();
     if (r >= m) return;
@@ -356,8 +372,8 @@ __global__ __launch_bounds__(256) void plan_scatter_multi_kernel(
         chunks[gbase[bin_f] + pos_f + c] = make_int4(row, cb, cb + chunk, slot0 + c);
     }
     if (rem) chunks[gbase[bin_r] + pos_r] = make_int4(row, b + full * chunk, e, slot0 + full);
-    out.split[blockIdx.y][split_pos[lo + r] - split_pos[lo]] =
-        make_int4(row, slot0, full + (rem ? 1 : 0), deg);
+    // split rows in degree bins, longest first (agg_long_kernel's order)
+    out.split[blockIdx.y][gbase[bin_s] + pos_s] = make_int4(row, slot0, full + (rem ? 1 : 0), deg);
 }
 
 struct MultiTemps {
@@ -371,8 +387,8 @@ MultiTemps carve_multi(Carver& c, int64_t rows, int nplans) {
     t.is_split = c.take<int32_t>(rows);
     t.slot_base = c.take<int32_t>(rows + 1);
     t.split_pos = c.take<int32_t>(rows + 1);
-    t.bin_count = c.take<int32_t>(static_cast<int64_t>(nplans) * kPlanBins);
-    t.bin_cursor = c.take<int32_t>(static_cast<int64_t>(nplans) * kPlanBins);
+    t.bin_count = c.take<int32_t>(static_cast<int64_t>(nplans) * 2 * kPlanBins);
+    t.bin_cursor = c.take<int32_t>(static_cast<int64_t>(nplans) * 2 * kPlanBins);
     t.totals = c.take<int64_t>(4 * static_cast<int64_t>(nplans));
     t.scan_tmp = c.take<int64_t>(scan_temp_elems(rows));
     return t;
@@ -397,7 +413,7 @@ void build_plans_multi(tg_spmm_plan_s* const* plans, int nplans, int64_t m,
     scratch.reserve(cv.bytes());
     Carver c(scratch.get(), scratch.size());
     const MultiTemps t = carve_multi(c, rows, nplans);
-    fill_i32(t.bin_count, static_cast<int64_t>(nplans) * kPlanBins, 0, s);
+    fill_i32(t.bin_count, static_cast<int64_t>(nplans) * 2 * kPlanBins, 0, s);
     const dim3 grid(static_cast<unsigned>(ceil_div(m, 256)), static_cast<unsigned>(nplans));
     plan_count_multi_kernel<<<grid, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk),
                                                  t.split_cnt, t.is_split, t.bin_count);
@@ -433,7 +449,7 @@ void build_plans_multi(tg_spmm_plan_s* const* plans, int nplans, int64_t m,
         out.split[b] = p.split.as<int4>();
     }
     plan_scatter_multi_kernel<<<grid, 256, 0, s>>>(row_ptr, m, static_cast<int>(chunk),
-                                                   t.slot_base, t.split_pos, t.bin_cursor, out);
+                                                   t.slot_base, t.bin_cursor, out);
     TG_LAUNCH_CHECK();
 }
 
@@ -667,6 +683,7 @@ __global__ __launch_bounds__(256, 4) void agg_chunk_kernel(
     if (cid >= (n_chunks_dev ? *n_chunks_dev : n_chunks)) return;
     const int4 ch = chunks[cid];
     if (epi.skip_empty && ch.z == ch.y) return;  // the row keeps its value in C
+    if (epi.long_rows && ch.w >= 0) return;      // a split row: agg_long_kernel's
     const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TILE;
     // attention weights: the row's score, max and 1/sum for the tile's head
     // (every tile lies in one head's columns); dst scores of that head
@@ -1011,6 +1028,7 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
     bool active = cid < nch;
     if (active) ch = chunks[cid];
     if (active && epi.skip_empty && ch.z == ch.y) active = false;
+    if (active && epi.long_rows && ch.w >= 0) active = false;  // agg_long_kernel's row
     if (!active) ch = make_int4(0, 0, 0, -1);
     if (__builtin_amdgcn_readfirstlane(__ballot(active) == 0 ? 1 : 0)) return;
 
@@ -1140,6 +1158,214 @@ __global__ __launch_bounds__(256) void agg_reduce_kernel(const int4* __restrict_
     }
 }
 
+// Column tile of the long-row kernel: the lane groups' tile when they are
+// given (column-blocked passes), else 32, 64 or 128 columns by f.
+inline int long_tile(int64_t f, const LaneLayout& L) {
+    if (L.tile == 32 || L.tile == 64 || L.tile == 128) {
+        if (L.n_tiles > 1 || L.tile >= f) return L.tile;
+    }
+    return f <= 32 ? 32 : f <= 64 ? 64 : 128;
+}
+
+// Rows of more than one chunk summed as ONE chain each, in nonzero order:
+// acc = combine(acc, B[col_e, j], w_e) for e along the row, exactly the
+// reference's loop (ops.cpp:266-287 for SpMM).  One workgroup takes one
+// (row, TW-column tile).  A chain is serial, so what bounds a long row is
+// how many of its gathers are in flight; here all 256 threads issue them:
+// G = TW / VEC lanes fetch one entry's tile row, 256 / G entries per round,
+// U rounds per batch (32 floats in flight per thread), BE = 8192 / TW
+// entries per batch, landing in LDS.  Threads [0, TW) then walk the batch
+// in order, one column each, while the next two batches' gathers are in
+// flight (two register sets, two 32 KB LDS buffers, one barrier per
+// batch).  The row's column indices go through LDS (one coalesced load per
+// entry), its weights likewise.  Split rows come longest first, so the
+// longest chains start first.
+template <int VEC, int TW, int MODE>
+__global__ __launch_bounds__(256, 2) void agg_long_kernel(
+    const int4* __restrict__ split, int64_t n_split, const int64_t* __restrict__ n_split_dev,
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ ci,
+    const float* __restrict__ av, const float* __restrict__ B, int64_t ldb,
+    float* __restrict__ C, int64_t ldc, int64_t f, AggEpilogue epi) {
+    static_assert(MODE == kAggWeighted || MODE == kAggSum || MODE == kAggSumTail ||
+                      MODE == kAggMax,
+                  "long rows: weighted, sum or max");
+    static_assert(TW == 32 || TW == 64 || TW == 128, "tile width");
+    constexpr int G = TW / VEC;   // lanes per gathered entry
+    constexpr int R = 256 / G;    // entries per round
+    constexpr int U = 32 / VEC;   // rounds per batch
+    constexpr int BE = U * R;     // entries per batch
+    static_assert(BE * TW == 8192 && BE <= 256, "batch shape");
+    __shared__ __align__(16) float dbuf[2][BE * TW];
+    __shared__ float wbuf[2][BE];
+    __shared__ int cbuf[2][BE];
+
+    const int64_t sid = blockIdx.x;
+    if (sid >= (n_split_dev ? *n_split_dev : n_split)) return;  // uniform
+    const int4 sp = split[sid];
+    const int row = sp.x;
+    const int rb = row_ptr[row];
+    const int re = rb + sp.w;
+    const int nb = (sp.w + BE - 1) / BE;
+    const int tid = threadIdx.x;
+    const int q = tid / G, p = tid % G;
+    const int64_t fbase = static_cast<int64_t>(blockIdx.y) * TW;
+    const int64_t fo = fbase + static_cast<int64_t>(p) * VEC;
+    // lanes past f load the tile's first vector (in bounds), never used
+    const int64_t fl = fo < f ? fo : fbase;
+    const char* bl = reinterpret_cast<const char*>(
+        epi.b_tile_stride > 0 ? B + (fl >> 5) * epi.b_tile_stride + (fl & 31) : B + fl);
+    const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
+
+    // Entry tid of batch t (its index clamped into the row, so every load is
+    // in bounds and unconditional: the slots past the row's end fetch a real
+    // entry whose value is never used, and no load needs a default value, so
+    // no wait on earlier loads is forced).  Only threads below BE store them.
+    const bool c16 = epi.ci16 != nullptr;
+    auto entry = [&](int t) {
+        const int64_t idx = static_cast<int64_t>(rb) + static_cast<int64_t>(t) * BE + tid;
+        return idx < re ? static_cast<int>(idx) : re - 1;
+    };
+    auto col_of = [&](int t) -> int {
+        const int idx = entry(t);
+        return c16 ? static_cast<int>(epi.ci16[idx]) : ci[idx];
+    };
+    auto w_of = [&](int t) -> float {
+        if constexpr (MODE == kAggWeighted) return av[entry(t)];
+        return 1.0f;
+    };
+    // two register sets: the gathers of batches t + 1 and t + 2 are in flight
+    // while batch t's chains run
+    float g0[U][VEC], g1[U][VEC];
+    // gathers of batch t (columns from cbuf[t & 1]) into g: every slot,
+    // those past the row's end included (their columns are real ones); a
+    // batch past the row's last (the steps run in pairs) loads row 0 only
+    auto issue = [&](int t, float (&g)[U][VEC]) {
+        const uint32_t pm = t < nb ? pitch : 0u;
+        int col[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) col[u] = cbuf[t & 1][u * R + q];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col[u])) * pm;
+            load_vec<VEC>(reinterpret_cast<const float*>(bl + off), g[u]);
+        }
+    };
+    auto land = [&](int t, const float (&g)[U][VEC]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) store_vec<VEC>(&dbuf[t & 1][(u * R + q) * TW + p * VEC], g[u]);
+    };
+
+    // chain lane: column fj of the tile; a blocked pass after the first
+    // continues the row's chain from the value the earlier passes stored
+    const int64_t fj = fbase + tid;
+    const bool chain_lane = tid < TW;
+    float acc = MODE == kAggMax ? -INFINITY : 0.0f;
+    if (epi.acc && chain_lane && fj < f) acc = C[static_cast<int64_t>(row) * ldc + fj];
+    auto walk = [&](int t) {
+        if (!chain_lane) return;
+        const float* d = &dbuf[t & 1][tid];
+        const float* w = wbuf[t & 1];
+        const int cnt = re - rb - t * BE;
+        if (cnt >= BE) {
+            // a full batch, unrolled: the LDS reads are scheduled ahead of
+            // the chain's fmas
+#pragma unroll
+            for (int e = 0; e < BE; ++e) acc = combine<MODE>(acc, d[e * TW], w[e]);
+        } else {
+            int e = 0;
+            for (; e + 8 <= cnt; e += 8) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc = combine<MODE>(acc, d[(e + k) * TW], w[e + k]);
+            }
+            for (; e < cnt; ++e) acc = combine<MODE>(acc, d[e * TW], w[e]);
+        }
+    };
+
+    // Batch x's columns sit in cbuf[x & 1] until its gathers are issued, its
+    // weights in wbuf[x & 1] and its rows in dbuf[x & 1] while it is walked.
+    // Step t (after a barrier: batch t landed, batch t + 1 in flight in the
+    // other register set, batch t + 2's columns in cbuf): issue batch t + 2,
+    // walk batch t, land batch t + 1 with its weights, store batch t + 3's
+    // columns, barrier.
+    const bool meta = tid < BE;  // threads that store columns and weights
+    {
+        const int c0 = col_of(0);
+        const float w0 = w_of(0);
+        const int c1 = col_of(1);
+        if (meta) {
+            cbuf[0][tid] = c0;
+            wbuf[0][tid] = w0;
+            cbuf[1][tid] = c1;
+        }
+    }
+    __syncthreads();
+    // weights of the batches in flight, one register per set like the
+    // gathers (a copy between registers would wait for the load); in a
+    // step the next columns and weights are loaded before the gathers, so
+    // storing them waits for those loads only, not for the gathers
+    float wa = 0.0f;
+    float wb = w_of(1);
+    issue(0, g0);
+    issue(1, g1);
+    const int c2 = col_of(2);
+    __syncthreads();  // cbuf[0] read by every issue(0)
+    land(0, g0);
+    if (meta) cbuf[0][tid] = c2;
+    __syncthreads();
+    auto step = [&](int t, float (&gnext)[U][VEC], float (&gland)[U][VEC], float& wnext,
+                    const float& wland) {
+        // gnext / wnext: the sets free since batch t landed; gland / wland:
+        // batch t + 1's
+        // Every load and store of a step is unconditional, so that the wait
+        // counters see one path: a branch around a register set's loads
+        // would make the compiler wait, at its next use, for every load
+        // issued since -- the gathers in flight included.  Past the row's
+        // end the loads fetch real entries or row 0 (all in bounds), and the
+        // stores rewrite buffers that are not read again.
+        const int c3 = col_of(t + 3);
+        wnext = w_of(t + 2);
+        issue(t + 2, gnext);
+        walk(t);
+        land(t + 1, gland);
+        if (meta) {
+            wbuf[(t + 1) & 1][tid] = wland;
+            cbuf[(t + 1) & 1][tid] = c3;
+        }
+        __syncthreads();
+    };
+    // steps in pairs (the register sets alternate); an odd nb ends with one
+    // step past the row, which walks nothing
+    for (int t = 0; t < nb; t += 2) {
+        step(t, g0, g1, wa, wb);
+        step(t + 1, g1, g0, wb, wa);
+    }
+    if (chain_lane && fj < f) {
+        float x[1] = {acc};
+        finish_store<1>(x, row, sp.w, fj, f, C, ldc, epi, false);
+    }
+}
+
+template <int VEC, int MODE>
+void launch_long(const PlanView& p, int tw, int64_t f, const int32_t* ci, const float* av,
+                 const float* B, int64_t ldb, float* C, int64_t ldc, const AggEpilogue& epi,
+                 hipStream_t s) {
+    require(p.row_ptr != nullptr, "aggregate: long rows need the plan's row pointers");
+    const int64_t* dc = p.dev_counts ? p.dev_counts + 1 : nullptr;
+    const dim3 grid(static_cast<unsigned>(p.n_split), static_cast<unsigned>(ceil_div(f, tw)));
+#define TG_LONG(TW_)                                                                     \
+    if (tw == TW_) {                                                                     \
+        agg_long_kernel<VEC, TW_, MODE><<<grid, 256, 0, s>>>(                            \
+            p.split, p.n_split, dc, p.row_ptr, ci, av, B, ldb, C, ldc, f, epi);          \
+        TG_LAUNCH_CHECK();                                                               \
+        return;                                                                          \
+    }
+    TG_LONG(32)
+    TG_LONG(64)
+    TG_LONG(128)
+#undef TG_LONG
+    throw std::logic_error("aggregate: no long-row kernel for this tile width");
+}
+
 template <int VEC, int LPR, int VPL, int MODE>
 void launch_agg(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t* ci,
                 const float* av, const float* B, int64_t ldb, float* C, int64_t ldc,
@@ -1147,6 +1373,14 @@ void launch_agg(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t
     constexpr int GPB = 256 / LPR;
     const int64_t ldp = round_up(f, VEC);  // padded partial rows
     const int64_t* dc = p.dev_counts;
+    if (epi.long_rows && p.n_split > 0) {
+        // the longest chains first; the chunk kernel then skips their chunks
+        if constexpr (MODE == kAggAttn) {
+            throw std::logic_error("aggregate: long rows do not take attention weights");
+        } else {
+            launch_long<VEC, MODE>(p, long_tile(f, L), f, ci, av, B, ldb, C, ldc, epi, s);
+        }
+    }
     if (p.n_chunks > 0) {
         // grid.y = column tile: the workgroups resident at a time (dispatched
         // in x order) gather from one or two tiles of B
@@ -1156,7 +1390,7 @@ void launch_agg(const PlanView& p, const LaneLayout& L, int64_t f, const int32_t
             p.chunks, p.n_chunks, dc, ci, av, B, ldb, C, ldc, p.partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
-    if (p.n_split > 0) {
+    if (p.n_split > 0 && !epi.long_rows) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_reduce_kernel<VEC, LPR, VPL, MODE><<<grid, 256, 0, s>>>(
@@ -1172,6 +1406,9 @@ void launch_agg_sidx(const PlanView& p, const LaneLayout& L, int64_t f, const fl
     constexpr int GPB = 256 / 8;
     const int64_t ldp = round_up(f, 4);
     const int64_t* dc = p.dev_counts;
+    if (epi.long_rows && p.n_split > 0)
+        launch_long<4, kAggSumTail>(p, long_tile(f, L), f, nullptr, nullptr, B, ldb, C, ldc,
+                                    epi, s);
     if (p.n_chunks > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
@@ -1179,7 +1416,7 @@ void launch_agg_sidx(const PlanView& p, const LaneLayout& L, int64_t f, const fl
                                              p.partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
-    if (p.n_split > 0) {
+    if (p.n_split > 0 && !epi.long_rows) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_split, GPB)),
                   static_cast<unsigned>(L.n_tiles));
         agg_reduce_kernel<4, 8, 1, kAggSumTail><<<grid, 256, 0, s>>>(
@@ -1351,7 +1588,7 @@ void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const in
     const NoAllocPlan P = carve_noalloc(cv, m, nnz, f);
     const int chunk = static_cast<int>(kDefaultChunk);
     const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
-    fill_i32(P.t.bin_count, kPlanBins, 0, s);  // a kernel, so the call stays capturable
+    fill_i32(P.t.bin_count, 2 * kPlanBins, 0, s);  // a kernel, so the call stays capturable
     plan_count_kernel<<<nblk, 256, 0, s>>>(rp, m, chunk, P.t.split_cnt, P.t.is_split,
                                            P.t.bin_count);
     TG_LAUNCH_CHECK();
@@ -1361,9 +1598,8 @@ void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const in
                                       P.t.split_pos, m, P.t.totals, P.cap_chunks, P.cap_split,
                                       P.cap_partials);
     TG_LAUNCH_CHECK();
-    plan_scatter_kernel<<<nblk, 256, 0, s>>>(rp, m, chunk, P.t.slot_base, P.t.split_pos,
-                                             P.t.bin_cursor, P.chunks, P.split, P.cap_chunks,
-                                             P.cap_split);
+    plan_scatter_kernel<<<nblk, 256, 0, s>>>(rp, m, chunk, P.t.slot_base, P.t.bin_cursor,
+                                             P.chunks, P.split, P.cap_chunks, P.cap_split);
     TG_LAUNCH_CHECK();
     PlanView pv;
     pv.m = m;
@@ -1373,8 +1609,10 @@ void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const in
     pv.chunks = P.chunks;
     pv.split = P.split;
     pv.partials = P.partials;
+    pv.row_ptr = rp;
     pv.dev_counts = P.t.totals;  // [0] chunks, [1] split rows
     AggEpilogue epi;
+    epi.long_rows = 1;  // tg_spmm's order: every row one chain in nonzero order
     run_aggregate(pv, f, ci, v, b, ldb, c, ldc, epi, s);
 }
 
@@ -1414,6 +1652,16 @@ int tg_spmm_plan_info(tg_spmm_plan_t plan, int64_t* n_chunks, int64_t* n_split_r
     });
 }
 
+int tg_spmm_plan_set_precision(tg_spmm_plan_t plan, int precision) {
+    return guard([&] {
+        require(plan != nullptr, "tg_spmm_plan_set_precision: plan is null");
+        require(precision == TG_PRECISION_FAST || precision == TG_PRECISION_EXACT,
+                "tg_spmm_plan_set_precision: precision must be TG_PRECISION_FAST or "
+                "TG_PRECISION_EXACT");
+        plan->precision = precision;
+    });
+}
+
 int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f, const int32_t* row_ptr,
                     const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
                     float* c, int64_t ldc, tg_stream_t stream) {
@@ -1424,16 +1672,19 @@ int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f, const int32_t* ro
         require(k >= 0 && f >= 0, "spmm: negative dimension");
         require(val != nullptr, "spmm: val is null");
         tg::AggEpilogue epi;
+        epi.long_rows = plan->precision == TG_PRECISION_EXACT;
         tg::run_aggregate(*plan, f, col_ind, val, b, ldb, c, ldc, epi,
                           static_cast<hipStream_t>(stream));
     });
 }
 
-int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
-            const int32_t* col_ind, const float* val, const float* b, int64_t ldb, float* c,
-            int64_t ldc, tg_stream_t stream) {
+int tg_spmm_ex(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+               const int32_t* col_ind, const float* val, const float* b, int64_t ldb, float* c,
+               int64_t ldc, int precision, tg_stream_t stream) {
     return guard([&] {
         require(m >= 0 && k >= 0 && f >= 0 && nnz >= 0, "spmm: negative dimension");
+        require(precision == TG_PRECISION_FAST || precision == TG_PRECISION_EXACT,
+                "spmm: precision must be TG_PRECISION_FAST or TG_PRECISION_EXACT");
         hipStream_t s = static_cast<hipStream_t>(stream);
         if (m == 0 || f == 0) return;
         if (nnz == 0) {
@@ -1444,9 +1695,17 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
         tg_spmm_plan_s p;
         tg::build_plan(p, m, nnz, row_ptr, f, 0, s);
         tg::AggEpilogue epi;
+        epi.long_rows = precision == TG_PRECISION_EXACT;
         tg::run_aggregate(p, f, col_ind, val, b, ldb, c, ldc, epi, s);
         TG_HIP(hipStreamSynchronize(s));  // the plan's buffers are freed on return
     });
+}
+
+int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
+            const int32_t* col_ind, const float* val, const float* b, int64_t ldb, float* c,
+            int64_t ldc, tg_stream_t stream) {
+    return tg_spmm_ex(m, k, f, nnz, row_ptr, col_ind, val, b, ldb, c, ldc, TG_PRECISION_EXACT,
+                      stream);
 }
 
 int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,

@@ -25,6 +25,10 @@ struct tg_spmm_plan_s {
     int64_t n_split = 0;
     int64_t n_partials = 0;
     int device = 0;
+    // summation order of the plan's executes: TG_PRECISION_EXACT (the
+    // default) sums split rows as single in-order chains, TG_PRECISION_FAST
+    // from per-chunk partials
+    int precision = TG_PRECISION_EXACT;
     const int32_t* row_ptr = nullptr;   // the structure the plan was built for
     tg::DeviceBuffer chunks;            // int4 {row, begin, end, slot (-1 = direct)}
     tg::DeviceBuffer split;             // int4 {row, first slot, n chunks, degree}
@@ -50,6 +54,7 @@ struct PlanView {
     const int4* split = nullptr;
     float* partials = nullptr;
     const int64_t* dev_counts = nullptr;
+    const int32_t* row_ptr = nullptr;  // the structure's row pointers (split rows' starts)
 };
 
 inline PlanView plan_view(const tg_spmm_plan_s& p) {
@@ -61,6 +66,7 @@ inline PlanView plan_view(const tg_spmm_plan_s& p) {
     v.chunks = p.chunks.as<int4>();
     v.split = p.split.as<int4>();
     v.partials = p.partials.as<float>();
+    v.row_ptr = p.row_ptr;
     return v;
 }
 

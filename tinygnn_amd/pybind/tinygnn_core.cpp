@@ -189,7 +189,8 @@ PYBIND11_MODULE(_tinygnn_core, m) {
              "(row_ptr, col_ind, values) device buffer descriptions (CUDA array interface)");
 
     m.def("matmul", &matmul, "C = A x B (Dense)", py::arg("A"), py::arg("B"));
-    m.def("spmm", &spmm, "C = A x B (SparseCSR x Dense)", py::arg("A"), py::arg("B"));
+    m.def("spmm", static_cast<Tensor (*)(const Tensor&, const Tensor&)>(&spmm),
+          "C = A x B (SparseCSR x Dense)", py::arg("A"), py::arg("B"));
     m.def("relu_inplace", &relu_inplace, py::arg("X"));
     m.def("leaky_relu_inplace", &leaky_relu_inplace, py::arg("X"), py::arg("alpha") = 0.01f);
     m.def("elu_inplace", &elu_inplace, py::arg("X"), py::arg("alpha") = 1.0f);
