@@ -470,6 +470,16 @@ int tg_cora_upload(tg_cora_t c, float* features, int32_t* row_ptr, int32_t* col_
                    float* val, tg_stream_t stream);
 int tg_cora_destroy(tg_cora_t c);
 
+/* ------------------------------------------------------------------------
+ * Measurement (no counterpart in the reference): the L2 read ceiling.
+ * Each of `workgroups` 256-thread workgroups reads the whole of `buf`
+ * (`bytes`, a power of two >= 32 KB, 16-byte aligned; a few MB stay in each
+ * XCD's 4 MB L2) with 16-byte loads; sink receives workgroups x 256 floats.
+ * Bytes read = workgroups x bytes.  Asynchronous on `stream`.
+ * ------------------------------------------------------------------------ */
+int tg_probe_l2_read(const void* buf, int64_t bytes, int64_t workgroups, float* sink,
+                     tg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
