@@ -1,7 +1,11 @@
 #!/usr/bin/env python3
 """Writes tests/golden/*.npz from the REAL reference, compiled from its own
-sources by oracle/Makefile into oracle/_ref/libtgref.so (development
-container only; the GPU box receives the fixtures, never the reference).
+sources by oracle/Makefile into oracle/_ref/libtgref.so.  The reference's
+sources exist only in the development container, so the fixtures are
+written there and committed.  The compiled library itself travels to the GPU
+box with the rest of the tree (it is git-ignored, not gpurun-ignored), where
+tests and bench.py load it as a checker and CPU baseline; nothing there
+compiles or reads the reference's sources.
 
 Fixtures (inputs are regenerated from tinygnn_amd.synth by seed; each fixture
 stores the SHA-256 of the inputs it was made from so a drifted generator

@@ -233,8 +233,10 @@ def matmul(a, b, bias=None, epilogue: int = EPI_NONE, algo: int = GEMM_AUTO, out
     """matmul (ops.cpp:70-162) with an optional fused bias + activation."""
     torch = _torch()
     if a.shape[1] != b.shape[0]:
+        # ops.cpp:90-97, the reference's text
         raise InvalidArgument(1, f"matmul: dimension mismatch — A is ({a.shape[0]}×{a.shape[1]})"
-                                 f" but B is ({b.shape[0]}×{b.shape[1]})")
+                                 f" but B is ({b.shape[0]}×{b.shape[1]}). Required: A.cols() == "
+                                 f"B.rows() (both = {a.shape[1]} vs {b.shape[0]}).")
     m, k = a.shape
     n = b.shape[1]
     if out is None:

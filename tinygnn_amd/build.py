@@ -8,6 +8,8 @@
 * ``tinygnn_amd/_build/libtinygnn.so`` -- TinyGNN's C++ API
   (include/tinygnn/*.hpp) over the C-ABI, from ``cpp/*.cpp`` (host code).
 * ``tinygnn_amd/_build/test_cpp_api`` -- the C++ API test (tests/cpp).
+* ``tinygnn_amd/_build/test_throw_sites`` -- every throw statement of the
+  reference driven through the C++ API (tests/cpp/throw_sites.cpp).
 * ``tinygnn_amd/_build/test_numparse`` -- the CSV number conversions checked
   against the host C library (tests/cpp/test_numparse.cpp).
 
@@ -31,6 +33,7 @@ LIB = os.path.join(BUILD, "libtinygnn_amd.so")
 CPP = os.path.join(HERE, "cpp")
 API_LIB = os.path.join(BUILD, "libtinygnn.so")
 CPP_TEST = os.path.join(BUILD, "test_cpp_api")
+THROW_TEST = os.path.join(BUILD, "test_throw_sites")
 NUMPARSE_TEST = os.path.join(BUILD, "test_numparse")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -92,6 +95,10 @@ def _build_cpp_api() -> None:
     _run(host + [test_src, "-o", tmp, f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd",
                  "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, CPP_TEST)
+    tmp = THROW_TEST + ".tmp"
+    _run(host + [os.path.join(ROOT, "tests", "cpp", "throw_sites.cpp"), "-o", tmp,
+                 f"-L{BUILD}", "-ltinygnn", "-ltinygnn_amd", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, THROW_TEST)
     _build_pybind()
     # the CSV number conversions (csrc/numparse.hpp) compiled for the host and
     # checked against the C library in tests/test_numparse.py

@@ -166,7 +166,7 @@ using detail::check;
 // ===========================================================================
 // Tensor (tensor.hpp / tensor.cpp:12-174)
 // ===========================================================================
-Tensor::Tensor() : shape_{0, 0}, strides_{0, 1} {}
+Tensor::Tensor() : shape_{0, 0}, strides_{0, 0} {}  // tensor.cpp:12-15
 
 Tensor::~Tensor() = default;
 
@@ -191,7 +191,7 @@ Tensor::Tensor(Tensor&& o) noexcept
       dev_(std::move(o.dev_)),
       version_(o.version_) {
     o.shape_ = {0, 0};
-    o.strides_ = {0, 1};
+    o.strides_ = {0, 0};
     o.count_ = 0;
     o.host_valid_ = true;
 }
@@ -217,7 +217,7 @@ Tensor& Tensor::operator=(Tensor&& o) noexcept {
         dev_ = std::move(o.dev_);
         ++version_;
         o.shape_ = {0, 0};
-        o.strides_ = {0, 1};
+        o.strides_ = {0, 0};
         o.count_ = 0;
         o.host_valid_ = true;
     }
@@ -231,8 +231,7 @@ Tensor Tensor::dense(std::size_t rows, std::size_t cols) {
 Tensor Tensor::dense(std::size_t rows, std::size_t cols, std::vector<float> data) {
     if (data.size() != rows * cols)
         throw std::invalid_argument("Tensor::dense: data.size() (" + std::to_string(data.size()) +
-                                    ") must equal rows*cols (" + std::to_string(rows * cols) +
-                                    ")");
+                                    ") != rows*cols (" + std::to_string(rows * cols) + ")");
     Tensor t;
     t.format_ = StorageFormat::Dense;
     t.shape_ = {rows, cols};
@@ -440,7 +439,7 @@ Tensor matmul(const Tensor& A, const Tensor& B) {
         throw std::invalid_argument("matmul: dimension mismatch — A is (" +
                                     detail::dims(A.rows(), A.cols()) + ") but B is (" +
                                     detail::dims(B.rows(), B.cols()) +
-                                    "). Required: A.cols() == B.rows() (" +
+                                    "). Required: A.cols() == B.rows() (both = " +
                                     std::to_string(A.cols()) + " vs " + std::to_string(B.rows()) +
                                     ").");
     Tensor C = Tensor::device_dense(A.rows(), B.cols());
@@ -907,6 +906,9 @@ Tensor Model::forward(const Tensor& adjacency, const Tensor& features) const {
 Tensor GraphLoader::edge_list_to_csr(const std::vector<std::pair<int32_t, int32_t>>& edges,
                                      std::size_t num_nodes) {
     const size_t e = edges.size();
+    if (num_nodes == 0 && e != 0)  // graph_loader.cpp:216-221, before any device work
+        throw std::invalid_argument(
+            "GraphLoader::edge_list_to_csr: num_nodes is 0 but edges is non-empty");
     std::vector<int32_t> src(e), dst(e);
     for (size_t i = 0; i < e; ++i) {
         src[i] = edges[i].first;
