@@ -302,6 +302,49 @@ def cpp_api_spmm(torch, tg, a, rp, ci, val, b, plan, reps):
                 ratio=round(cpp_ms / cabi_ms, 4), bit_identical=same, calls=reps)
 
 
+def cpp_api_gcn_layer(torch, rp, ci, val, x, w, b, reps):
+    """GCNLayer::forward (the reference's layers.hpp:172-214, layers.cpp:
+    286-339) through the pybind module over libtinygnn.so at config E's layer
+    1 (602 -> 256, ReLU) on gcn_norm(A): wall ms per call, against the same
+    steps as separate C++ API calls (matmul, spmm, add_bias, relu_inplace --
+    the reference's sequence, two more passes over the 238 MB output).  The
+    layer fuses bias and ReLU into the SpMM's store; the two results must be
+    bit-identical."""
+    T = _tinygnn_pkg()
+    n = rp.shape[0] - 1
+    A = T.Tensor.from_scipy_csr(_csr_view(n, n, rp, ci, val))
+    An = T.gcn_norm(A)
+    H = T.from_torch(x)
+    W = T.from_torch(w)
+    B = T.from_torch(b.reshape(1, -1))
+    layer = T.GCNLayer(w.shape[0], w.shape[1], True, T.Activation.RELU)
+    layer.set_weight(W)
+    layer.set_bias(B)
+    keep = [None, None]
+
+    def fused():
+        keep[0] = layer.forward(An, H)
+
+    def chain():
+        out = T.spmm(An, T.matmul(H, W))
+        T.add_bias(out, B)
+        T.relu_inplace(out)
+        keep[1] = out
+
+    fused_ms = wall_ms_per_call(torch, fused, reps)
+    chain_ms = wall_ms_per_call(torch, chain, reps)
+    same = bool(torch.equal(T.to_torch(keep[0]).view(torch.int32),
+                            T.to_torch(keep[1]).view(torch.int32)))
+    log(f"C++ API GCNLayer::forward (602 -> 256, ReLU, unblocked): {fused_ms:.2f} ms/call fused, "
+        f"{chain_ms:.2f} ms as separate calls, bit-identical {same}")
+    del keep, A, An, H, W, B, layer
+    return dict(gcn_layer_ms_per_call=round(fused_ms, 3),
+                separate_calls_ms_per_call=round(chain_ms, 3), bit_identical=same, calls=reps,
+                note="layer 1 of config E's GCN on gcn_norm(A) through libtinygnn.so: matmul, "
+                     "then spmm with add_bias and relu fused into its store, against matmul, "
+                     "spmm, add_bias, relu_inplace as separate calls")
+
+
 def cpp_api_model(torch, tg, spec, w, adj, rp, ci, val, x, y_cabi, reps):
     """Model::forward (the reference's model.hpp:148) through the pybind
     module over libtinygnn.so, against tg_model_forward through ctypes on the
@@ -548,6 +591,12 @@ def run_forward_e(args, torch, tg):
             cpp_ms, same = cpp_api_model(torch, tg, spec, w, adj, rp_e, ci_e, val_e, x, y, reps)
             cpp = dict(cpp_api_ms_per_call=round(cpp_ms, 3), c_abi_ms_per_call=round(cabi_wall, 3),
                        ratio=round(cpp_ms / cabi_wall, 4), bit_identical=same, calls=reps)
+            if name == "gcn":
+                torch.cuda.empty_cache()
+                cpp["gcn_layer"] = cpp_api_gcn_layer(
+                    torch, rp_e, ci_e, val_e, x,
+                    torch.from_numpy(w["layer0.weight"]).to(dev),
+                    torch.randn(w["layer0.bias"].shape[1], device=dev), 3)
             log(f"{name}: C++ API Model::forward {cpp_ms:.2f} ms/call, C-ABI {cabi_wall:.2f} "
                 f"ms/call, bit-identical {same}")
         # the timed (cached) forward's raw outputs and logits are the ones checked

@@ -49,6 +49,9 @@ enum { TG_ACT_NONE = 0, TG_ACT_RELU = 1 };
 enum { TG_POST_NONE = 0, TG_POST_RELU = 1, TG_POST_ELU = 2 };
 /* SAGE aggregator (layers.hpp:250-253 {Mean=0, Max=1}). */
 enum { TG_AGG_MEAN = 0, TG_AGG_MAX = 1 };
+/* Epilogue fused into a matmul or SpMM store: bias add, then ReLU or ELU
+ * (alpha 1), as add_bias then relu_inplace / elu_inplace (ops.cpp:328-661). */
+enum { TG_EPI_NONE = 0, TG_EPI_RELU = 1, TG_EPI_ELU = 2 };
 /* Summation order of SpMM plans and Model forwards (no counterpart in the
  * reference, which has one order): TG_PRECISION_EXACT keeps the reference's
  * order bit for bit; TG_PRECISION_FAST may regroup sums (see the entry
@@ -146,6 +149,16 @@ int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f,
                     const int32_t* row_ptr, const int32_t* col_ind, const float* val,
                     const float* b, int64_t ldb, float* c, int64_t ldc,
                     tg_stream_t stream);
+/* tg_spmm_execute with the epilogue of GCNLayer::forward fused into the
+ * store (src/layers.cpp:319-336): C = act(A B + bias), bias of f floats (or
+ * NULL), epilogue TG_EPI_NONE / TG_EPI_RELU / TG_EPI_ELU (alpha 1).  The
+ * result is bit-identical to tg_spmm_execute, then tg_add_bias, then
+ * tg_relu / tg_elu, without the two extra passes over C. */
+int tg_spmm_execute_epilogue(tg_spmm_plan_t plan, int64_t k, int64_t f,
+                             const int32_t* row_ptr, const int32_t* col_ind,
+                             const float* val, const float* b, int64_t ldb, float* c,
+                             int64_t ldc, const float* bias, int epilogue,
+                             tg_stream_t stream);
 /* Summation order of the plan's later executes and of tg_sage_aggregate /
  * tg_sage_forward over it (TG_PRECISION_EXACT by default).  EXACT sums
  * every row, split rows included, as one chain in nonzero order from 0 --
@@ -197,7 +210,6 @@ int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t*
  * tolerance, not bit-identical).
  * ------------------------------------------------------------------------ */
 enum { TG_GEMM_AUTO = 0, TG_GEMM_INORDER = 1, TG_GEMM_MFMA = 2 };
-enum { TG_EPI_NONE = 0, TG_EPI_RELU = 1, TG_EPI_ELU = 2 };
 int tg_matmul(int64_t m, int64_t k, int64_t n, const float* a, int64_t lda,
               const float* b, int64_t ldb, float* c, int64_t ldc,
               const float* bias, int epilogue, int algo, tg_stream_t stream);

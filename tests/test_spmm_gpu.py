@@ -182,3 +182,43 @@ def test_spmm_reference_known_answers(gpu):
     b = np.array([[2, -4], [1, 8]], np.float32)
     got, _ = _run(gpu, a, b)
     np.testing.assert_allclose(got, [[-0.5, -14.0], [0.25, 2.0]], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("f", [7, 41, 128])
+@pytest.mark.parametrize("epilogue", ["none", "relu", "elu"])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_spmm_epilogue_fused(gpu, restate, f, epilogue, with_bias):
+    """tg_spmm_execute_epilogue (GCNLayer::forward's spmm + add_bias + act in
+    one pass, layers.cpp:319-336) against the three separate calls, bit for
+    bit, and against the oracle's chain: bit-exact for none / relu, within
+    the tolerance for elu (device expf vs the host's)."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(40 + f)
+    a = random_csr(rng, 600, 600, avg_deg=12, max_deg=3000, empty_frac=0.05)
+    b = rng.standard_normal((600, f)).astype(np.float32)
+    bias = rng.standard_normal(f).astype(np.float32) if with_bias else None
+    da = tg.DeviceCSR.from_numpy(a.n_rows, a.n_cols, a.row_ptr, a.col_ind, a.val)
+    db = gpu.from_numpy(b).cuda()
+    dbias = gpu.from_numpy(bias).cuda() if with_bias else None
+    plan = tg.SpmmPlan(da.row_ptr, a.n_rows, a.nnz, f)
+    code = {"none": tg.EPI_NONE, "relu": tg.EPI_RELU, "elu": tg.EPI_ELU}[epilogue]
+    fused = tg.spmm_epilogue(da, db, plan, bias=dbias, epilogue=code).cpu().numpy()
+    chain = tg.spmm(da, db, plan=plan)
+    if with_bias:
+        tg.add_bias_(chain, dbias)
+    if epilogue == "relu":
+        tg.relu_(chain)
+    elif epilogue == "elu":
+        tg.elu_(chain)
+    np.testing.assert_array_equal(bits(fused), bits(chain.cpu().numpy()))
+    want = restate.spmm(a, b)
+    if with_bias:
+        want = want + bias[None, :]
+    if epilogue == "relu":
+        want = np.where(want > 0, want, np.float32(0)).astype(np.float32)
+        np.testing.assert_array_equal(bits(fused), bits(want))
+    elif epilogue == "none":
+        np.testing.assert_array_equal(bits(fused), bits(want.astype(np.float32)))
+    else:
+        want = restate.activation("elu", want.astype(np.float32), 1.0)
+        np.testing.assert_allclose(fused, want, rtol=1e-6, atol=1e-7)

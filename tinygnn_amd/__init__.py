@@ -126,6 +126,24 @@ def _check_spmm_shapes(a: DeviceCSR, b):
                                  f"Required: A.cols() == B.rows() ({a.n_cols} vs {b.shape[0]}).")
 
 
+def spmm_epilogue(a: DeviceCSR, b, plan: SpmmPlan, bias=None, epilogue: int = EPI_NONE,
+                  out=None, stream=None):
+    """act(A * B + bias) in one pass (tg_spmm_execute_epilogue): the SpMM of
+    GCNLayer::forward with add_bias and the activation fused into its store
+    (reference layers.cpp:319-336); bit-identical to spmm, add_bias_, then
+    relu_ / elu_."""
+    torch = _torch()
+    _check_spmm_shapes(a, b)
+    f = b.shape[1]
+    if out is None:
+        out = torch.empty((a.n_rows, f), dtype=torch.float32, device=b.device)
+    lib.check(lib.tg_spmm_execute_epilogue(plan.h, a.n_cols, f, dptr(a.row_ptr),
+                                           dptr(a.col_ind), dptr(a.val), dptr(b), b.stride(0),
+                                           dptr(out), out.stride(0), dptr(bias), epilogue,
+                                           stream_handle(stream)))
+    return out
+
+
 def spmm(a: DeviceCSR, b, plan: SpmmPlan | None = None, out=None, stream=None,
          precision: int = PRECISION_EXACT):
     """C = A * B (reference ops.cpp:198-297).  With a plan, the plan's

@@ -70,6 +70,7 @@ SIGNATURES = {
     "tg_spmm_plan_info": (i32, [vp, pi64, pi64, pi64]),
     "tg_spmm_execute": (i32, [vp, i64, i64, vp, vp, vp, vp, i64, vp, i64, vp]),
     "tg_spmm_plan_set_precision": (i32, [vp, i32]),
+    "tg_spmm_execute_epilogue": (i32, [vp, i64, i64, vp, vp, vp, vp, i64, vp, i64, vp, i32, vp]),
     "tg_probe_l2_read": (i32, [vp, i64, i64, vp, vp]),
     "tg_spmm": (i32, [i64, i64, i64, i64, vp, vp, vp, vp, i64, vp, i64, vp]),
     "tg_spmm_ex": (i32, [i64, i64, i64, i64, vp, vp, vp, vp, i64, vp, i64, i32, vp]),

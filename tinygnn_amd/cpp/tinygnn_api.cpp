@@ -664,9 +664,26 @@ Tensor GCNLayer::forward(const Tensor& A_norm, const Tensor& H) const {
                                     std::to_string(A_norm.rows()) + " rows but H has " +
                                     std::to_string(H.rows()) +
                                     " rows. They must match (N nodes).");
-    Tensor out = spmm(A_norm, matmul(H, weight_));
-    if (use_bias_) add_bias(out, bias_);
-    if (activation_ == Activation::ReLU) relu_inplace(out);
+    const Tensor hw = matmul(H, weight_);
+    if (A_norm.rows() == 0 || hw.cols() == 0 || A_norm.nnz() == 0) {
+        // spmm's zero result (ops.cpp:231-236), then the epilogue
+        Tensor out = spmm(A_norm, hw);
+        if (use_bias_) add_bias(out, bias_);
+        if (activation_ == Activation::ReLU) relu_inplace(out);
+        return out;
+    }
+    // spmm, add_bias and relu_inplace (layers.cpp:319-336) as one pass: the
+    // bias and the activation are applied in the SpMM's store, bit-identical
+    // to the three calls
+    const int64_t f = i64(hw.cols());
+    Tensor out = Tensor::device_dense(A_norm.rows(), hw.cols());
+    tg_spmm_plan_t plan = detail::plan_for(A_norm, f);
+    check(tg_spmm_plan_set_precision(plan, TG_PRECISION_EXACT));
+    check(tg_spmm_execute_epilogue(
+        plan, i64(A_norm.cols()), f, A_norm.device_row_ptr(), A_norm.device_col_ind(),
+        A_norm.device_data(), hw.device_data(), f, out.device_data_mutable(), f,
+        use_bias_ ? bias_.device_data() : nullptr,
+        activation_ == Activation::ReLU ? TG_EPI_RELU : TG_EPI_NONE, nullptr));
     return out;
 }
 

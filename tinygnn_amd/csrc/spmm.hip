@@ -1678,6 +1678,30 @@ int tg_spmm_execute(tg_spmm_plan_t plan, int64_t k, int64_t f, const int32_t* ro
     });
 }
 
+int tg_spmm_execute_epilogue(tg_spmm_plan_t plan, int64_t k, int64_t f, const int32_t* row_ptr,
+                             const int32_t* col_ind, const float* val, const float* b,
+                             int64_t ldb, float* c, int64_t ldc, const float* bias, int epilogue,
+                             tg_stream_t stream) {
+    return guard([&] {
+        require(plan != nullptr, "tg_spmm_execute_epilogue: plan is null");
+        require(row_ptr == plan->row_ptr,
+                "tg_spmm_execute_epilogue: row_ptr differs from the one the plan was built for");
+        require(k >= 0 && f >= 0, "spmm: negative dimension");
+        require(val != nullptr, "spmm: val is null");
+        require(epilogue == TG_EPI_NONE || epilogue == TG_EPI_RELU || epilogue == TG_EPI_ELU,
+                "tg_spmm_execute_epilogue: unknown epilogue");
+        tg::AggEpilogue epi;
+        epi.long_rows = plan->precision == TG_PRECISION_EXACT;
+        epi.bias = bias;
+        // add_bias (ops.cpp:622-661), then relu_inplace / elu_inplace with
+        // alpha 1 (ops.cpp:328-392): the same operations in the store
+        epi.act = epilogue == TG_EPI_RELU ? TG_ACT_RELU : TG_ACT_NONE;
+        epi.post = epilogue == TG_EPI_ELU ? TG_POST_ELU : TG_POST_NONE;
+        tg::run_aggregate(*plan, f, col_ind, val, b, ldb, c, ldc, epi,
+                          static_cast<hipStream_t>(stream));
+    });
+}
+
 int tg_spmm_ex(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
                const int32_t* col_ind, const float* val, const float* b, int64_t ldb, float* c,
                int64_t ldc, int precision, tg_stream_t stream) {
