@@ -180,18 +180,26 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
  * SpMM that allocates nothing.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  Arguments and
- * result bits are tg_spmm's (the same plan and kernels), but the plan lives
- * in a fixed device array of TG_SPMM_NOALLOC_SCRATCH_BYTES per GPU, held
- * from the first call on that GPU until the process ends, and the call
- * neither allocates nor synchronises: it only enqueues kernels on `stream`.
+ * result bits are tg_spmm's (the same plan and kernels: every row in the
+ * reference's order), but the plan lives in a fixed device array of
+ * TG_SPMM_NOALLOC_SCRATCH_BYTES per GPU, and the call neither allocates nor
+ * synchronises: it only enqueues kernels on `stream`.
+ *   The array is the only content of its code object, which a GPU loads
+ *   when a process first calls tg_spmm_noalloc on it (resolving the array's
+ *   address): from then until the process ends, that GPU holds the 128 MiB
+ *   for that process; processes that never call it do not hold it.  That
+ *   first call on each GPU must be made outside stream capture (under
+ *   capture it fails with TG_ERR_INVALID_ARGUMENT); later calls may be
+ *   captured into HIP graphs and replayed.
  *   Limit: the plan takes 16(m+1) + 16(m + nnz/1024) + 16 nnz/1025
  *   + 4 round_up(f, 4) (nnz/1024 + nnz/1025) bytes, about (256-byte aligned
  *   pieces); larger sizes fail with TG_ERR_INVALID_ARGUMENT before any device
  *   work.  Config D (10^6 rows, 5 x 10^7 nonzeros) fits for f <= 256.
  *   Every call on one GPU uses that GPU's one array and leaves its contents
  *   behind: calls that overlap in time on one GPU (other streams, other
- *   threads) race, and the caller must serialise them.  row_ptr[m] must
- *   equal nnz, as for tg_spmm (a larger row_ptr[m] leaves C unwritten).
+ *   threads, graph replays) race, and the caller must serialise them.
+ *   row_ptr[m] must equal nnz, as for tg_spmm; a larger row_ptr[m] that
+ *   overflows the plan's capacities fills C with NaN.
  * ------------------------------------------------------------------------ */
 #define TG_SPMM_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
 int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,

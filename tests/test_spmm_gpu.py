@@ -205,7 +205,7 @@ def test_spmm_epilogue_fused(gpu, restate, f, epilogue, with_bias):
     fused = tg.spmm_epilogue(da, db, plan, bias=dbias, epilogue=code).cpu().numpy()
     chain = tg.spmm(da, db, plan=plan)
     if with_bias:
-        tg.add_bias_(chain, dbias)
+        tg.add_bias_(chain, dbias.reshape(1, -1))
     if epilogue == "relu":
         tg.relu_(chain)
     elif epilogue == "elu":

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -42,19 +43,35 @@ void check(int status) {
 // Device buffers come from the stream-ordered allocator on the null stream,
 // the stream every op of this API runs on: a buffer released while kernels
 // that use it are still queued is only reused by work queued after them, so
-// no release waits for the device.  The device's default pool keeps freed
-// memory (release threshold raised once per device), so a warm loop of ops
-// allocates without calling into the driver.
-void prepare_pool() {
-    static bool done[64] = {};
+// no release waits for the device.  They come from a memory pool of the
+// library's own per device (created once, under a lock), which keeps freed
+// memory (its release threshold is raised), so a warm loop of ops allocates
+// without calling into the driver; the device's default pool, which other
+// code in the process may use, keeps its own settings.
+hipMemPool_t library_pool() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static hipMemPool_t pools[kMaxDevices] = {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64 || done[dev]) return;
-    hipMemPool_t pool = nullptr;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess && pool) {
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        throw std::runtime_error("device ordinal out of range for the memory pools");
+    std::lock_guard<std::mutex> lock(mu);
+    if (pools[dev] == nullptr) {
+        hipMemPoolProps props{};
+        props.allocType = hipMemAllocationTypePinned;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = nullptr;
+        e = hipMemPoolCreate(&pool, &props);
+        if (e != hipSuccess) hip_fail(e, "hipMemPoolCreate");
         uint64_t keep = ~uint64_t(0);
-        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) hip_fail(e, "hipMemPoolSetAttribute");
+        pools[dev] = pool;
     }
-    done[dev] = true;
+    return pools[dev];
 }
 
 struct DevBuf {
@@ -73,9 +90,8 @@ struct DevBuf {
         if (bytes <= n && p) return;
         release();
         if (bytes == 0) bytes = 4;
-        prepare_pool();
-        hipError_t e = hipMallocAsync(&p, bytes, nullptr);
-        if (e != hipSuccess) hip_fail(e, "hipMallocAsync");
+        hipError_t e = hipMallocFromPoolAsync(&p, bytes, library_pool(), nullptr);
+        if (e != hipSuccess) hip_fail(e, "hipMallocFromPoolAsync");
         n = bytes;
     }
 };

@@ -17,7 +17,6 @@
 #include <algorithm>
 #include <climits>
 #include <memory>
-#include <mutex>
 
 namespace tg {
 
@@ -1509,41 +1508,15 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
 }  // namespace tg
 
 // ---------------------------------------------------------------------------
-// SpMM without allocation (tg_spmm_noalloc): the plan of one call -- its
-// build temporaries, chunks, split records and partials -- carved from one
-// fixed device array instead of allocated buffers.  The host never reads the
-// plan's counts: the grids cover upper bounds and the kernels read the true
-// counts from the array, so the call only enqueues kernels.
+// SpMM without allocation (tg_spmm_noalloc, whose C-ABI and fixed device
+// array are in noalloc.hip): the plan of one call -- its build temporaries,
+// chunks, split records and partials -- carved from a caller-given device
+// array instead of allocated buffers.  The host never reads the plan's
+// counts: the grids cover upper bounds and the kernels read the true counts
+// from the array, so the call only enqueues kernels.
 // ---------------------------------------------------------------------------
-
-// Each GPU holds its own copy from the library's first use on it until the
-// process ends; every call on one GPU shares it (overlapping calls race).
-static __device__ __align__(256) unsigned char scratch[TG_SPMM_NOALLOC_SCRATCH_BYTES];
-
 namespace tg {
 namespace {
-
-constexpr int kMaxDevices = 64;
-
-// The array's device address on the current device.  The array's name in
-// host code is a host-side stand-in, not a device address, so every use
-// goes through the address hipGetSymbolAddress returns, taken once per
-// device with that device current.
-char* noalloc_scratch() {
-    int dev = 0;
-    TG_HIP(hipGetDevice(&dev));
-    require(dev >= 0 && dev < kMaxDevices, "tg_spmm_noalloc: device ordinal out of range");
-    static std::mutex mu;
-    static void* addr[kMaxDevices] = {};
-    std::lock_guard<std::mutex> lock(mu);
-    if (addr[dev] == nullptr) {
-        void* p = nullptr;
-        TG_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        require(p != nullptr, "tg_spmm_noalloc: no device address for the scratch array");
-        addr[dev] = p;
-    }
-    return static_cast<char*>(addr[dev]);
-}
 
 // Capacities of a plan for m rows and nnz nonzeros in chunks of c:
 // chunks <= m + nnz / c (each row one chunk, plus one per further c
@@ -1571,20 +1544,32 @@ NoAllocPlan carve_noalloc(Carver& cv, int64_t m, int64_t nnz, int64_t f) {
     return P;
 }
 
-void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const int32_t* ci,
-                  const float* v, const float* b, int64_t ldb, float* c, int64_t ldc,
-                  hipStream_t s) {
-    // sizes first: a rejected call does no device work
+// A row_ptr whose last entry exceeds the caller's nnz overflows the plan's
+// capacities; plan_bins_kernel then zeroes the counts (nothing else runs)
+// and sets totals[3], and this kernel fills C with NaN, so that the misuse
+// shows in the output instead of leaving it unwritten.
+__global__ __launch_bounds__(256) void noalloc_poison_kernel(const int64_t* __restrict__ totals,
+                                                             float* __restrict__ c, int64_t m,
+                                                             int64_t f, int64_t ldc) {
+    if (totals[3] == 0) return;
+    const int64_t n = m * f;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+        c[(i / f) * ldc + i % f] = __builtin_nanf("");
+}
+
+}  // namespace
+
+size_t spmm_noalloc_bytes(int64_t m, int64_t nnz, int64_t f) {
     Carver sizing(nullptr, 0);
     carve_noalloc(sizing, m, nnz, f);
-    if (sizing.bytes() > TG_SPMM_NOALLOC_SCRATCH_BYTES)
-        throw std::invalid_argument(
-            "tg_spmm_noalloc: the plan for m=" + std::to_string(m) + ", nnz=" +
-            std::to_string(nnz) + ", f=" + std::to_string(f) + " needs " +
-            std::to_string(sizing.bytes()) + " bytes of scratch; the maximum is " +
-            std::to_string(static_cast<size_t>(TG_SPMM_NOALLOC_SCRATCH_BYTES)) +
-            " (use tg_spmm or a plan)");
-    Carver cv(noalloc_scratch(), TG_SPMM_NOALLOC_SCRATCH_BYTES);
+    return sizing.bytes();
+}
+
+void spmm_noalloc(char* scratch, size_t scratch_bytes, int64_t m, int64_t f, int64_t nnz,
+                  const int32_t* rp, const int32_t* ci, const float* v, const float* b,
+                  int64_t ldb, float* c, int64_t ldc, hipStream_t s) {
+    Carver cv(scratch, scratch_bytes);
     const NoAllocPlan P = carve_noalloc(cv, m, nnz, f);
     const int chunk = static_cast<int>(kDefaultChunk);
     const unsigned nblk = static_cast<unsigned>(ceil_div(m, 256));
@@ -1614,9 +1599,11 @@ void spmm_noalloc(int64_t m, int64_t f, int64_t nnz, const int32_t* rp, const in
     AggEpilogue epi;
     epi.long_rows = 1;  // tg_spmm's order: every row one chain in nonzero order
     run_aggregate(pv, f, ci, v, b, ldb, c, ldc, epi, s);
+    const unsigned pblk = static_cast<unsigned>(std::min<int64_t>(ceil_div(m * f, 256), 1024));
+    noalloc_poison_kernel<<<pblk, 256, 0, s>>>(P.t.totals, c, m, f, ldc);
+    TG_LAUNCH_CHECK();
 }
 
-}  // namespace
 }  // namespace tg
 
 // ---------------------------------------------------------------------------
@@ -1730,25 +1717,6 @@ int tg_spmm(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr
             int64_t ldc, tg_stream_t stream) {
     return tg_spmm_ex(m, k, f, nnz, row_ptr, col_ind, val, b, ldb, c, ldc, TG_PRECISION_EXACT,
                       stream);
-}
-
-int tg_spmm_noalloc(int64_t m, int64_t k, int64_t f, int64_t nnz, const int32_t* row_ptr,
-                    const int32_t* col_ind, const float* val, const float* b, int64_t ldb,
-                    float* c, int64_t ldc, tg_stream_t stream) {
-    return guard([&] {
-        require(m >= 0 && k >= 0 && f >= 0 && nnz >= 0, "spmm: negative dimension");
-        require(m < (int64_t(1) << 31) && nnz < (int64_t(1) << 31),
-                "spmm: m and nnz must be < 2^31 (int32 CSR)");
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        if (m == 0 || f == 0) return;
-        if (nnz == 0) {
-            // ops.cpp:231-236: the result is the zero-initialised C.
-            tg::fill_zero_2d(c, m, f, ldc, s);
-            return;
-        }
-        require(row_ptr && col_ind && val && b && c, "spmm: null pointer");
-        tg::spmm_noalloc(m, f, nnz, row_ptr, col_ind, val, b, ldb, c, ldc, s);
-    });
 }
 
 }  // extern "C"

@@ -125,6 +125,16 @@ int pick_load_vec(int64_t f, int64_t ldb, const void* b);
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// tg_spmm's plan and aggregation with every buffer carved from `scratch`, a
+// device array of scratch_bytes (>= spmm_noalloc_bytes(m, nnz, f)): only
+// kernels are enqueued on s, nothing is allocated and the host reads no
+// count.  C's bits are tg_spmm's; a row_ptr[m] larger than nnz fills C with
+// NaN.
+size_t spmm_noalloc_bytes(int64_t m, int64_t nnz, int64_t f);
+void spmm_noalloc(char* scratch, size_t scratch_bytes, int64_t m, int64_t f, int64_t nnz,
+                  const int32_t* rp, const int32_t* ci, const float* v, const float* b,
+                  int64_t ldb, float* c, int64_t ldc, hipStream_t s);
+
 // Row pitch (floats) for a dense matrix whose rows are gathered: widths of
 // 4, 8, 16 or 32 floats after 4-float padding tile a 128-byte cache line
 // exactly; wider rows are padded to whole lines, so a gathered row always
