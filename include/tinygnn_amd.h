@@ -389,9 +389,13 @@ int tg_model_invalidate(tg_model_t model);
  * counterpart in the reference): blocks and columns per lane group of A + I's
  * blocked copy (GCN, GAT) and of A's (SAGE mean); 0 blocks = unblocked or no
  * cached state; sl_direct = 1 when A + I's blocked copy was split from A
- * directly (below).  Filled by the last forward; any pointer may be null. */
+ * directly (below); resident: bit 0 set when A + I's blocked copy is
+ * prepared for the output-resident passes, bit 1 when A's is
+ * (tg_model_set_resident_passes).  Filled by the last forward; any pointer
+ * may be null. */
 int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
-                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct);
+                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct,
+                           int64_t* resident);
 /* How a fast-precision model whose blocked A + I is read only by the
  * factored GCN passes (A's values all 1) or by GAT passes that carry their
  * softmax gets that copy (no counterpart in the reference; for tests and
@@ -404,6 +408,20 @@ int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_s
  * then split.  Both give the same blocked copy and the same outputs bit for
  * bit.  Drops the cached state. */
 int tg_model_set_self_loop_split(tg_model_t model, int direct);
+/* The blocked aggregations without values in fast precision (SAGE mean;
+ * the factored GCN over a unit A + I) as output-resident passes (no
+ * counterpart in the reference; for tests and measurement).  on = 1: one
+ * workgroup per CU owns a range of rows (at most 1088; used when the rows
+ * fit, n <= 1088 x CUs) and keeps their 32-column output tile in LDS while
+ * it walks every column block, each block's entries of the range split
+ * evenly over its lane groups; one launch per aggregation, the output
+ * written once, the workgroups paced block by block so that they gather
+ * from one block's slice of B at a time.  on = 0 (the default): one pass
+ * per block, each reading and writing the output (config E: the resident
+ * form reaches a 94% L2 hit rate but keeps fewer gathers in flight, and is
+ * slower).  The sums are deterministic either way and differ in rounding
+ * only.  Drops the cached state. */
+int tg_model_set_resident_passes(tg_model_t model, int on);
 
 /* ------------------------------------------------------------------------
  * CSV ingestion -- replaces GraphLoader::parse_edges / parse_features and

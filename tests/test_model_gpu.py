@@ -721,3 +721,81 @@ def test_blocked_wide_blocks_int32(gpu, restate, model):
         assert info["blocks_sl" if model == "gcn" else "blocks_raw"] == (2 if blocking else 0)
     np.testing.assert_array_equal(bits(outs[70_000]), bits(outs[0]))
     assert_close(outs[0], restate.model_forward(spec, w, a, x), what=model)
+
+
+@pytest.mark.parametrize("case", ["sage_concat", "sage_transform_first", "sage_wide_tail",
+                                  "sage_split_rows", "sage_two_blocks", "sage_exact",
+                                  "sage_many_rows", "gcn_unit", "gcn_unit_split_rows"])
+def test_resident_passes(gpu, restate, case):
+    """The output-resident passes (one workgroup per CU keeps its rows'
+    32-column output tile in LDS across every column block) in fast
+    precision, for the aggregations without values -- SAGE's mean (both
+    dataflows, a last tile of 25 valid columns, rows of thousands of entries
+    shared by many lane groups, two blocks) and the factored GCN over a unit
+    A + I: within the fast tolerance of the oracle, deterministic from call
+    to call, and within tolerance of the per-block passes.  In exact
+    precision, and where the rows do not fit the workgroups' LDS (more than
+    1088 per CU), the per-block passes run instead: exact stays the
+    reference's bytes."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(83)
+    split = case.endswith("split_rows")
+    n = 300_000 if case == "sage_many_rows" else 4000 if split else 3000
+    blocking = (2000 if split else n // 2 + 1 if case == "sage_two_blocks"
+                else 10_000 if case == "sage_many_rows" else 100)
+    if case == "sage_many_rows":
+        a = random_csr(rng, n, n, avg_deg=6)
+    else:
+        a = random_csr(rng, n, n, avg_deg=40, max_deg=3600 if split else 2800,
+                       empty_frac=0.05)
+    if split:  # rows with more than 1024 entries in a block
+        assert (np.diff(a.row_ptr) > 3000).any()
+    if case.startswith("gcn"):
+        rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
+        keep = rows != a.col_ind
+        a = restate.edge_list_to_csr(rows[keep], a.col_ind[keep].astype(np.int32), n)
+        assert (a.val == 1.0).all()
+        spec = synth.spec_gcn(48, 300, 7)
+    elif case == "sage_wide_tail":
+        spec = synth.spec_sage(96, 60, 25)
+    elif case == "sage_many_rows":
+        spec = synth.spec_sage(16, 32, 5)
+    else:
+        spec = synth.spec_sage(96, 300, 10)
+    w = synth.model_weights(spec, seed=8)
+    for k in w:
+        if k.endswith("bias"):
+            w[k] = (rng.standard_normal(w[k].shape) * 0.1).astype(np.float32)
+    x = rng.standard_normal((n, spec[0]["in"])).astype(np.float32)
+    want = restate.model_forward(spec, w, a, x)
+    da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)
+    xt = _t(gpu, x)
+    gcn = case.startswith("gcn")
+    expect = case not in ("sage_exact", "sage_many_rows")
+    outs = {}
+    for on in (True, False):
+        m = tg.Model.from_spec(spec, w)
+        if case == "sage_concat":
+            m.set_sage_dataflow(tg.SAGE_CONCAT)
+        elif case.startswith("sage"):
+            m.set_sage_dataflow(tg.SAGE_TRANSFORM_FIRST)
+        if case == "sage_exact":
+            m.set_precision(tg.PRECISION_EXACT)
+        m.set_blocking(blocking)
+        m.set_resident_passes(on)
+        got = m.forward(da, xt).cpu().numpy()
+        info = m.blocking_info()
+        assert info["resident_sl" if gcn else "resident_raw"] == (on and expect), info
+        assert info["blocks_sl" if gcn else "blocks_raw"] == -(-n // blocking), info
+        for mode in (tg.FORWARD_REFERENCE, tg.FORWARD_CACHED):
+            again = m.forward(da, xt, mode=mode).cpu().numpy()
+            np.testing.assert_array_equal(bits(got), bits(again), err_msg=f"resident={on}")
+        if case == "sage_exact":
+            np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
+        else:
+            assert_close(got, want, what=f"{case} resident={on}")
+        outs[on] = got
+    if expect:
+        assert_close(outs[True], outs[False], what=f"{case} resident vs passes")
+    else:
+        np.testing.assert_array_equal(bits(outs[True]), bits(outs[False]))

@@ -446,12 +446,15 @@ class Model:
 
     def blocking_info(self) -> dict:
         """The column blocking the last forward used (tg_model_blocking_info):
-        blocks and lane-group columns of A + I's and A's blocked copies, and
-        whether A + I's was split from A directly (sl_direct)."""
-        v = [C.c_int64() for _ in range(5)]
+        blocks and lane-group columns of A + I's and A's blocked copies,
+        whether A + I's was split from A directly (sl_direct), and whether
+        each copy is prepared for the output-resident passes (resident_sl,
+        resident_raw)."""
+        v = [C.c_int64() for _ in range(6)]
         lib.check(lib.tg_model_blocking_info(self.h, *[C.byref(x) for x in v]))
         return dict(blocks_sl=v[0].value, cols_sl=v[1].value, blocks_raw=v[2].value,
-                    cols_raw=v[3].value, sl_direct=bool(v[4].value))
+                    cols_raw=v[3].value, sl_direct=bool(v[4].value),
+                    resident_sl=bool(v[5].value & 1), resident_raw=bool(v[5].value & 2))
 
     def set_self_loop_split(self, direct: bool = True) -> None:
         """Whether a fast GCN-only model splits its blocked A + I from A
@@ -459,6 +462,14 @@ class Model:
         outputs bit for bit either way).  Drops the cached state."""
         self._adj_key = None
         lib.check(lib.tg_model_set_self_loop_split(self.h, 1 if direct else 0))
+
+    def set_resident_passes(self, on: bool = True) -> None:
+        """Whether the fast blocked aggregations without values (SAGE mean,
+        the factored GCN) run as output-resident passes, one launch with the
+        output tile in LDS, or one pass per column block
+        (tg_model_set_resident_passes).  Drops the cached state."""
+        self._adj_key = None
+        lib.check(lib.tg_model_set_resident_passes(self.h, 1 if on else 0))
 
     def invalidate(self) -> None:
         """Forgets the cached adjacency state (tg_model_invalidate)."""

@@ -109,8 +109,9 @@ SIGNATURES = {
     "tg_model_set_blocking": (i32, [vp, i64]),
     "tg_model_forward": (i32, [vp, i64, i64, vp, vp, vp, i64, vp, vp, i32, vp]),
     "tg_model_invalidate": (i32, [vp]),
-    "tg_model_blocking_info": (i32, [vp, pi64, pi64, pi64, pi64, pi64]),
+    "tg_model_blocking_info": (i32, [vp, pi64, pi64, pi64, pi64, pi64, pi64]),
     "tg_model_set_self_loop_split": (i32, [vp, i32]),
+    "tg_model_set_resident_passes": (i32, [vp, i32]),
     "tg_csv_open": (i32, [C.c_char_p, C.POINTER(vp), vp]),
     "tg_csv_index": (i32, [vp, i64, C.c_char_p, C.POINTER(vp), vp]),
     "tg_csv_destroy": (i32, [vp]),

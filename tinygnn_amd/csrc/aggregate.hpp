@@ -50,6 +50,11 @@ struct AggEpilogue {
     // B's layout (tile_cols = 32 only): > 0 = tile-major, 32-column tile t
     // of row j at B + t * b_tile_stride + j * ldb (ldb = 32); 0 = row-major
     int64_t b_tile_stride = 0;
+    // rows of B from its (offset) first row to its end (a blocked pass: the
+    // rows from the block's first source row), set only where every 16-bit
+    // column is below 65535; 0 = unknown.  Lets the 16-bit passes gather
+    // through buffer loads that read zeros past the end.
+    int64_t b_rows = 0;
     // self's layout: > 0 = tile-major as B (ld_self = 32); 0 = row-major
     int64_t self_tile_stride = 0;
     // columns per head of the attention mode below (tiles never straddle
@@ -108,6 +113,21 @@ struct BlockedCSR {
     // columns): block order is nonzero order, so unsplit rows (plans built
     // with chunk >= the longest row) sum in the unblocked order bit for bit
     bool in_order = false;
+    // set by the caller before the build: also prepare the output-resident
+    // passes (run_aggregate_resident) for the copy's plain sums, where the
+    // indices are 16-bit and the rows fit the workgroups' LDS
+    bool resident = false;
+    // the resident passes' row ranges, one per workgroup (0 = not prepared):
+    // int32 [resident_wgs + 1] first rows, balanced by entries
+    int64_t resident_wgs = 0;
+    DeviceBuffer wg_rows;
+    // the resident passes' phase counters (one per column tile and block,
+    // for the tiles of max_f columns), cleared before each launch
+    DeviceBuffer phase_count;
+    int64_t max_phases = 0;
+    // the copy holds A + I's entries with rp = A's row_ptr (each row's
+    // diagonal placed by the split, build_blocked_self_loops)
+    bool vdiag = false;
     DeviceBuffer brp;  // int32 [n_blocks * n + 1]
     // the entries' columns: with idx16 (blocks of at most 65,536 rows) uint16
     // offsets within their block, column - block * rows_per_block (half the
@@ -155,5 +175,29 @@ int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_
 // into chunks are summed from per-chunk partials.  epi.max is not supported.
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
                            float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s);
+
+// The output-resident passes (fast precision; plain sums over 16-bit
+// indices): one workgroup per CU owns a range of at most kResidentRows rows
+// and keeps their 32-column output tile in LDS while it walks every column
+// block in order, so all workgroups gather from one block's slice of B at a
+// time (the slice stays in L2) and no pass reads or writes the output in
+// between.  Each block's entries of the range are split evenly over the
+// workgroup's lane groups; a row cut by such a split is summed as the
+// owning group's chain plus the later groups' partials, in group order
+// (deterministic; the unblocked and the per-pass sums differ in rounding
+// only).  Requires bk.resident_wgs > 0, and B with 16-byte aligned rows
+// (tile-major, or row-major with ldb % 4 == 0).
+constexpr int kResidentThreads = 1024;  // per workgroup
+constexpr int kResidentPerCU = 1;       // workgroups per CU (LDS: 157 KB)
+constexpr int kResidentRows = 1088;
+bool resident_ok(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
+                 const AggEpilogue& epi);
+void run_aggregate_resident(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
+                            float* c, int64_t ldc, const AggEpilogue& epi, hipStream_t s);
+// Splits bk's rows into bk.resident_wgs ranges (one per CU, at most
+// kResidentRows rows each, balanced by entries) and sizes the phase
+// counters for widths up to max_f; leaves resident_wgs = 0 when the rows do
+// not fit.  No synchronisation.
+void build_resident_split(BlockedCSR& bk, int64_t max_f, hipStream_t s);
 
 }  // namespace tg

@@ -505,6 +505,8 @@ void build_block_plans(BlockedCSR& bk, int64_t max_f, int64_t chunk, hipStream_t
     build_plans_multi(plans.data(), static_cast<int>(bk.n_blocks), bk.n, bk.nnz,
                       bk.brp.as<int32_t>(), max_f, chunk, bk.plan_scratch,
                       bk.host.as<int64_t>(), s);
+    if (bk.resident) build_resident_split(bk, max_f, s);
+    else bk.resident_wgs = 0;
 }
 
 // The flat split (with or without the virtual diagonal); false when some
@@ -607,6 +609,7 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
                    hipStream_t s, int64_t chunk) {
     const SplitTemps t = setup_blocked(bk, n, nnz, nnz, rp, v != nullptr, rows_per_block);
     require(nnz == 0 || ci != nullptr, "blocked CSR: null structure");
+    bk.vdiag = false;
     // rows in block order (sorted rows) take the flat split; the general
     // one runs when some row is not
     if (split_flat(bk, t, rp, ci, v, nnz, false, max_f, chunk, s)) {
@@ -622,9 +625,72 @@ bool build_blocked_self_loops(BlockedCSR& bk, int64_t n, int64_t nnz, const int3
     require(nnz + n < (int64_t(1) << 31), "blocked CSR: nnz + n must be < 2^31");
     const SplitTemps t = setup_blocked(bk, n, nnz + n, nnz, rp, false, rows_per_block);
     require(nnz == 0 || ci != nullptr, "blocked CSR: null structure");
+    bk.vdiag = true;
     if (!split_flat(bk, t, rp, ci, nullptr, nnz, true, max_f, chunk, s)) return false;
     bk.in_order = true;
     return true;
+}
+
+namespace {
+
+// The resident passes' row ranges: range w starts near the row where the
+// running count of the copy's entries (rp[r], plus r for the rows'
+// diagonals when the split placed them: the same counts for both ways of
+// building A + I's copy) reaches w/W of the total, then one thread walks the
+// W bounds so that every range holds at most `cap` rows (n <= W * cap).
+__global__ __launch_bounds__(1024) void resident_split_kernel(const int32_t* __restrict__ rp,
+                                                              int64_t n, int vdiag, int W,
+                                                              int cap,
+                                                              int32_t* __restrict__ wg_rows) {
+    __shared__ int32_t lb[1024];
+    const int w = threadIdx.x;
+    const int64_t tot = static_cast<int64_t>(rp[n]) + (vdiag ? n : 0);
+    if (w <= W) {
+        const int64_t target = tot * w / W;
+        int64_t lo = 0, hi = n;  // the first r whose count reaches target
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (static_cast<int64_t>(rp[mid]) + (vdiag ? mid : 0) < target) lo = mid + 1;
+            else hi = mid;
+        }
+        lb[w] = static_cast<int32_t>(lo);
+    }
+    __syncthreads();
+    if (w == 0) {
+        int64_t prev = 0;
+        lb[0] = 0;
+        for (int k = 1; k < W; ++k) {
+            int64_t e = lb[k];
+            e = e < prev ? prev : e;
+            e = e > prev + cap ? prev + cap : e;
+            const int64_t need = n - static_cast<int64_t>(W - k) * cap;
+            e = e < need ? need : e;
+            lb[k] = static_cast<int32_t>(e);
+            prev = e;
+        }
+        lb[W] = static_cast<int32_t>(n);
+    }
+    __syncthreads();
+    if (w <= W) wg_rows[w] = lb[w];
+}
+
+}  // namespace
+
+void build_resident_split(BlockedCSR& bk, int64_t max_f, hipStream_t s) {
+    bk.resident_wgs = 0;
+    if (!bk.idx16 || bk.weighted || bk.n <= 0) return;
+    int dev = 0, cus = 0;
+    TG_HIP(hipGetDevice(&dev));
+    TG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int64_t W = std::min<int64_t>(std::min<int64_t>(kResidentPerCU * cus, 1023), bk.n);
+    if (W <= 0 || bk.n > W * kResidentRows) return;
+    bk.wg_rows.reserve(static_cast<size_t>(W + 1) * sizeof(int32_t));
+    resident_split_kernel<<<1, 1024, 0, s>>>(bk.rp, bk.n, bk.vdiag ? 1 : 0, static_cast<int>(W),
+                                             kResidentRows, bk.wg_rows.as<int32_t>());
+    TG_LAUNCH_CHECK();
+    bk.max_phases = ceil_div(std::max<int64_t>(max_f, 1), 32) * bk.n_blocks;
+    bk.phase_count.reserve(static_cast<size_t>(bk.max_phases) * sizeof(int32_t));
+    bk.resident_wgs = W;
 }
 
 void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int64_t ldb,
@@ -632,6 +698,7 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
     require(!epi.max, "blocked aggregation: max is not supported");
     require(!epi.acc && !epi.skip_empty, "blocked aggregation: pass flags are set per block");
     if (bk.n == 0 || f == 0) return;
+    if (resident_ok(bk, f, b, ldb, epi)) return run_aggregate_resident(bk, f, b, ldb, c, ldc, epi, s);
     const int32_t* bci = bk.idx16 ? nullptr : bk.bci.as<int32_t>();
     // attention passes compute their weights (no value stream)
     const float* bv = epi.att_dst == nullptr && bk.weighted ? bk.bv.as<float>() : nullptr;
@@ -668,6 +735,8 @@ void run_aggregate_blocked(const BlockedCSR& bk, int64_t f, const float* b, int6
         // 16-bit indices count from the block's first source row
         const int64_t r0 = bk.idx16 ? blk * bk.rows_per_block : 0;
         const float* bb = b + r0 * (epi.b_tile_stride > 0 ? 32 : ldb);
+        // (the buffer gathers' column 0xFFFF must lie past every block)
+        e.b_rows = bk.idx16 && bk.rows_per_block <= 65535 ? bk.n - r0 : 0;
         if (bk.idx16) {
             e.ci16 = bk.bci.as<uint16_t>();
             if (e.att_dst) e.att_dst = epi.att_dst + r0 * epi.att_heads;

@@ -91,6 +91,7 @@ struct tg_model_s {
     int built_precision = -1;  // precision the cached plans were built for
     int64_t block_rows = -1;   // column blocking (tg_model_set_blocking)
     bool direct_split = true;  // tg_model_set_self_loop_split
+    bool resident = false;     // tg_model_set_resident_passes
     int64_t built_block_rows = -2;  // blocking the blocked copies were built for (-2: none)
 
     // bumped by every add_*_layer: the cached adjacency state (which of
@@ -300,6 +301,7 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         // A + I's blocked copy was split from A by prepare_adjacency
     } else if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
+        m.blk_sl->resident = m.resident && !exact && gc_sl == 32;  // the factored GCN's sums
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() && !m.unit_sl ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s,
                       chunk);
@@ -311,6 +313,7 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const int64_t r_raw = resolve_block_rows(m.block_rows, n, nnz, 32);
     if (m.need_raw_mean() && r_raw > 0) {
         if (!m.blk_raw) m.blk_raw = std::make_unique<BlockedCSR>();
+        m.blk_raw->resident = m.resident && !exact;  // SAGE's mean: plain sums
         build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s, chunk);
         m.blk_raw->group_cols = 32;
         if (exact && !m.blk_raw->in_order) m.blk_raw.reset();
@@ -426,6 +429,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
                                       hipMemcpyDeviceToHost, s));
             }
             if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
+            m.blk_sl->resident = m.resident && gcn_direct;  // (fast precision only)
             // (synchronises s: host[1] is current after the call)
             const bool built =
                 build_blocked_self_loops(*m.blk_sl, n, nnz, rp, ci, r_unit, maxf, s, chunk);
@@ -756,7 +760,8 @@ int tg_model_set_blocking(tg_model_t model, int64_t rows_per_block) {
 }
 
 int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_sl,
-                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct) {
+                           int64_t* blocks_raw, int64_t* cols_raw, int64_t* sl_direct,
+                           int64_t* resident) {
     return guard([&] {
         require(model != nullptr, "model is null");
         const tg::BlockedCSR* sl = model->have_cache ? model->blk_sl.get() : nullptr;
@@ -766,6 +771,8 @@ int tg_model_blocking_info(tg_model_t model, int64_t* blocks_sl, int64_t* cols_s
         if (blocks_raw) *blocks_raw = raw ? raw->n_blocks : 0;
         if (cols_raw) *cols_raw = raw ? raw->group_cols : 0;
         if (sl_direct) *sl_direct = sl && model->blk_sl_direct ? 1 : 0;
+        auto res = [](const tg::BlockedCSR* b) { return b && b->resident_wgs > 0; };
+        if (resident) *resident = (res(sl) ? 1 : 0) | (res(raw) ? 2 : 0);
     });
 }
 
@@ -773,6 +780,14 @@ int tg_model_set_self_loop_split(tg_model_t model, int direct) {
     return guard([&] {
         require(model != nullptr, "model is null");
         model->direct_split = direct != 0;
+        model->have_cache = false;
+    });
+}
+
+int tg_model_set_resident_passes(tg_model_t model, int on) {
+    return guard([&] {
+        require(model != nullptr, "model is null");
+        model->resident = on != 0;
         model->have_cache = false;
     });
 }

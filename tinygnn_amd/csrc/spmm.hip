@@ -1012,10 +1012,39 @@ __device__ __forceinline__ uint32_t put_group(const uint32_t (&d)[8], int gg, ui
     return v;
 }
 
+// A raw buffer load of 16 bytes at byte offset `off` of the range the
+// descriptor covers; an offset past the range's end reads zeros without a
+// memory access.  Descriptor: base address, stride 0, num_records = the
+// range's bytes, and the gfx9 data-format word.
+typedef int BufRsrc __attribute__((ext_vector_type(4)));
+typedef float Float4v __attribute__((ext_vector_type(4)));
+__device__ Float4v raw_buffer_load_f32x4(BufRsrc rsrc, uint32_t voffset, uint32_t soffset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+
+__device__ __forceinline__ BufRsrc buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    BufRsrc r;
+    r.x = static_cast<int>(a & 0xFFFFFFFFu);
+    r.y = static_cast<int>(a >> 32);  // stride 0
+    r.z = static_cast<int>(bytes);
+    r.w = 0x00020000;
+    return r;
+}
+
+// BUF = 0: gathers through 64-bit addresses, slots outside the chunk
+// skipped and masked; BUF = 1 (tile-major B) / 2 (row-major B with rows of
+// less than 2^16 bytes): gathers through buffer loads over B's first
+// min(b_rows, 65535) rows, where the slots outside the chunk take column
+// 0xFFFF, past that range, and read zeros -- added unconditionally (the
+// sums start from +0 or an earlier pass's sum, never -0, so adding +0
+// changes no bit).  Fewer instructions per gathered row (the passes issue
+// their gathers at a higher rate).
+template <int BUF>
 __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
     const int4* __restrict__ chunks, int64_t n_chunks, const int64_t* __restrict__ n_chunks_dev,
     const float* __restrict__ B, int64_t ldb, float* __restrict__ C, int64_t ldc,
     float* __restrict__ partials, int64_t ldp, int64_t f, AggEpilogue epi) {
+    static_assert(BUF >= 0 && BUF <= 2, "gather mode");
     constexpr int LPR = 8, VEC = 4, U = 16;
     const int g = threadIdx.x / LPR;
     const int l = threadIdx.x % LPR;
@@ -1051,6 +1080,17 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
     const char* bl = reinterpret_cast<const char*>(
         epi.b_tile_stride > 0 ? B + (fl >> 5) * epi.b_tile_stride + (fl & 31) : B + fl);
     const uint32_t pitch = static_cast<uint32_t>(ldb) * 4u;
+    // the buffer modes: the tile's first column of B's first row (the same
+    // for the whole workgroup) and the lane's columns as an offset in a row
+    BufRsrc rsrc{};
+    uint32_t laneoff = 0;
+    if constexpr (BUF != 0) {
+        const int64_t rows = epi.b_rows < 65535 ? epi.b_rows : 65535;
+        const float* bt = BUF == 1 ? B + static_cast<int64_t>(blockIdx.y) * epi.b_tile_stride
+                                   : B + fbase;
+        rsrc = buffer_rsrc(bt, static_cast<uint32_t>(rows * pitch));
+        laneoff = ok ? static_cast<uint32_t>(l) * 16u : 0u;
+    }
 
     // the group's batches: 16 entries each from the dword-aligned start
     const int a = ch.y & ~1;
@@ -1084,17 +1124,38 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
         // slots [lo, cnt) of this batch are the group's entries
         const int base = a + 16 * t;
         const int lo = ch.y - base, cnt = ch.z - base;
-        const int c0 = static_cast<int>(packed & 0xFFFFu), c1 = static_cast<int>(packed >> 16);
         float bv[U][VEC];
+        if constexpr (BUF == 0) {
+            const int c0 = static_cast<int>(packed & 0xFFFFu);
+            const int c1 = static_cast<int>(packed >> 16);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int col = __shfl((u & 1) ? c1 : c0, u >> 1, LPR);
-            if (u >= lo && u < cnt) {
-                const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
-                load_vec<VEC>(reinterpret_cast<const float*>(bl + off), bv[u]);
-            } else {
+            for (int u = 0; u < U; ++u) {
+                const int col = __shfl((u & 1) ? c1 : c0, u >> 1, LPR);
+                if (u >= lo && u < cnt) {
+                    const uint64_t off =
+                        static_cast<uint64_t>(static_cast<uint32_t>(col)) * pitch;
+                    load_vec<VEC>(reinterpret_cast<const float*>(bl + off), bv[u]);
+                } else {
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) bv[u][k] = 0.0f;
+                    for (int k = 0; k < VEC; ++k) bv[u][k] = 0.0f;
+                }
+            }
+        } else {
+            // the lane's two slots 2l and 2l + 1: outside the chunk, column
+            // 0xFFFF (past the range: zeros)
+            const uint32_t keep = (2 * l >= lo && 2 * l < cnt ? 0x0000FFFFu : 0u) |
+                                  (2 * l + 1 >= lo && 2 * l + 1 < cnt ? 0xFFFF0000u : 0u);
+            const uint32_t pk = (packed & keep) | ~keep;
+            const uint32_t c0 = pk & 0xFFFFu, c1 = pk >> 16;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t col = static_cast<uint32_t>(__shfl((u & 1) ? c1 : c0, u >> 1, LPR));
+                const uint32_t off = BUF == 1 ? (col << 7) + laneoff : __umul24(col, pitch) + laneoff;
+                const Float4v v = raw_buffer_load_f32x4(rsrc, off, 0u, 0);
+                bv[u][0] = v.x;
+                bv[u][1] = v.y;
+                bv[u][2] = v.z;
+                bv[u][3] = v.w;
             }
         }
         // the next batch's indices, behind this batch's gathers
@@ -1103,11 +1164,16 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool valid = u >= lo && u < cnt;  // a select, not a branch
+            if constexpr (BUF == 0) {
+                const bool valid = u >= lo && u < cnt;  // a select, not a branch
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                const float nx = acc[k] + bv[u][k];
-                acc[k] = valid ? nx : acc[k];
+                for (int k = 0; k < VEC; ++k) {
+                    const float nx = acc[k] + bv[u][k];
+                    acc[k] = valid ? nx : acc[k];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) acc[k] += bv[u][k];
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1120,6 +1186,257 @@ __global__ __launch_bounds__(256, 4) void agg_sidx_kernel(
         finish_store<VEC>(acc, ch.x, ch.z - ch.y, fo, f, C, ldc, epi, false);
     } else {
         store_vec<VEC>(partials + static_cast<int64_t>(ch.w) * ldp + fo, acc);
+    }
+}
+
+// The output-resident passes (run_aggregate_resident).  One 1024-thread
+// workgroup per CU owns rows [R0, R0 + nr) (nr <= kResidentRows) and keeps
+// their running sums for one 32-column tile in LDS, while it walks the
+// column blocks in order: all workgroups start together and have about the
+// same work per block, so they gather from the same block's slice of B
+// (rows_per_block x 128 bytes) at the same time and the slice stays in L2;
+// the output is written once per tile, with the epilogue.  Within a block,
+// the range's entries are contiguous in the blocked copy and are split
+// evenly over the 128 lane groups (8 lanes x 4 columns each, as
+// agg_sidx_kernel's), so heavy rows are shared and every batch of 16
+// entries is full, across row boundaries.  A group walks its entries in
+// order: a row that starts in its share is the group's ("owned"), summed
+// as a chain continued from the row's LDS sum; the part of a row that
+// started in an earlier group's share is summed from zero as a head
+// partial.  After a barrier, the owner of a row that ran past the end of
+// its share adds the later groups' heads of that row in group order.  The
+// split depends on the structure alone, so the sums are deterministic.
+struct ResidentArgs {
+    const int32_t* brp;      // block s's row r at s * n + r
+    const int32_t* wg_rows;  // the workgroups' first rows (gridDim.x + 1)
+    const float* B;
+    int64_t ldb;
+    float* C;
+    int64_t ldc;
+    int64_t n;
+    int64_t f;
+    int64_t rows_per_block;
+    int nb;
+    // per phase (tile x block), the workgroups that finished it (zeroed
+    // before the launch; null: no pacing)
+    int* phase_count;
+};
+
+constexpr int kResGroups = kResidentThreads / 8;  // 8-lane groups of a workgroup
+// Pacing: a workgroup starts phase q + 1 once every workgroup has finished
+// phase q + 1 - kResSlack, so at most kResSlack blocks' slices are being
+// gathered at a time.  The wait is bounded (kResSpin polls); after a
+// time-out (workgroups not all resident) a workgroup stops waiting.  The
+// pacing orders nothing: the sums do not depend on it.
+constexpr int kResSlack = 2;
+constexpr int kResSpin = 4096;
+
+// TILED: B tile-major (rows of 128 bytes: offsets by shift); else
+// row-major with a pitch of less than 2^16 bytes (24-bit multiplies).
+template <bool TILED>
+// (4 waves per SIMD: one workgroup per CU)
+__global__ __launch_bounds__(kResidentThreads, 4) void agg_resident_kernel(
+    ResidentArgs a, AggEpilogue epi) {
+    constexpr int LPR = 8, VEC = 4, U = 16;
+    __shared__ float4 sums[kResidentRows][LPR];
+    __shared__ float4 heads[kResGroups][LPR];
+    __shared__ int brps[kResidentRows + 1];
+    __shared__ int head_row[kResGroups];  // -1: no head; -2: an empty share
+    const int g = threadIdx.x / LPR;
+    const int l = threadIdx.x % LPR;
+    const int R0 = a.wg_rows[blockIdx.x];
+    const int nr = a.wg_rows[blockIdx.x + 1] - R0;
+    const uint32_t pitch = static_cast<uint32_t>(a.ldb) * 4u;  // bytes per row of B
+    // lane p of a group loads entries 2p and 2p + 1 of a batch (one dword)
+    const uint32_t* cw = reinterpret_cast<const uint32_t*>(epi.ci16);
+    const int ntiles = static_cast<int>((a.f + 31) / 32);
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    auto load_rows = [&](int s) {  // block s's row pointers of the range
+        const int32_t* bp = a.brp + static_cast<int64_t>(s) * a.n + R0;
+        for (int i = threadIdx.x; i <= nr; i += kResidentThreads) brps[i] = bp[i];
+    };
+    for (int i = threadIdx.x; i < nr * LPR; i += kResidentThreads) sums[i / LPR][i % LPR] = zero4;
+    load_rows(0);
+    __syncthreads();
+    bool paced = true;  // (thread 0's)
+
+    for (int q = 0; q < ntiles * a.nb; ++q) {
+        const int tile = q / a.nb, s = q % a.nb;
+        const int64_t fbase = static_cast<int64_t>(tile) * 32;
+        const int64_t fo = fbase + static_cast<int64_t>(l) * VEC;
+        const bool ok = fo < a.f;
+        // block s's rows of the tile: a buffer range from the tile's first
+        // column of the block's first row (the same for the whole
+        // workgroup), and the lane's columns as an offset into each row
+        // (lanes past f read the tile's first columns, unused)
+        const int64_t row0 = static_cast<int64_t>(s) * a.rows_per_block;
+        const int64_t rows_s = (a.n - row0 < a.rows_per_block ? a.n - row0 : a.rows_per_block);
+        const float* bt = TILED ? a.B + static_cast<int64_t>(tile) * epi.b_tile_stride + row0 * 32
+                                : a.B + row0 * a.ldb + fbase;
+        const BufRsrc rsrc = buffer_rsrc(bt, static_cast<uint32_t>(rows_s * pitch));
+        const uint32_t laneoff = ok ? static_cast<uint32_t>(l) * 16u : 0u;
+
+        // the group's share [a0, b0) of the range's entries in block s
+        const int E0 = brps[0], L = brps[nr] - E0;
+        const int a0 = E0 + static_cast<int>((static_cast<int64_t>(g) * L) / kResGroups);
+        const int b0 = E0 + static_cast<int>((static_cast<int64_t>(g + 1) * L) / kResGroups);
+        const bool has = a0 < b0;
+        // the row holding entry a0: the last r with brps[r] <= a0
+        int r = 0;
+        if (has) {
+            int lo = 0, hi = nr;  // brps[lo] <= a0 < brps[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (brps[mid] <= a0) lo = mid;
+                else hi = mid;
+            }
+            r = lo;
+        }
+        const int head_r = has && brps[r] < a0 ? r : -1;  // the share starts inside row r
+        int end = has ? brps[r + 1] : 0;
+        float acc[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (has && head_r < 0) {
+            const float4 p4 = sums[r][l];
+            acc[0] = p4.x;
+            acc[1] = p4.y;
+            acc[2] = p4.z;
+            acc[3] = p4.w;
+        }
+        float hacc[VEC] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+        // 16-entry batches from the dword-aligned start of the share
+        const int p0 = a0 & ~1;
+        const int nbt = has ? (b0 - p0 + 15) >> 4 : 0;
+        int nmax = 0;
+#pragma unroll
+        for (int gg = 0; gg < kWave / LPR; ++gg) {
+            const int x = __builtin_amdgcn_readlane(nbt, gg * LPR);
+            nmax = x > nmax ? x : nmax;
+        }
+        // dword offset of batch t (the last batch once done; 0 without any):
+        // every load stays within the share's batches, at most 15 entries
+        // past its end (the blocked copy keeps 64 bytes of padding)
+        auto batch_off = [&](int t) { return nbt > 0 ? (p0 >> 1) + 8 * (t < nbt ? t : nbt - 1) : 0; };
+        uint32_t packed = cw[batch_off(0) + l];
+
+        // where the current row ends, while that is inside the share (else
+        // never: -1)
+        int endv = has && end < b0 ? end : -1;
+        for (int t = 0; t < nmax; ++t) {
+            const int base = p0 + 16 * t;
+            const int lo = a0 - base, cnt = b0 - base;  // slots [lo, cnt) are the share's
+            // the lane's two slots 2l and 2l + 1: outside the share, column
+            // 0xFFFF, past the range (at most 65535 rows): they gather zeros
+            const uint32_t keep = (2 * l >= lo && 2 * l < cnt ? 0x0000FFFFu : 0u) |
+                                  (2 * l + 1 >= lo && 2 * l + 1 < cnt ? 0xFFFF0000u : 0u);
+            const uint32_t pk = (packed & keep) | ~keep;
+            const uint32_t c0 = pk & 0xFFFFu, c1 = pk >> 16;
+            Float4v bv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t col = static_cast<uint32_t>(__shfl((u & 1) ? c1 : c0, u >> 1, LPR));
+                const uint32_t off = TILED ? (col << 7) + laneoff : __umul24(col, pitch) + laneoff;
+                bv[u] = raw_buffer_load_f32x4(rsrc, off, 0u, 0);
+            }
+            // the next batch's indices, behind this batch's gathers
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t next = cw[batch_off(t + 1) + l];
+            __builtin_amdgcn_sched_barrier(0);
+            int dend = endv - base;  // the slot where the current row ends (if in 0..15)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (dend == u) {
+                    // row r ends before this entry: keep its sum, move on to
+                    // the row holding the entry (past rows without entries)
+                    if (r == head_r) {
+#pragma unroll
+                        for (int k = 0; k < VEC; ++k) hacc[k] = acc[k];
+                    } else {
+                        sums[r][l] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                    }
+                    int r2 = r + 1;
+                    while (brps[r2 + 1] == end) ++r2;
+                    r = r2;
+                    end = brps[r2 + 1];
+                    endv = end < b0 ? end : -1;
+                    dend = endv - base;
+                    const float4 p4 = sums[r2][l];
+                    acc[0] = p4.x;
+                    acc[1] = p4.y;
+                    acc[2] = p4.z;
+                    acc[3] = p4.w;
+                }
+                // (slots outside the share add zeros)
+                acc[0] += bv[u].x;
+                acc[1] += bv[u].y;
+                acc[2] += bv[u].z;
+                acc[3] += bv[u].w;
+            }
+            packed = next;
+        }
+
+        // the share's last row: a head (the share lies inside it) or owned;
+        // an owned row that runs past the share's end collects the heads
+        int tail = -1;
+        if (has) {
+            if (r == head_r) {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) hacc[k] = acc[k];
+            } else {
+                sums[r][l] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                if (end > b0) tail = r;
+            }
+        }
+        heads[g][l] = make_float4(hacc[0], hacc[1], hacc[2], hacc[3]);
+        if (l == 0) head_row[g] = has ? head_r : -2;
+        __syncthreads();
+        if (tail >= 0) {
+            const float4 p4 = sums[tail][l];
+            float x[VEC] = {p4.x, p4.y, p4.z, p4.w};
+            for (int g2 = g + 1; g2 < kResGroups; ++g2) {
+                const int hr = head_row[g2];
+                if (hr == -2) continue;  // an empty share
+                if (hr != tail) break;
+                const float4 h4 = heads[g2][l];
+                x[0] += h4.x;
+                x[1] += h4.y;
+                x[2] += h4.z;
+                x[3] += h4.w;
+            }
+            sums[tail][l] = make_float4(x[0], x[1], x[2], x[3]);
+        }
+        if (s == a.nb - 1) {
+            // the tile is complete: store it with the epilogue
+            __syncthreads();
+            if (ok) {
+                for (int rr = g; rr < nr; rr += kResGroups) {
+                    const float4 p4 = sums[rr][l];
+                    float x[VEC] = {p4.x, p4.y, p4.z, p4.w};
+                    finish_store<VEC>(x, R0 + rr, 0, fo, a.f, a.C, a.ldc, epi, false);
+                }
+            }
+            __syncthreads();
+            if (q + 1 < ntiles * a.nb)
+                for (int i = threadIdx.x; i < nr * LPR; i += kResidentThreads) sums[i / LPR][i % LPR] = zero4;
+        }
+        if (q + 1 < ntiles * a.nb) load_rows((q + 1) % a.nb);
+        if (threadIdx.x == 0 && a.phase_count != nullptr) {
+            atomicAdd(a.phase_count + q, 1);
+            const int wait_q = q + 1 - kResSlack;
+            if (paced && q + 1 < ntiles * a.nb && wait_q >= 0) {
+                int it = 0;
+                while (__hip_atomic_load(a.phase_count + wait_q, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) < static_cast<int>(gridDim.x)) {
+                    if (++it == kResSpin) {
+                        paced = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -1411,8 +1728,20 @@ void launch_agg_sidx(const PlanView& p, const LaneLayout& L, int64_t f, const fl
     if (p.n_chunks > 0) {
         dim3 grid(static_cast<unsigned>(ceil_div(p.n_chunks, GPB)),
                   static_cast<unsigned>(L.n_tiles));
-        agg_sidx_kernel<<<grid, 256, 0, s>>>(p.chunks, p.n_chunks, dc, B, ldb, C, ldc,
-                                             p.partials, ldp, f, epi);
+        // buffer gathers where column 0xFFFF lies past B's rows (blocks of
+        // at most 65535 rows) and a row's offsets fit 32 bits
+        const bool tiled = epi.b_tile_stride > 0;
+        const bool buf = epi.b_rows > 0 && (tiled ? ldb == 32 : ldb < 16384) &&
+                         reinterpret_cast<uintptr_t>(B) % 16 == 0;
+        if (buf && tiled)
+            agg_sidx_kernel<1><<<grid, 256, 0, s>>>(p.chunks, p.n_chunks, dc, B, ldb, C, ldc,
+                                                    p.partials, ldp, f, epi);
+        else if (buf)
+            agg_sidx_kernel<2><<<grid, 256, 0, s>>>(p.chunks, p.n_chunks, dc, B, ldb, C, ldc,
+                                                    p.partials, ldp, f, epi);
+        else
+            agg_sidx_kernel<0><<<grid, 256, 0, s>>>(p.chunks, p.n_chunks, dc, B, ldb, C, ldc,
+                                                    p.partials, ldp, f, epi);
         TG_LAUNCH_CHECK();
     }
     if (p.n_split > 0 && !epi.long_rows) {
@@ -1503,6 +1832,59 @@ void run_aggregate(const PlanView& p, int64_t f, const int32_t* ci, const float*
     }
     TG_AGG_MODE(kAggSum)
 #undef TG_AGG_MODE
+}
+
+bool resident_ok(const BlockedCSR& bk, int64_t f, const float* B, int64_t ldb,
+                 const AggEpilogue& epi) {
+    // (column 0xFFFF must lie past every block: at most 65535 rows per block)
+    if (bk.resident_wgs <= 0 || !bk.idx16 || bk.weighted || bk.group_cols != 32 ||
+        bk.rows_per_block > 65535)
+        return false;
+    if (epi.max || epi.att_dst || f <= 0) return false;
+    const bool tiled = epi.b_tile_stride > 0;
+    if (tiled) return ldb == 32 && epi.b_tile_stride % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(B) % 16 == 0;
+    // row-major: rows of less than 2^16 bytes (24-bit offsets)
+    return ldb % 4 == 0 && ldb >= round_up(f, 4) && ldb < 16384 &&
+           reinterpret_cast<uintptr_t>(B) % 16 == 0;
+}
+
+void run_aggregate_resident(const BlockedCSR& bk, int64_t f, const float* B, int64_t ldb,
+                            float* C, int64_t ldc, const AggEpilogue& epi, hipStream_t s) {
+    require(resident_ok(bk, f, B, ldb, epi), "resident aggregation: unsupported pass");
+    require(!epi.acc && !epi.skip_empty, "resident aggregation: pass flags are internal");
+    require(ldc >= f, "aggregate: leading dimension smaller than f");
+    require(epi.self == nullptr || (epi.self_tile_stride > 0 ? epi.ld_self == 32
+                                                              : epi.ld_self >= f),
+            "aggregate: self ld smaller than f");
+    if (bk.n == 0 || f == 0) return;
+    AggEpilogue e = epi;
+    e.ci16 = bk.bci.as<uint16_t>();
+    if (e.mean) e.deg_rp = bk.rp;
+    e.vec_io = pick_vec(f, {ldc, epi.self ? epi.ld_self : 4}, {C, epi.self, epi.bias}) >= 4;
+    ResidentArgs a{};
+    a.brp = bk.brp.as<int32_t>();
+    a.wg_rows = bk.wg_rows.as<int32_t>();
+    a.B = B;
+    a.ldb = ldb;
+    a.C = C;
+    a.ldc = ldc;
+    a.n = bk.n;
+    a.f = f;
+    a.rows_per_block = bk.rows_per_block;
+    a.nb = static_cast<int>(bk.n_blocks);
+    const int64_t phases = ceil_div(f, 32) * bk.n_blocks;
+    if (phases <= bk.max_phases) {
+        a.phase_count = bk.phase_count.as<int>();
+        fill_i32(a.phase_count, phases, 0, s);
+    }
+    if (epi.b_tile_stride > 0)
+        agg_resident_kernel<true>
+            <<<static_cast<unsigned>(bk.resident_wgs), kResidentThreads, 0, s>>>(a, e);
+    else
+        agg_resident_kernel<false>
+            <<<static_cast<unsigned>(bk.resident_wgs), kResidentThreads, 0, s>>>(a, e);
+    TG_LAUNCH_CHECK();
 }
 
 }  // namespace tg
