@@ -49,11 +49,25 @@ void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* 
                     const BlockedCSR* blocked = nullptr);
 size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
                        int64_t nnz);
+// t_pre (transform-first only, optional): T = H * [Ws | 0 | Wn | 0]
+// already computed by sage_transform with the same `tiled` layout the call
+// picks (sage_tf_tiled); the call then starts at the aggregation.
 void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_out, int agg,
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
                   size_t work_bytes, hipStream_t s, int gemm_algo = TG_GEMM_AUTO,
-                  const BlockedCSR* blocked = nullptr);
+                  const BlockedCSR* blocked = nullptr, const float* t_pre = nullptr);
+// The resolved dataflow (TG_SAGE_AUTO decided as sage_forward does).
+int sage_dataflow_for(int dataflow, int agg, int64_t f_in, int64_t f_out, int64_t nnz);
+// Transform-first: whether T is stored tile-major (a blocked aggregation
+// over 32-column tiles), and T's size in floats.
+bool sage_tf_tiled(int64_t f_out, bool blocked);
+int64_t sage_tf_floats(int64_t n, int64_t f_out);
+// T = H * [Ws | 0 | Wn | 0] into t (sage_tf_floats(n, f_out) floats), with
+// wcat (f_in x 2 gather_pitch(f_out) floats) as the concatenated weights.
+void sage_transform(int64_t n, int64_t f_in, int64_t f_out, const float* h, const float* wn,
+                    const float* ws, bool tiled, float* t, float* wcat, hipStream_t s,
+                    int gemm_algo);
 
 // gat.hip
 void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ldwh,

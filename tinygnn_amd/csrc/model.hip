@@ -128,6 +128,24 @@ struct tg_model_s {
     // per-forward buffers
     DeviceBuffer act[2], tmp, scores, work;
 
+    // Layer 0's transform (X * W, for GAT also its scores), computed on a
+    // side stream while the per-call preprocessing of the adjacency runs on
+    // the caller's stream, which it synchronises; the caller's stream waits
+    // for it before the aggregation (pre_*: its outputs)
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    DeviceBuffer pre, pre_w, pre_dis, pre_flag;
+
+    tg_model_s() = default;
+    tg_model_s(const tg_model_s&) = delete;
+    tg_model_s& operator=(const tg_model_s&) = delete;
+    ~tg_model_s() {
+        if (side) (void)hipStreamSynchronize(side);
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
+        if (side) (void)hipStreamDestroy(side);
+    }
+
     bool need_norm() const {
         for (auto& l : layers) if (l.type == LType::GCN) return true;
         return false;
@@ -335,8 +353,10 @@ void ensure_plan_sl(tg_model_s& m, int64_t n, int64_t nnz, hipStream_t s) {
     m.plan_sl_built = true;
 }
 
-void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
-                       const int32_t* ci, const float* v, int mode, hipStream_t s) {
+// Whether the forward can keep the cached adjacency state (prepare_adjacency
+// then rebuilds at most the blocked copies).
+bool adjacency_cached(const tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
+                      const int32_t* ci, const float* v, int mode) {
     const bool same = m.have_cache && m.key_rp == rp && m.key_ci == ci && m.key_v == v &&
                       m.key_n == n && m.key_nnz == nnz && m.built_precision == m.precision &&
                       m.built_layers_gen == m.layers_gen;
@@ -344,7 +364,12 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     // were skipped for the factored path (an unblocked GCN needs them), or
     // A + I's blocked copy came straight from A (A + I was not written)
     const bool values_ok = (m.sl_values || !m.need_norm()) && !m.blk_sl_direct;
-    if (mode == TG_FORWARD_CACHED && same && (values_ok || m.built_block_rows == m.block_rows)) {
+    return mode == TG_FORWARD_CACHED && same && (values_ok || m.built_block_rows == m.block_rows);
+}
+
+void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
+                       const int32_t* ci, const float* v, int mode, hipStream_t s) {
+    if (adjacency_cached(m, n, nnz, rp, ci, v, mode)) {
         // a cached call after a reference-mode one (or a new blocking
         // setting) adds the blocked copies to the state it reuses
         if (m.built_block_rows != m.block_rows) {
@@ -489,6 +514,125 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     if (m.need_norm() || m.need_sl()) ensure_plan_sl(m, n, nnz, s);
 }
 
+// GAT's scores buffer: src and dst scores [n x heads], then the blocked
+// path's row statistics or softmax state [n x slots]
+size_t scores_bytes(const tg_model_s& m, int64_t n) {
+    int64_t heads_max = 1, slots_max = 1;
+    for (auto& l : m.layers) {
+        heads_max = std::max(heads_max, l.heads);
+        if (l.type == LType::GAT) slots_max = std::max(slots_max, gat_stat_slots(l.heads, l.out));
+    }
+    return static_cast<size_t>(2 * heads_max + 2 * slots_max) * n * sizeof(float) + 256;
+}
+
+// Layer 0's transform beside the preprocessing: what it computed, in which
+// layout.  The layout is the one the preprocessing most likely leads to
+// (blocked where the default blocking applies; for GCN in fast precision, a
+// unit A + I split from A directly: the factored aggregation); `matches`
+// checks it against the preprocessing's outcome, and layer 0 recomputes
+// the transform when it differs.
+struct PreTransform {
+    bool on = false;
+    bool tiled = false;     // GCN / SAGE: T tile-major
+    bool factored = false;  // GCN: rows scaled by D^-1/2
+};
+
+PreTransform launch_pre_transform(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
+                                  const float* x, hipStream_t s) {
+    PreTransform p;
+    const Layer& l = m.layers[0];
+    const bool exact = m.precision == TG_PRECISION_EXACT;
+    const int algo = exact ? TG_GEMM_INORDER : TG_GEMM_AUTO;
+    const bool sage_tf =
+        l.type == LType::SAGE &&
+        sage_dataflow_for(exact ? TG_SAGE_CONCAT : m.sage_dataflow, l.agg, l.in, l.out, nnz) ==
+            TG_SAGE_TRANSFORM_FIRST;
+    if (l.type == LType::SAGE && !sage_tf) return p;  // (the aggregation comes first)
+    if (!m.side) {
+        TG_HIP(hipStreamCreateWithFlags(&m.side, hipStreamNonBlocking));
+        TG_HIP(hipEventCreateWithFlags(&m.ev_fork, hipEventDisableTiming));
+        TG_HIP(hipEventCreateWithFlags(&m.ev_join, hipEventDisableTiming));
+    }
+    // buffers first (a reallocation must not meet work in flight)
+    if (l.type == LType::GCN) {
+        const int gc = (!exact && !m.need_sl()) ? 32 : 64;
+        p.tiled = resolve_block_rows(m.block_rows, n, nnz + n, gc) > 0;
+        p.factored = p.tiled && !exact && !m.need_sl();
+        m.pre.reserve(n * round_up(gather_pitch(l.out), 32) * sizeof(float));
+        if (p.factored) {
+            m.pre_dis.reserve(n * sizeof(float));
+            m.pre_flag.reserve(sizeof(int32_t));
+        }
+    } else if (l.type == LType::GAT) {
+        m.pre.reserve(n * gather_pitch(l.wide()) * sizeof(float));
+        m.scores.reserve(scores_bytes(m, n));
+    } else {
+        p.tiled = sage_tf_tiled(l.out, l.agg == TG_AGG_MEAN &&
+                                           resolve_block_rows(m.block_rows, n, nnz, 32) > 0);
+        m.pre.reserve(sage_tf_floats(n, l.out) * sizeof(float));
+        m.pre_w.reserve(l.in * 2 * gather_pitch(l.out) * sizeof(float));
+    }
+    hipStream_t t = m.side;
+    TG_HIP(hipEventRecord(m.ev_fork, s));
+    TG_HIP(hipStreamWaitEvent(t, m.ev_fork, 0));
+    if (l.type == LType::GCN) {
+        if (p.factored) {
+            fill_i32(m.pre_flag.as<int32_t>(), 1, 0, t);
+            unit_self_loop_dis(n, rp, m.pre_dis.as<float>(), m.pre_flag.as<int32_t>(), t);
+        }
+        GemmArgs g;
+        g.m = n;
+        g.n = l.out;
+        g.a1 = x;
+        g.lda1 = l.in;
+        g.b1 = l.w.as<float>();
+        g.ldb1 = l.out;
+        g.k1 = l.in;
+        g.c = m.pre.as<float>();
+        g.ldc = p.tiled ? 32 : gather_pitch(l.out);
+        g.c_tile_stride = p.tiled ? n * 32 : 0;
+        if (p.factored) g.row_scale = m.pre_dis.as<float>();
+        gemm(g, algo, t);
+    } else if (l.type == LType::GAT) {
+        const int64_t wide = l.wide(), ldwh = gather_pitch(wide);
+        GemmArgs g;
+        g.m = n;
+        g.n = wide;
+        g.a1 = x;
+        g.lda1 = l.in;
+        g.b1 = l.w.as<float>();
+        g.ldb1 = wide;
+        g.k1 = l.in;
+        g.c = m.pre.as<float>();
+        g.ldc = ldwh;
+        gemm(g, algo, t);
+        float* src = m.scores.as<float>();
+        gat_scores(n, l.heads, l.out, m.pre.as<float>(), ldwh, l.al.as<float>(),
+                   l.ar.as<float>(), src, src + n * l.heads, t);
+    } else {
+        sage_transform(n, l.in, l.out, x, l.wn.as<float>(), l.ws.as<float>(), p.tiled,
+                       m.pre.as<float>(), m.pre_w.as<float>(), t, algo);
+    }
+    TG_HIP(hipEventRecord(m.ev_join, t));
+    p.on = true;
+    return p;
+}
+
+// Whether the side stream's transform has the layout layer 0 needs after
+// the preprocessing.
+bool pre_matches(const tg_model_s& m, const PreTransform& p) {
+    if (!p.on) return false;
+    const Layer& l = m.layers[0];
+    if (l.type == LType::GCN) {
+        const bool tiled = m.blk_sl != nullptr;
+        const bool factored = tiled && m.unit_sl;
+        // (a factored transform's D^-1/2 is the one the direct split checked)
+        return tiled == p.tiled && factored == p.factored && (!factored || m.blk_sl_direct);
+    }
+    if (l.type == LType::SAGE) return sage_tf_tiled(l.out, m.blk_raw != nullptr) == p.tiled;
+    return true;
+}
+
 void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int32_t* ci,
              const float* v, int64_t f_in, const float* x, float* out, int mode, hipStream_t s) {
     if (m.layers.empty()) throw std::runtime_error("Model::forward: no layers configured.");
@@ -519,7 +663,13 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     require(rp && x && out, "Model::forward: null pointer");
     require(nnz == 0 || (ci && v), "Model::forward: null pointer");
 
+    // a full preprocessing of the adjacency (every reference-semantics call):
+    // layer 0's transform runs beside it on the side stream
+    PreTransform pre;
+    if (!adjacency_cached(m, n, nnz, rp, ci, v, mode)) pre = launch_pre_transform(m, n, nnz, rp, x, s);
     prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
+    if (pre.on) TG_HIP(hipStreamWaitEvent(s, m.ev_join, 0));
+    const bool use_pre = pre_matches(m, pre);
 
     // precision: the exact mode keeps the reference's operation order
     const bool exact = m.precision == TG_PRECISION_EXACT;
@@ -528,11 +678,8 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
 
     // buffers
     const int64_t wmax = m.max_wide();
-    int64_t heads_max = 1, slots_max = 1;
     size_t ws = 0;
     for (auto& l : m.layers) {
-        heads_max = std::max(heads_max, l.heads);
-        if (l.type == LType::GAT) slots_max = std::max(slots_max, gat_stat_slots(l.heads, l.out));
         if (l.type == LType::SAGE)
             ws = std::max(ws, sage_forward_ws(n, l.in, l.out, l.agg, dataflow, nnz));
         if (l.type == LType::GAT)
@@ -545,9 +692,7 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     // the transform's output: row-major at gather_pitch, or tile-major (32-column
     // tiles of n rows) for the blocked aggregations
     m.tmp.reserve(n * round_up(gather_pitch(wmax), 32) * sizeof(float));
-    // GAT: src and dst scores [n x heads], then the blocked path's row
-    // statistics or softmax state [n x slots]
-    m.scores.reserve((2 * heads_max + 2 * slots_max) * n * sizeof(float) + 256);
+    m.scores.reserve(scores_bytes(m, n));
     m.work.reserve(ws);
 
     const float* h = x;
@@ -559,25 +704,28 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             // H*W, then A_norm * (H*W) + b -> act -> post  (layers.cpp:319-336);
             // H*W's rows are padded (gather_pitch) for 128-bit, line-aligned gathers
             // (blocked: tile-major, each 32-column tile one slab of n rows)
-            float* hw = m.tmp.as<float>();
             const bool tiled = m.blk_sl != nullptr;
             // factored (unit A + I, blocked): D^-1/2 in the GEMM's and the
             // aggregation's stores, an unweighted blocked copy
             const bool factored = tiled && m.unit_sl;
             const int64_t ldhw = tiled ? 32 : gather_pitch(l.out);
-            GemmArgs g;
-            g.m = n;
-            g.n = l.out;
-            g.a1 = h;
-            g.lda1 = l.in;
-            g.b1 = l.w.as<float>();
-            g.ldb1 = l.out;
-            g.k1 = l.in;
-            g.c = hw;
-            g.ldc = ldhw;
-            g.c_tile_stride = tiled ? n * 32 : 0;
-            if (factored) g.row_scale = m.dis.as<float>();
-            gemm(g, algo, s);
+            // (layer 0: computed beside the preprocessing, same layout)
+            float* hw = li == 0 && use_pre ? m.pre.as<float>() : m.tmp.as<float>();
+            if (!(li == 0 && use_pre)) {
+                GemmArgs g;
+                g.m = n;
+                g.n = l.out;
+                g.a1 = h;
+                g.lda1 = l.in;
+                g.b1 = l.w.as<float>();
+                g.ldb1 = l.out;
+                g.k1 = l.in;
+                g.c = hw;
+                g.ldc = ldhw;
+                g.c_tile_stride = tiled ? n * 32 : 0;
+                if (factored) g.row_scale = m.dis.as<float>();
+                gemm(g, algo, s);
+            }
             AggEpilogue epi;
             if (factored) {
                 epi.row_scale = m.dis.as<float>();
@@ -598,29 +746,33 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
             sage_forward(*m.plan_raw, n, l.in, l.out, l.agg, ci, h, l.wn.as<float>(),
                          l.ws.as<float>(), l.bias ? l.b.as<float>() : nullptr, l.act, l.post,
                          dataflow, y, m.work.get(), m.work.size(), s, algo,
-                         l.agg == TG_AGG_MEAN ? m.blk_raw.get() : nullptr);
+                         l.agg == TG_AGG_MEAN ? m.blk_raw.get() : nullptr,
+                         li == 0 && use_pre ? m.pre.as<float>() : nullptr);
         } else {
             const int64_t wide = l.heads * l.out;
             // line-aligned rows for the gathers (row-major: the score kernel
             // reads each row's heads; a tile-major Wh measured 0.3 ms slower)
             const bool blocked = m.blk_sl != nullptr && gat_blocked_ok(l.heads, l.out, l.concat);
             const int64_t ldwh = gather_pitch(wide);
-            float* wh = m.tmp.as<float>();
-            GemmArgs g;
-            g.m = n;
-            g.n = wide;
-            g.a1 = h;
-            g.lda1 = l.in;
-            g.b1 = l.w.as<float>();
-            g.ldb1 = wide;
-            g.k1 = l.in;
-            g.c = wh;
-            g.ldc = ldwh;
-            gemm(g, algo, s);
+            // (layer 0: computed beside the preprocessing, scores included)
+            float* wh = li == 0 && use_pre ? m.pre.as<float>() : m.tmp.as<float>();
             float* src = m.scores.as<float>();
             float* dst = src + n * l.heads;
-            gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src, dst,
-                       s);
+            if (!(li == 0 && use_pre)) {
+                GemmArgs g;
+                g.m = n;
+                g.n = wide;
+                g.a1 = h;
+                g.lda1 = l.in;
+                g.b1 = l.w.as<float>();
+                g.ldb1 = wide;
+                g.k1 = l.in;
+                g.c = wh;
+                g.ldc = ldwh;
+                gemm(g, algo, s);
+                gat_scores(n, l.heads, l.out, wh, ldwh, l.al.as<float>(), l.ar.as<float>(), src,
+                           dst, s);
+            }
             if (blocked) {
                 float* rmax = dst + n * l.heads;
                 float* rinv = rmax + n * gat_stat_slots(l.heads, l.out);

@@ -62,6 +62,44 @@ void sage_aggregate(const tg_spmm_plan_s& p, int64_t f, int agg, const int32_t* 
     }
 }
 
+int sage_dataflow_for(int dataflow, int agg, int64_t f_in, int64_t f_out, int64_t nnz) {
+    return resolve_dataflow(dataflow, agg, f_in, f_out, nnz);
+}
+
+bool sage_tf_tiled(int64_t f_out, bool blocked) { return blocked && gather_pitch(f_out) % 32 == 0; }
+
+int64_t sage_tf_floats(int64_t n, int64_t f_out) { return n * 2 * gather_pitch(f_out); }
+
+void sage_transform(int64_t n, int64_t f_in, int64_t f_out, const float* h, const float* wn,
+                    const float* ws, bool tiled, float* t, float* wcat, hipStream_t s,
+                    int gemm_algo) {
+    // [Ws | 0 | Wn | 0]: each half padded to fp = gather_pitch(f_out)
+    // columns, so the neighbour half's rows start line-aligned and are
+    // gathered with 128-bit loads; the zero columns make the GEMM write
+    // zeros into the padding.
+    const int64_t fp = gather_pitch(f_out);
+    if (fp != f_out) fill_zero_2d(wcat, f_in, 2 * fp, 2 * fp, s);
+    TG_HIP(hipMemcpy2DAsync(wcat, 2 * fp * sizeof(float), ws, f_out * sizeof(float),
+                            f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
+    TG_HIP(hipMemcpy2DAsync(wcat + fp, 2 * fp * sizeof(float), wn, f_out * sizeof(float),
+                            f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
+    // The blocked passes gather T tile-major (32-column tiles of n rows
+    // each, the GEMM's store layout): a tile's rows are one contiguous
+    // slab instead of lines 2 fp floats apart.
+    GemmArgs g;
+    g.m = n;
+    g.n = 2 * fp;
+    g.a1 = h;
+    g.lda1 = f_in;
+    g.b1 = wcat;
+    g.ldb1 = 2 * fp;
+    g.k1 = f_in;
+    g.c = t;
+    g.ldc = tiled ? 32 : 2 * fp;
+    g.c_tile_stride = tiled ? n * 32 : 0;
+    gemm(g, gemm_algo, s);
+}
+
 size_t sage_forward_ws(int64_t n, int64_t f_in, int64_t f_out, int agg, int dataflow,
                        int64_t nnz) {
     return sage_ws(n, f_in, f_out, resolve_dataflow(dataflow, agg, f_in, f_out, nnz));
@@ -71,7 +109,7 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
                   const int32_t* ci, const float* h, const float* wn, const float* ws,
                   const float* bias, int act, int post, int dataflow, float* out, void* work,
                   size_t work_bytes, hipStream_t s, int gemm_algo,
-                  const BlockedCSR* blocked) {
+                  const BlockedCSR* blocked, const float* t_pre) {
     require(n == p.m, "SAGELayer::forward: plan rows differ from n");
     require(f_in >= 0 && f_out >= 0, "SAGELayer::forward: negative size");
     require(act == TG_ACT_NONE || act == TG_ACT_RELU, "SAGELayer: unknown activation");
@@ -140,34 +178,14 @@ void sage_forward(const tg_spmm_plan_s& p, int64_t n, int64_t f_in, int64_t f_ou
         gemm(g, gemm_algo, s);
         add_bias_act(out, n, f_out, f_out, nullptr, TG_ACT_NONE, post, s);
     } else {
-        // [Ws | 0 | Wn | 0]: each half padded to fp = gather_pitch(f_out)
-        // columns, so the neighbour half's rows start line-aligned and are
-        // gathered with 128-bit loads; the zero columns make the GEMM write
-        // zeros into the padding.
         const int64_t fp = gather_pitch(f_out);
         float* t = c.take<float>(n * 2 * fp);
         float* wcat = c.take<float>(f_in * 2 * fp);
-        if (fp != f_out) fill_zero_2d(wcat, f_in, 2 * fp, 2 * fp, s);
-        TG_HIP(hipMemcpy2DAsync(wcat, 2 * fp * sizeof(float), ws, f_out * sizeof(float),
-                                f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
-        TG_HIP(hipMemcpy2DAsync(wcat + fp, 2 * fp * sizeof(float), wn, f_out * sizeof(float),
-                                f_out * sizeof(float), f_in, hipMemcpyDeviceToDevice, s));
-        // The blocked passes gather T tile-major (32-column tiles of n rows
-        // each, the GEMM's store layout): a tile's rows are one contiguous
-        // slab instead of lines 2 fp floats apart.
-        const bool tiled = blocked != nullptr && fp % 32 == 0;
-        GemmArgs g;
-        g.m = n;
-        g.n = 2 * fp;
-        g.a1 = h;
-        g.lda1 = f_in;
-        g.b1 = wcat;
-        g.ldb1 = 2 * fp;
-        g.k1 = f_in;
-        g.c = t;
-        g.ldc = tiled ? 32 : 2 * fp;
-        g.c_tile_stride = tiled ? n * 32 : 0;
-        gemm(g, gemm_algo, s);
+        const bool tiled = sage_tf_tiled(f_out, blocked != nullptr);
+        if (t_pre != nullptr)
+            t = const_cast<float*>(t_pre);  // (read only from here on)
+        else
+            sage_transform(n, f_in, f_out, h, wn, ws, tiled, t, wcat, s, gemm_algo);
         AggEpilogue epi;
         epi.mean = 1;
         epi.self = t;
@@ -224,7 +242,7 @@ int tg_sage_forward(tg_spmm_plan_t plan, int64_t n, int64_t f_in, int64_t f_out,
         require(row_ptr == plan->row_ptr, "SAGELayer::forward: row_ptr differs from the plan's");
         tg::sage_forward(*plan, n, f_in, f_out, agg, col_ind, h, w_neigh, w_self, bias, act, post,
                          dataflow, out, workspace, workspace_bytes,
-                         static_cast<hipStream_t>(stream), TG_GEMM_AUTO, nullptr);
+                         static_cast<hipStream_t>(stream), TG_GEMM_AUTO, nullptr, nullptr);
     });
 }
 
