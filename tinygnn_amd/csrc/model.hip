@@ -663,10 +663,12 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     require(rp && x && out, "Model::forward: null pointer");
     require(nnz == 0 || (ci && v), "Model::forward: null pointer");
 
-    // a full preprocessing of the adjacency (every reference-semantics call):
-    // layer 0's transform runs beside it on the side stream
+    // a reference-semantics call preprocesses the adjacency every time:
+    // layer 0's transform runs beside it on the side stream (a cached call's
+    // one-time build keeps the single stream, and allocates no side buffers)
     PreTransform pre;
-    if (!adjacency_cached(m, n, nnz, rp, ci, v, mode)) pre = launch_pre_transform(m, n, nnz, rp, x, s);
+    if (mode == TG_FORWARD_REFERENCE && !adjacency_cached(m, n, nnz, rp, ci, v, mode))
+        pre = launch_pre_transform(m, n, nnz, rp, x, s);
     prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
     if (pre.on) TG_HIP(hipStreamWaitEvent(s, m.ev_join, 0));
     const bool use_pre = pre_matches(m, pre);
