@@ -21,6 +21,9 @@ namespace tg {
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+// 128-bit loads at any dword address (gfx950's global loads take them
+// unaligned)
+typedef float Float4Dw __attribute__((ext_vector_type(4), aligned(4)));
 
 // Element (m, n) of the output, row-major or tile-major (GemmArgs).
 __device__ __forceinline__ int64_t c_index(const GemmArgs& g, int64_t m, int64_t n) {
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
             const float* pa = A + (gm < M ? gm : 0) * lda + ka;
             const int64_t va = gm < M ? K - ka : 0;
             if (VA == 4 && va >= 4) {
-                const float4 t = *reinterpret_cast<const float4*>(pa);
+                const Float4Dw t = *reinterpret_cast<const Float4Dw*>(pa);
                 ra[p][0] = t.x; ra[p][1] = t.y; ra[p][2] = t.z; ra[p][3] = t.w;
             } else {
 #pragma unroll
@@ -409,8 +412,8 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
             const int64_t kb = k0 + bk, nb = n0 + bn;
             const float* pb = B + (kb < K ? kb : 0) * ldb + nb;
             const int64_t vb = kb < K ? N - nb : 0;
-            if (vb >= 4 && (ldb % 4) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0) {
-                const float4 t = *reinterpret_cast<const float4*>(pb);
+            if (vb >= 4) {
+                const Float4Dw t = *reinterpret_cast<const Float4Dw*>(pb);
                 rb[p][0] = t.x; rb[p][1] = t.y; rb[p][2] = t.z; rb[p][3] = t.w;
             } else {
 #pragma unroll
@@ -515,7 +518,10 @@ constexpr int kMLDA = kMBK + 4;   // A tile pitch (floats): 16-byte aligned rows
 constexpr int kMLDB = kMBN + 4;   // B tile pitch
 
 // Loads 8 consecutive floats p[0..7] of which the first `valid` exist
-// (valid <= 0: none), with V-wide accesses when all 8 exist.
+// (valid <= 0: none), with V-wide accesses when all 8 exist.  V = 4 needs
+// 4-byte alignment only: gfx950's global loads take a 128-bit access at
+// any dword address (config-E transform, 602-float rows of A at 8-byte
+// alignment: 128-bit loads 0.68 ms, 64-bit 0.72 ms).
 template <int V>
 __device__ __forceinline__ void load8(const float* __restrict__ p, int64_t valid,
                                       float (&x)[8]) {
@@ -523,7 +529,7 @@ __device__ __forceinline__ void load8(const float* __restrict__ p, int64_t valid
 #pragma unroll
         for (int u = 0; u < 8; u += V) {
             if constexpr (V == 4) {
-                const float4 t = *reinterpret_cast<const float4*>(p + u);
+                const Float4Dw t = *reinterpret_cast<const Float4Dw*>(p + u);
                 x[u] = t.x;
                 x[u + 1] = t.y;
                 x[u + 2] = t.z;
@@ -677,8 +683,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_thin_kernel(GemmArgs g) {
             const int64_t gm = m0 + 16 * i + r;
             const float* p = A + (gm < M ? gm : 0) * lda + (kv > 0 ? k : 0);
             if (ALIGNED && gm < M && kv >= 8) {
-                const float4 x0 = *reinterpret_cast<const float4*>(p);
-                const float4 x1 = *reinterpret_cast<const float4*>(p + 4);
+                const Float4Dw x0 = *reinterpret_cast<const Float4Dw*>(p);
+                const Float4Dw x1 = *reinterpret_cast<const Float4Dw*>(p + 4);
                 ra[i][0] = x0.x; ra[i][1] = x0.y; ra[i][2] = x0.z; ra[i][3] = x0.w;
                 ra[i][4] = x1.x; ra[i][5] = x1.y; ra[i][6] = x1.z; ra[i][7] = x1.w;
             } else {
@@ -770,8 +776,8 @@ __global__ __launch_bounds__(512) void gemm_mfma_thin_lds_kernel(GemmArgs g) {
             const int64_t gm = m0 + 16 * i + r;
             const float* p = A + (gm < M ? gm : 0) * lda + (kv > 0 ? k : 0);
             if (gm < M && kv >= 8) {
-                const float4 x0 = *reinterpret_cast<const float4*>(p);
-                const float4 x1 = *reinterpret_cast<const float4*>(p + 4);
+                const Float4Dw x0 = *reinterpret_cast<const Float4Dw*>(p);
+                const Float4Dw x1 = *reinterpret_cast<const Float4Dw*>(p + 4);
                 ra[i][0] = x0.x; ra[i][1] = x0.y; ra[i][2] = x0.z; ra[i][3] = x0.w;
                 ra[i][4] = x1.x; ra[i][5] = x1.y; ra[i][6] = x1.z; ra[i][7] = x1.w;
             } else {
@@ -994,9 +1000,9 @@ void dispatch_inorder(const GemmArgs& g, hipStream_t s) {
         return launch_inorder_small<64, DUAL>(g, s);
     }
     if (g.n > 32) {
-        // the 8x8 register-blocked kernel; 128-bit A loads when rows allow
-        auto aligned = [](const float* p, int64_t ld) {
-            return p == nullptr || (ld % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0);
+        // the 8x8 register-blocked kernel; 128-bit A loads at dword addresses
+        auto aligned = [](const float* p, int64_t) {
+            return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 3) == 0;
         };
         const bool va4 = aligned(g.a1, g.lda1) && (!DUAL || aligned(g.a2, g.lda2));
         dim3 grid(static_cast<unsigned>(ceil_div(g.m, kWBM)),
@@ -1082,8 +1088,8 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
     if (algo == TG_GEMM_MFMA && g.n <= 64) {
         // thin: one wavefront per 64 rows, 16-column MFMA tiles up to n
         const unsigned grid = static_cast<unsigned>(ceil_div(g.m, 256));
-        auto al4 = [](const float* p, int64_t ld) {
-            return p == nullptr || (ld % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0);
+        auto al4 = [](const float* p, int64_t) {  // 128-bit loads at dword addresses
+            return p == nullptr || reinterpret_cast<uintptr_t>(p) % 4 == 0;
         };
         const bool aligned = al4(g.a1, g.lda1) && (!dual || al4(g.a2, g.lda2));
         const int ntile = static_cast<int>(ceil_div(g.n, 16));
@@ -1117,23 +1123,17 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
         const int64_t wgs = 8 * ceil_div(ceil_div(g.m, kMBM), 8) * ceil_div(g.n, kMBN);
         require(wgs < (int64_t(1) << 31), "matmul: too many row tiles");
         dim3 grid(static_cast<unsigned>(wgs));
-        auto width = [](std::initializer_list<int64_t> lds, std::initializer_list<const void*> ps) {
-            for (int v : {4, 2}) {
-                bool ok = true;
-                for (int64_t ld : lds) ok = ok && ld % v == 0;
-                for (const void* p : ps)
-                    ok = ok && reinterpret_cast<uintptr_t>(p) % (sizeof(float) * v) == 0;
-                if (ok) return v;
-            }
-            return 1;
+        // 128-bit loads at any dword address (load8)
+        auto width = [](std::initializer_list<int64_t>, std::initializer_list<const void*> ps) {
+            for (const void* p : ps)
+                if (reinterpret_cast<uintptr_t>(p) % sizeof(float) != 0) return 1;
+            return 4;
         };
         const int va = dual ? width({g.lda1, g.lda2}, {g.a1, g.a2}) : width({g.lda1}, {g.a1});
         const int vb = dual ? width({g.ldb1, g.ldb2}, {g.b1, g.b2}) : width({g.ldb1}, {g.b1});
 #define TG_MFMA_CASE(A_, B_) \
         if (va == A_ && vb == B_) { gemm_mfma_kernel<A_, B_><<<grid, 256, 0, s>>>(g); TG_LAUNCH_CHECK(); return; }
-        TG_MFMA_CASE(4, 4) TG_MFMA_CASE(4, 2) TG_MFMA_CASE(4, 1)
-        TG_MFMA_CASE(2, 4) TG_MFMA_CASE(2, 2) TG_MFMA_CASE(2, 1)
-        TG_MFMA_CASE(1, 4) TG_MFMA_CASE(1, 2) TG_MFMA_CASE(1, 1)
+        TG_MFMA_CASE(4, 4) TG_MFMA_CASE(4, 1) TG_MFMA_CASE(1, 4) TG_MFMA_CASE(1, 1)
 #undef TG_MFMA_CASE
         throw std::logic_error("matmul: no MFMA kernel for this access width");
     }
