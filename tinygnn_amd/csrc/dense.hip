@@ -47,6 +47,80 @@ __device__ __forceinline__ float epi_out(const GemmArgs& g, float x, int64_t m, 
     return epi_apply(x, g.bias, n, g.epi);
 }
 
+// epi_apply's activation with the epilogue fixed at compile time.
+template <int EPI>
+__device__ __forceinline__ float epi_act(float x) {
+    if (EPI == TG_EPI_RELU) return (0.0f < x) ? x : 0.0f;
+    if (EPI == TG_EPI_ELU) return (x < 0.0f) ? 1.0f * (expf(x) - 1.0f) : x;
+    return x;
+}
+
+// c_index as one formula: element (m, n) at (n / 32) * tile + m * row + n % 32
+// (row-major: tile = 32, row = ldc).
+struct CStrides {
+    int64_t tile, row;
+};
+__device__ __forceinline__ CStrides c_strides(const GemmArgs& g) {
+    return g.c_tile_stride > 0 ? CStrides{g.c_tile_stride, 32} : CStrides{32, g.ldc};
+}
+
+// Stores one lane's outputs of MI x NJ 16x16 MFMA tiles (D layout of
+// v_mfma_f32_16x16x4f32: lane (q, r) holds rows 4q..4q+3 of column r), the
+// tiles' rows from mb, columns from nb: C[m][n] = EPI(acc * row_scale[m] +
+// bias[n]) as epi_out computes it.  The row factors and bias terms are loaded
+// before the first store: C may alias them as far as the compiler knows, so
+// loads between the stores would each wait for a round trip.  A missing row
+// factor is 1 (x * 1 = x exactly), and the store loop has no branch but the
+// bounds (per-element loads and epilogue branches cost 6% of the config-E
+// layer-1 transform).
+template <int EPI, int MI, int NJ>
+__device__ __forceinline__ void store_tiles(const GemmArgs& g, const v4f (&acc)[MI][NJ],
+                                            int64_t mb, int64_t nb, int q, int r) {
+    float rsv[MI][4], bv[NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int64_t m = mb + i * 16 + 4 * q + rr;
+            rsv[i][rr] = (g.row_scale && m < g.m) ? g.row_scale[m] : 1.0f;
+        }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int64_t n = nb + j * 16 + r;
+        bv[j] = (g.bias && n < g.n) ? g.bias[n] : 0.0f;
+    }
+    const bool has_bias = g.bias != nullptr;
+    const CStrides cs = c_strides(g);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int64_t gn = nb + j * 16 + r;
+            if (gn >= g.n) continue;
+            float* cc = g.c + (gn >> 5) * cs.tile + (gn & 31);
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t m = mb + i * 16 + 4 * q + rr;
+                if (m >= g.m) continue;
+                float x = acc[i][j][rr] * rsv[i][rr];
+                if (has_bias) x = x + bv[j];
+                cc[m * cs.row] = epi_act<EPI>(x);
+            }
+        }
+}
+
+// store_tiles with the epilogue chosen at run time (one of three bodies runs).
+template <int MI, int NJ>
+__device__ __forceinline__ void store_tiles_any(const GemmArgs& g, const v4f (&acc)[MI][NJ],
+                                                int64_t mb, int64_t nb, int q, int r) {
+    if (g.epi == TG_EPI_RELU)
+        store_tiles<TG_EPI_RELU>(g, acc, mb, nb, q, r);
+    else if (g.epi == TG_EPI_ELU)
+        store_tiles<TG_EPI_ELU>(g, acc, mb, nb, q, r);
+    else
+        store_tiles<TG_EPI_NONE>(g, acc, mb, nb, q, r);
+}
+
 // ---------------------------------------------------------------------------
 // In-order GEMM (bit-exact)
 // ---------------------------------------------------------------------------
@@ -510,44 +584,37 @@ __global__ __launch_bounds__(256) void gemm_inorder_wide_kernel(GemmArgs g) {
 // Lane (q = lane/16, r = lane%16) feeds k = 4q + s at MFMA step s for both
 // operands (the products pair up; only the order of the k sum changes).
 // A is staged as [m][k] so a lane's four k values of a row are one 128-bit
-// LDS read; B stays [k][n] with a 132-float pitch, so the 64 lanes' reads of
-// B[4q+s][n0+r] fall in 64 distinct banks.
+// LDS read; B stays [k][n] and is read 32 bits at a time.
+// LDS layouts, measured free of bank conflicts on gfx950 (SQ_LDS_BANK_CONFLICT
+// = 0): A rows at a 24-float pitch, read by 16 rows x 4 chunks per
+// wavefront step, written by each 16 lanes as 8 rows x 2 chunks (the 16
+// chunk addresses cover the 64 banks once); B rows at a 132-float pitch,
+// written 16 lanes per row as 256 contiguous bytes.  (A at a 20-float pitch,
+// 2 lanes per row, and B at 8 columns per lane each cost a 2-way conflict:
+// 29% of LDS cycles.)
 // ---------------------------------------------------------------------------
 constexpr int kMBM = 128, kMBN = 128, kMBK = 16;
-constexpr int kMLDA = kMBK + 4;   // A tile pitch (floats): 16-byte aligned rows
+constexpr int kMLDA = kMBK + 8;   // A tile pitch (floats)
 constexpr int kMLDB = kMBN + 4;   // B tile pitch
 
-// Loads 8 consecutive floats p[0..7] of which the first `valid` exist
-// (valid <= 0: none), with V-wide accesses when all 8 exist.  V = 4 needs
-// 4-byte alignment only: gfx950's global loads take a 128-bit access at
-// any dword address (config-E transform, 602-float rows of A at 8-byte
-// alignment: 128-bit loads 0.68 ms, 64-bit 0.72 ms).
+// Loads p[0..3] of which the first `valid` exist (valid <= 0: none) as one
+// 128-bit access when all 4 exist and V = 4.  gfx950's global loads take a
+// 128-bit access at any dword address (config-E transform, 602-float rows of
+// A at 8-byte alignment: 128-bit loads 0.68 ms, 64-bit 0.72 ms).
 template <int V>
-__device__ __forceinline__ void load8(const float* __restrict__ p, int64_t valid,
-                                      float (&x)[8]) {
-    if (valid >= 8 && V > 1) {
+__device__ __forceinline__ v4f load4(const float* __restrict__ p, int64_t valid) {
+    if (V == 4 && valid >= 4) return *reinterpret_cast<const Float4Dw*>(p);
+    v4f x;
 #pragma unroll
-        for (int u = 0; u < 8; u += V) {
-            if constexpr (V == 4) {
-                const Float4Dw t = *reinterpret_cast<const Float4Dw*>(p + u);
-                x[u] = t.x;
-                x[u + 1] = t.y;
-                x[u + 2] = t.z;
-                x[u + 3] = t.w;
-            } else {
-                const float2 t = *reinterpret_cast<const float2*>(p + u);
-                x[u] = t.x;
-                x[u + 1] = t.y;
-            }
-        }
-        return;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = (u < valid) ? p[u] : 0.0f;
+    for (int u = 0; u < 4; ++u) x[u] = (u < valid) ? p[u] : 0.0f;
+    return x;
 }
 
-template <int VA, int VB>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
+// VA / VB: 4 = 128-bit operand loads (dword-aligned pointers), 1 = 32-bit.
+// EPI: g.epi.  Launch bound (256, 3): three workgroups per CU (41.5 KB of
+// LDS each) need at most 168 registers per lane.
+template <int VA, int VB, int EPI>
+__global__ __launch_bounds__(256, 3) void gemm_mfma_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) float As[2][kMBM][kMLDA];
     __shared__ __attribute__((aligned(16))) float Bs[2][kMBK][kMLDB];
     const int lane = threadIdx.x & 63;
@@ -568,32 +635,53 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     const int64_t t1 = (g.k1 + kMBK - 1) / kMBK;
     const int64_t nt = t1 + (g.a2 ? (g.k2 + kMBK - 1) / kMBK : 0);
 
-    // this thread's share of a tile: A row ar (8 k values from ak), B row bk
-    // (8 n values from bn)
-    const int ar = threadIdx.x >> 1, ak = (threadIdx.x & 1) * 8;
-    const int bk = threadIdx.x >> 4, bn = (threadIdx.x & 15) * 8;
-    float ra[8], rb[8];
+    // This thread's share of a tile: A row ar, k chunks ac and ac + 2 (4
+    // floats each); B row bkr, column chunks bc and bc + 16.  Rows past M
+    // read row M - 1 (their outputs are not stored), so a tile whose k range
+    // is whole loads A without guards.
+    const int ar = threadIdx.x >> 1, ac = threadIdx.x & 1;
+    const int bkr = threadIdx.x >> 4, bc = threadIdx.x & 15;
+    const int64_t gm = m0 + ar;
+    const int64_t gmc = gm < M ? gm : M - 1;
+    const int64_t nb0 = n0 + 4 * bc, nb1 = nb0 + 64;
+    const bool colfull = n0 + kMBN <= N;  // uniform
+    const float* pa1 = g.a1 ? g.a1 + gmc * g.lda1 + 4 * ac : nullptr;
+    const float* pa2 = g.a2 ? g.a2 + gmc * g.lda2 + 4 * ac : nullptr;
+    const float* pb1 = g.b1 ? g.b1 + bkr * g.ldb1 : nullptr;
+    const float* pb2 = g.b2 ? g.b2 + bkr * g.ldb2 : nullptr;
+    v4f ra0, ra1, rb0, rb1;
 
     auto fetch = [&](int64_t kt) {
         const bool seg2 = kt >= t1;
-        const float* A = seg2 ? g.a2 : g.a1;
-        const float* B = seg2 ? g.b2 : g.b1;
-        const int64_t lda = seg2 ? g.lda2 : g.lda1;
+        const float* pa = seg2 ? pa2 : pa1;
         const int64_t ldb = seg2 ? g.ldb2 : g.ldb1;
         const int64_t K = seg2 ? g.k2 : g.k1;
         const int64_t k0 = (seg2 ? kt - t1 : kt) * kMBK;
-        const int64_t gm = m0 + ar;
-        const int64_t ka = k0 + ak;
-        load8<VA>(A + (gm < M ? gm : 0) * lda + ka, gm < M ? K - ka : 0, ra);
-        const int64_t kb = k0 + bk;
-        const int64_t nb = n0 + bn;
-        load8<VB>(B + (kb < K ? kb : 0) * ldb + nb, kb < K ? N - nb : 0, rb);
+        const int64_t kb = k0 + bkr;
+        const float* pb = kb < K ? (seg2 ? pb2 : pb1) + k0 * ldb : (seg2 ? g.b2 : g.b1);
+        if (k0 + kMBK <= K) {  // whole k range (uniform)
+            ra0 = load4<VA>(pa + k0, 4);
+            ra1 = load4<VA>(pa + k0 + 8, 4);
+            if (colfull) {
+                rb0 = load4<VB>(pb + nb0, 4);
+                rb1 = load4<VB>(pb + nb1, 4);
+            } else {
+                rb0 = load4<VB>(pb + nb0, N - nb0);
+                rb1 = load4<VB>(pb + nb1, N - nb1);
+            }
+        } else {
+            const int64_t ka = k0 + 4 * ac;
+            ra0 = load4<1>(pa + k0, gm < M ? K - ka : 0);
+            ra1 = load4<1>(pa + k0 + 8, gm < M ? K - ka - 8 : 0);
+            rb0 = load4<1>(pb + nb0, kb < K ? N - nb0 : 0);
+            rb1 = load4<1>(pb + nb1, kb < K ? N - nb1 : 0);
+        }
     };
     auto stage = [&](int buf) {
-        *reinterpret_cast<float4*>(&As[buf][ar][ak]) = make_float4(ra[0], ra[1], ra[2], ra[3]);
-        *reinterpret_cast<float4*>(&As[buf][ar][ak + 4]) = make_float4(ra[4], ra[5], ra[6], ra[7]);
-        *reinterpret_cast<float4*>(&Bs[buf][bk][bn]) = make_float4(rb[0], rb[1], rb[2], rb[3]);
-        *reinterpret_cast<float4*>(&Bs[buf][bk][bn + 4]) = make_float4(rb[4], rb[5], rb[6], rb[7]);
+        *reinterpret_cast<v4f*>(&As[buf][ar][4 * ac]) = ra0;
+        *reinterpret_cast<v4f*>(&As[buf][ar][4 * ac + 8]) = ra1;
+        *reinterpret_cast<v4f*>(&Bs[buf][bkr][4 * bc]) = rb0;
+        *reinterpret_cast<v4f*>(&Bs[buf][bkr][4 * bc + 64]) = rb1;
     };
 
     v4f acc[4][4];
@@ -610,6 +698,9 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
     for (int64_t kt = 0; kt < nt; ++kt) {
         const int cb = static_cast<int>(kt & 1);
         if (kt + 1 < nt) fetch(kt + 1);
+        // keep the next tile's loads ahead of this tile's MFMAs (left to
+        // itself the scheduler sinks them below, exposing their latency)
+        __builtin_amdgcn_sched_barrier(0);
         v4f a[4];
         float b[4][4];
 #pragma unroll
@@ -629,19 +720,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g) {
         if (kt + 1 < nt) stage(cb ^ 1);
         __syncthreads();
     }
-    // D layout of 16x16x4 f32: lane holds rows 4q..4q+3 of column r.
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t gn = n0 + wn + j * 16 + r;
-            if (gn >= N) continue;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int64_t gm = m0 + wm + i * 16 + 4 * q + rr;
-                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
-            }
-        }
+    store_tiles<EPI>(g, acc, m0 + wm, n0 + wn, q, r);
 }
 
 // ---------------------------------------------------------------------------
@@ -729,19 +808,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_thin_kernel(GemmArgs g) {
                 for (int t = 0; t < 8; ++t) b[j][t] = nb[j][t];
         }
     }
-    // D layout of 16x16x4 f32: lane (q, r) holds rows 4q..4q+3 of column r.
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int64_t gn = 16 * j + r;
-            if (gn >= N) continue;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int64_t gm = m0 + 16 * i + 4 * q + rr;
-                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
-            }
-        }
+    store_tiles_any(g, acc, m0, 0, q, r);
 }
 
 // Thin MFMA GEMM with B in LDS (one pair, n <= 64, round_up(k, 32) x 16 NT
@@ -843,18 +910,7 @@ __global__ __launch_bounds__(512) void gemm_mfma_thin_lds_kernel(GemmArgs g) {
                 a1[i][t] = a2[i][t];
             }
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int64_t gn = 16 * j + r;
-            if (gn >= N) continue;
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int64_t gm = m0 + 16 * i + 4 * q + rr;
-                if (gm < M) g.c[c_index(g, gm, gn)] = epi_out(g, acc[i][j][rr], gm, gn);
-            }
-        }
+    store_tiles_any(g, acc, m0, 0, q, r);
 }
 
 // ---------------------------------------------------------------------------
@@ -1123,7 +1179,7 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
         const int64_t wgs = 8 * ceil_div(ceil_div(g.m, kMBM), 8) * ceil_div(g.n, kMBN);
         require(wgs < (int64_t(1) << 31), "matmul: too many row tiles");
         dim3 grid(static_cast<unsigned>(wgs));
-        // 128-bit loads at any dword address (load8)
+        // 128-bit loads at any dword address (load4)
         auto width = [](std::initializer_list<int64_t>, std::initializer_list<const void*> ps) {
             for (const void* p : ps)
                 if (reinterpret_cast<uintptr_t>(p) % sizeof(float) != 0) return 1;
@@ -1131,9 +1187,16 @@ void gemm(const GemmArgs& g, int algo, hipStream_t s) {
         };
         const int va = dual ? width({g.lda1, g.lda2}, {g.a1, g.a2}) : width({g.lda1}, {g.a1});
         const int vb = dual ? width({g.ldb1, g.ldb2}, {g.b1, g.b2}) : width({g.ldb1}, {g.b1});
-#define TG_MFMA_CASE(A_, B_) \
-        if (va == A_ && vb == B_) { gemm_mfma_kernel<A_, B_><<<grid, 256, 0, s>>>(g); TG_LAUNCH_CHECK(); return; }
-        TG_MFMA_CASE(4, 4) TG_MFMA_CASE(4, 1) TG_MFMA_CASE(1, 4) TG_MFMA_CASE(1, 1)
+#define TG_MFMA_CASE(A_, B_, E_)                                                            \
+        if (va == A_ && vb == B_ && g.epi == E_) {                                          \
+            gemm_mfma_kernel<A_, B_, E_><<<grid, 256, 0, s>>>(g);                           \
+            TG_LAUNCH_CHECK();                                                              \
+            return;                                                                         \
+        }
+#define TG_MFMA_CASES(E_) \
+        TG_MFMA_CASE(4, 4, E_) TG_MFMA_CASE(4, 1, E_) TG_MFMA_CASE(1, 4, E_) TG_MFMA_CASE(1, 1, E_)
+        TG_MFMA_CASES(TG_EPI_NONE) TG_MFMA_CASES(TG_EPI_RELU) TG_MFMA_CASES(TG_EPI_ELU)
+#undef TG_MFMA_CASES
 #undef TG_MFMA_CASE
         throw std::logic_error("matmul: no MFMA kernel for this access width");
     }
