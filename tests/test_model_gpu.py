@@ -191,7 +191,8 @@ def test_zero_weights_default(gpu):
 @pytest.mark.parametrize("case", ["gcn_sorted", "gcn_unsorted", "gcn_split_rows",
                                   "gcn_wide_tail", "sage_concat", "sage_transform_first",
                                   "sage_split_rows", "sage_wide_tail", "gat", "gat_split_rows",
-                                  "gat_negative_slope", "gat_wide_heads"])
+                                  "gat_negative_slope", "gat_wide_heads", "gcn_dense",
+                                  "gcn_dense_unsorted", "sage_dense", "gat_dense"])
 def test_blocked_aggregation(gpu, restate, case):
     """Column-blocked GCN / SAGE-mean / GAT aggregation (forced on small
     graphs with few rows per block): against the oracle at the
@@ -202,14 +203,18 @@ def test_blocked_aggregation(gpu, restate, case):
     32-column groups), two 64-column heads (one per 64-column lane group,
     destination scores computed from the gathered rows), empty rows, unsorted rows and rows of more than one plan chunk
     inside a block.  Last tiles of 12, 7 and 10 valid columns, and of 28,
-    25 (the wide_tail cases)."""
+    25 (the wide_tail cases).  The dense cases (100 entries per row on
+    average) take the row split of sorted structures (block starts by binary
+    search, one wavefront per row scattering); unsorted, it declines and the
+    general split runs."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(31)
     split = case.endswith("split_rows")
+    dense = "_dense" in case
     n = 4000 if split else 3000
     rows_per_block = 2000 if split else 100
-    a = random_csr(rng, n, n, avg_deg=40, max_deg=3600 if split else 2800, empty_frac=0.05,
-                   sorted_cols=case != "gcn_unsorted")
+    a = random_csr(rng, n, n, avg_deg=100 if dense else 40, max_deg=3600 if split else 2800,
+                   empty_frac=0.05, sorted_cols=not case.endswith("unsorted"))
     if split:  # a row with more than 1024 entries in each of the two blocks
         assert (np.diff(a.row_ptr) > 3000).any()
     if case.startswith("gcn"):
@@ -226,6 +231,8 @@ def test_blocked_aggregation(gpu, restate, case):
                 layer["slope"] = -0.3
     elif case == "sage_wide_tail":
         spec = synth.spec_sage(96, 60, 25)
+    elif case == "sage_dense":
+        spec = synth.spec_sage(48, 300, 10)
     else:
         spec = synth.spec_sage(96, 300, 10)
     w = synth.model_weights(spec, seed=3)
@@ -462,9 +469,10 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
         np.testing.assert_array_equal(exact[100].view(np.int32), want.view(np.int32))
 
 
+@pytest.mark.parametrize("avg_deg", [30, 100])
 @pytest.mark.parametrize("model", ["gcn", "gat"])
 @pytest.mark.parametrize("order", ["sorted", "unsorted", "unsorted_in_block"])
-def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
+def test_direct_self_loop_split_long_rows(gpu, restate, order, model, avg_deg):
     """The blocked A + I split straight from A (rows of up to 9,000 entries:
     the workgroup-per-row kernels past 4,096) equals the copy split from the
     A + I gcn_norm / add_self_loops write, bit for bit in both forward modes,
@@ -473,11 +481,13 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
     out of order makes the direct split decline (sl_direct False) and the
     forward take the written A + I; so does a row out of order inside one
     block (two adjacent columns around the diagonal swapped), where the
-    block order holds but the diagonal's place would not be unique."""
+    block order holds but the diagonal's place would not be unique.  At 100
+    entries per row on average the split is the row split (binary-searched
+    block starts, the diagonal's place searched too)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(91)
     n = 3000
-    a = random_csr(rng, n, n, avg_deg=30, max_deg=9000, empty_frac=0.03)
+    a = random_csr(rng, n, n, avg_deg=avg_deg, max_deg=9000, empty_frac=0.03)
     rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
     keep = rows != a.col_ind
     g = restate.edge_list_to_csr(rows[keep], a.col_ind[keep].astype(np.int32), n)
@@ -524,7 +534,8 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order, model):
 
 @pytest.mark.parametrize("model,sorted_cols", [("gcn", True), ("sage", True), ("gat", True),
                                                ("gat64", True), ("gcn", False), ("sage", False),
-                                               ("gat", False)])
+                                               ("gat", False), ("gcn_dense", True),
+                                               ("sage_dense", True), ("gat_dense", True)])
 def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
     """PRECISION_EXACT with forced column blocking: with sorted rows each pass
     continues the rows' fma / add chains in nonzero order, so GCN and SAGE
@@ -532,11 +543,14 @@ def test_exact_precision_blocked(gpu, restate, model, sorted_cols):
     span many blocks), and GAT's equal the unblocked exact path's (the
     reference's order; exp as in that path).  Unsorted rows are not in block
     order: the model then keeps the unblocked exact path, with the same
-    bytes."""
+    bytes.  The dense cases (100 entries per row on average) build their
+    copies by the row split."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(78)
     n = 3000
-    a = random_csr(rng, n, n, avg_deg=25, max_deg=3000, empty_frac=0.02,
+    dense = model.endswith("_dense")
+    model = model.replace("_dense", "")
+    a = random_csr(rng, n, n, avg_deg=100 if dense else 25, max_deg=3000, empty_frac=0.02,
                    sorted_cols=sorted_cols)
     x = rng.standard_normal((n, 70)).astype(np.float32)
     spec = {"gcn": synth.spec_gcn(70, 96, 41), "sage": synth.spec_sage(70, 96, 41),

@@ -417,6 +417,147 @@ __global__ __launch_bounds__(256) void flat_diag_kernel(FlatSplit a, const int32
         a.bci[out] = i;
 }
 
+// ---------------------------------------------------------------------------
+// Row split, for long sorted rows (at least kRowSplitMinAvg entries per row
+// on average).  A group of lanes per row finds every block's start in the
+// row by binary search over its sorted columns (a running maximum keeps the
+// starts non-decreasing, so a row's counts sum to its length whatever its
+// order); the counts' scan gives the copy's offsets, and one wavefront per
+// row streams the row's entries to them, each entry's block start and base
+// from the lane that loaded them.  No pass reads every entry to count it:
+// the flat split reads each column twice (count and scatter) and finds its
+// row through a chain of dependent loads (config E's A + I: flat count 0.22
+// + scatter 0.25 ms; row search 0.08 + scatter 0.37 ms, and none of the flat
+// split's bitmap, rank and non-empty-row passes).  The scatter checks the
+// order as it goes: a column below its predecessor, or one outside its
+// block's run of the row, sets flags[0] (and an entry outside its run is not
+// written, so every store stays in its (block, row) segment); with vdiag a
+// diagonal sets flags[1].
+// ---------------------------------------------------------------------------
+constexpr int64_t kRowSplitMinAvg = 64;
+
+// The first position in ci[lo, hi) whose column is >= key (ci[lo, hi) sorted).
+__device__ __forceinline__ int lower_bound_col(const int32_t* __restrict__ ci, int lo, int hi,
+                                               int64_t key) {
+    while (lo < hi) {
+        const int mid = lo + ((hi - lo) >> 1);
+        if (ci[mid] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Per row: starts[b][r] (relative to the row) and the counts cnt[b][r] (the
+// virtual entry in its block), and with vdiag the virtual entry's position
+// ins[r] (the first column >= r, kept inside its block's run) and flags[1]
+// for a diagonal.  A group of G lanes (G a power of two > nb) per row: lane
+// b in 1..nb-1 searches the whole row for block b's start, lane nb for the
+// virtual entry's place, and a running maximum over the group keeps the
+// starts non-decreasing whatever the order (one search deep instead of nb
+// in sequence: config E 95 -> 20 us).
+template <int G>
+__global__ __launch_bounds__(256) void rows_search_kernel(FlatSplit a, int32_t* __restrict__ cnt) {
+    const int lane = threadIdx.x & 63;
+    const int j = lane & (G - 1);
+    const int64_t r = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / G;
+    const bool live = r < a.n;
+    const int lo = live ? a.rp[r] : 0, hi = live ? a.rp[r + 1] : 0;
+    const int len = hi - lo;
+    int sj = 0;
+    if (live && j >= 1 && j < a.nb)
+        sj = lower_bound_col(a.ci, lo, hi, static_cast<int64_t>(j) * a.rows_per_block) - lo;
+    else if (live && j >= a.nb)
+        sj = len;
+    int ins = 0;
+    if (live && a.vdiag && j == a.nb) ins = lower_bound_col(a.ci, lo, hi, r) - lo;
+    // running maximum over the group's lanes 0..j (starts non-decreasing)
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) {
+        const int v = __shfl_up(sj, o, G);
+        if (j >= o) sj = sj > v ? sj : v;
+    }
+    const int next = __shfl_down(sj, 1, G);  // lane j + 1's start (lanes < nb)
+    const int d = a.vdiag ? block_of(static_cast<int>(live ? r : 0), a) : -1;
+    const int sd = __shfl(sj, d < 0 ? 0 : d, G), sd1 = __shfl(sj, d < 0 ? 0 : d + 1, G);
+    ins = __shfl(ins, a.nb, G);
+    if (!live) return;
+    if (j < a.nb) {
+        const int64_t t = static_cast<int64_t>(j) * a.n + r;
+        const int e = j + 1 < a.nb ? next : len;
+        a.starts[t] = sj;
+        cnt[t] = e - sj + (j == d ? 1 : 0);
+    }
+    if (a.vdiag && j == 0) {
+        ins = ins < sd ? sd : (ins > sd1 ? sd1 : ins);
+        a.ins[r] = ins;
+        if (ins < len && a.ci[lo + ins] == r) atomicOr(&a.flags[1], 1);
+    }
+}
+
+constexpr int kRowSU = 4;  // 64-entry slices in flight per wavefront
+
+// One wavefront per row: entry k of block b goes to obase[b][r] + k (one
+// further past the virtual entry in its block).  (Eight rows per wavefront,
+// the next row's bounds and bases loaded while a row is written, measured
+// 0.48 ms against 0.37 for config E's A + I; eight slices in flight instead
+// of four, no change.)
+__global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= a.n) return;  // uniform per wave
+    const int lo = a.rp[r], hi = a.rp[r + 1];
+    const int len = hi - lo;
+    // lane j < nb: block j's base and start
+    int ob = 0, st = 0;
+    if (lane < a.nb) {
+        const int64_t t = static_cast<int64_t>(lane) * a.n + r;
+        ob = a.obase[t];
+        st = a.starts[t];
+    }
+    const int d = a.vdiag ? block_of(static_cast<int>(r), a) : -1;
+    int carry = 0;  // the column before this slice group (k > lo)
+    for (int k0 = lo; k0 < hi; k0 += 64 * kRowSU) {
+        int c[kRowSU];
+        float x[kRowSU];
+#pragma unroll
+        for (int u = 0; u < kRowSU; ++u) {
+            const int k = k0 + u * 64 + lane;
+            c[u] = k < hi ? a.ci[k] : 0;
+            x[u] = (a.bv && k < hi) ? a.v[k] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kRowSU; ++u) {
+            const int k = k0 + u * 64 + lane;
+            // every lane takes part in the shuffles (a shuffle inside a
+            // condition would read the lanes it leaves out as zeros)
+            int pc = __shfl_up(c[u], 1, 64);
+            if (lane == 0) pc = carry;
+            carry = __shfl(c[u], 63, 64);
+            const int b = block_of(c[u], a);
+            const int sb = __shfl(st, b, 64);
+            const int sn = __shfl(st, b + 1 < 64 ? b + 1 : 63, 64);
+            const int se = b + 1 < a.nb ? sn : len;
+            const int base = __shfl(ob, b, 64);
+            if (k >= hi) continue;
+            const int c0 = c[u];
+            if (k > lo && pc > c0) atomicOr(&a.flags[0], 1);
+            if (a.vdiag && c0 == r) atomicOr(&a.flags[1], 1);
+            const int kr = k - lo;
+            if (kr < sb || kr >= se) {
+                atomicOr(&a.flags[0], 1);
+                continue;
+            }
+            int o = base + k;
+            if (a.vdiag && c0 > r && b == d) ++o;
+            if (a.bci16)
+                a.bci16[o] = static_cast<uint16_t>(c0 - b * a.rows_per_block);
+            else
+                a.bci[o] = c0;
+            if (a.bv) a.bv[o] = x[u];
+        }
+    }
+}
+
 }  // namespace
 
 int64_t resolve_block_rows(int64_t requested, int64_t n, int64_t nnz, int group_cols) {
@@ -574,6 +715,71 @@ bool split_flat(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
     return hf[0] == 0 && hf[1] == 0;
 }
 
+// The row split (long sorted rows; with or without the virtual diagonal);
+// false as split_flat.
+bool split_rows(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const int32_t* ci,
+                const float* v, int64_t nnz_src, bool vdiag, int64_t max_f, int64_t chunk,
+                hipStream_t s) {
+    const int64_t n = bk.n, nb = bk.n_blocks;
+    auto grid = [](int64_t x) { return static_cast<unsigned>(ceil_div(std::max<int64_t>(x, 1), 256)); };
+    fill_i32(t.flags, 4, 0, s);
+    FlatSplit a{};
+    a.rp = rp;
+    a.ci = ci;
+    a.v = v;
+    a.n = n;
+    a.nnz = nnz_src;
+    a.rows_per_block = static_cast<int>(bk.rows_per_block);
+    a.inv_rows = 1.0 / static_cast<double>(bk.rows_per_block);
+    a.nb = static_cast<int>(nb);
+    a.vdiag = vdiag ? 1 : 0;
+    a.starts = t.starts;
+    a.ins = t.ins;
+    a.flags = t.flags;
+    // a group of G lanes per row, G the power of two above nb
+    const int g = nb < 2 ? 2 : nb < 4 ? 4 : nb < 8 ? 8 : nb < 16 ? 16 : nb < 32 ? 32 : 64;
+    require(nb < 64, "blocked CSR: the row split takes at most 63 blocks");
+    const unsigned sgrid = static_cast<unsigned>(ceil_div(n * g, 256));
+    switch (g) {
+        case 2: rows_search_kernel<2><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+        case 4: rows_search_kernel<4><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+        case 8: rows_search_kernel<8><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+        case 16: rows_search_kernel<16><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+        case 32: rows_search_kernel<32><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+        default: rows_search_kernel<64><<<sgrid, 256, 0, s>>>(a, t.cnt); break;
+    }
+    TG_LAUNCH_CHECK();
+    int32_t* brp = bk.brp.as<int32_t>();
+    exclusive_scan_i32(t.cnt, brp, nb * n, t.scan_tmp, s);
+    flat_bases_kernel<<<grid(n * nb), 256, 0, s>>>(a, brp, t.cnt);
+    TG_LAUNCH_CHECK();
+    a.obase = t.cnt;
+    a.bci = bk.idx16 ? nullptr : bk.bci.as<int32_t>();
+    a.bci16 = bk.idx16 ? bk.bci.as<uint16_t>() : nullptr;
+    a.bv = v ? bk.bv.as<float>() : nullptr;
+    if (nnz_src > 0) {
+        rows_scatter_kernel<<<static_cast<unsigned>(ceil_div(n, 4)), 256, 0, s>>>(a);
+        TG_LAUNCH_CHECK();
+    }
+    if (vdiag) {
+        flat_diag_kernel<<<grid(n), 256, 0, s>>>(a, brp);
+        TG_LAUNCH_CHECK();
+    }
+    int32_t* hf = reinterpret_cast<int32_t*>(bk.host.as<int64_t>() + 4 * nb);
+    TG_HIP(hipMemcpyAsync(hf, t.flags, 2 * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    build_block_plans(bk, max_f, chunk, s);
+    return hf[0] == 0 && hf[1] == 0;
+}
+
+// Sorted-row splits: the row split for long rows, the flat one otherwise.
+bool split_sorted(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const int32_t* ci,
+                  const float* v, int64_t nnz_src, bool vdiag, int64_t max_f, int64_t chunk,
+                  hipStream_t s) {
+    if (nnz_src >= kRowSplitMinAvg * bk.n && bk.n_blocks < 64)
+        return split_rows(bk, t, rp, ci, v, nnz_src, vdiag, max_f, chunk, s);
+    return split_flat(bk, t, rp, ci, v, nnz_src, vdiag, max_f, chunk, s);
+}
+
 // The general split (any order), with the disorder flag: count, scan,
 // scatter, plans.
 void split_general(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const int32_t* ci,
@@ -612,7 +818,7 @@ void build_blocked(BlockedCSR& bk, int64_t n, int64_t nnz, const int32_t* rp,
     bk.vdiag = false;
     // rows in block order (sorted rows) take the flat split; the general
     // one runs when some row is not
-    if (split_flat(bk, t, rp, ci, v, nnz, false, max_f, chunk, s)) {
+    if (split_sorted(bk, t, rp, ci, v, nnz, false, max_f, chunk, s)) {
         bk.in_order = true;
         return;
     }
@@ -626,7 +832,7 @@ bool build_blocked_self_loops(BlockedCSR& bk, int64_t n, int64_t nnz, const int3
     const SplitTemps t = setup_blocked(bk, n, nnz + n, nnz, rp, false, rows_per_block);
     require(nnz == 0 || ci != nullptr, "blocked CSR: null structure");
     bk.vdiag = true;
-    if (!split_flat(bk, t, rp, ci, nullptr, nnz, true, max_f, chunk, s)) return false;
+    if (!split_sorted(bk, t, rp, ci, nullptr, nnz, true, max_f, chunk, s)) return false;
     bk.in_order = true;
     return true;
 }
