@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <vector>
 
@@ -139,6 +140,11 @@ struct BlockedCSR {
     DeviceBuffer plan_scratch;  // the block plans' build temporaries
     PinnedBuffer host;          // the build's device-to-host results (plan totals, disorder)
     std::vector<std::unique_ptr<tg_spmm_plan_s>> plans;
+    // called once by the next build, right after it enqueues the copy's
+    // scatter (before the block plans), then cleared: a caller starts other
+    // streams' work there, so that it does not take the CUs from the split's
+    // latency-bound passes
+    std::function<void()> after_split;
 };
 
 // Blocks with at most 64 column blocks; v may be null (structure only);

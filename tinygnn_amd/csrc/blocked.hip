@@ -217,7 +217,9 @@ struct FlatSplit {
     int32_t* bci;
     uint16_t* bci16;
     float* bv;
-    int32_t* flags;             // [0] an entry out of block order, [1] (vdiag) a diagonal
+    int32_t* flags;             // [0] an entry out of block order, [1] (vdiag) a diagonal,
+                                // [3] (row split) rows longer than kRowCap
+    int32_t* long_rows;         // row split: those rows
 };
 
 __device__ __forceinline__ int block_of(int c, const FlatSplit& a) {
@@ -427,14 +429,15 @@ __global__ __launch_bounds__(256) void flat_diag_kernel(FlatSplit a, const int32
 // from the lane that loaded them.  No pass reads every entry to count it:
 // the flat split reads each column twice (count and scatter) and finds its
 // row through a chain of dependent loads (config E's A + I: flat count 0.22
-// + scatter 0.25 ms; row search 0.08 + scatter 0.37 ms, and none of the flat
-// split's bitmap, rank and non-empty-row passes).  The scatter checks the
-// order as it goes: a column below its predecessor, or one outside its
-// block's run of the row, sets flags[0] (and an entry outside its run is not
-// written, so every store stays in its (block, row) segment); with vdiag a
-// diagonal sets flags[1].
+// + scatter 0.25 ms, plus the flat split's bitmap, rank and non-empty-row
+// passes).  The scatter checks the order as it goes: a column below its
+// predecessor sets flags[0]; with vdiag a diagonal sets flags[1].
 // ---------------------------------------------------------------------------
 constexpr int64_t kRowSplitMinAvg = 64;
+// entries of a row that its own wavefront writes; the rest of a longer row
+// is shared by a workgroup of kLongWaves wavefronts
+constexpr int kRowCap = 2048;
+constexpr int kLongWaves = 16;
 
 // The first position in ci[lo, hi) whose column is >= key (ci[lo, hi) sorted).
 __device__ __forceinline__ int lower_bound_col(const int32_t* __restrict__ ci, int lo, int hi,
@@ -487,6 +490,8 @@ __global__ __launch_bounds__(256) void rows_search_kernel(FlatSplit a, int32_t* 
         a.starts[t] = sj;
         cnt[t] = e - sj + (j == d ? 1 : 0);
     }
+    // rows past the per-row scatter's share, for rows_scatter_long_kernel
+    if (j == 0 && len > kRowCap) a.long_rows[atomicAdd(&a.flags[3], 1)] = static_cast<int32_t>(r);
     if (a.vdiag && j == 0) {
         ins = ins < sd ? sd : (ins > sd1 ? sd1 : ins);
         a.ins[r] = ins;
@@ -496,35 +501,36 @@ __global__ __launch_bounds__(256) void rows_search_kernel(FlatSplit a, int32_t* 
 
 constexpr int kRowSU = 4;  // 64-entry slices in flight per wavefront
 
-// One wavefront per row: entry k of block b goes to obase[b][r] + k (one
-// further past the virtual entry in its block).  (Eight rows per wavefront,
-// the next row's bounds and bases loaded while a row is written, measured
-// 0.48 ms against 0.37 for config E's A + I; eight slices in flight instead
-// of four, no change.)
-__global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (r >= a.n) return;  // uniform per wave
-    const int lo = a.rp[r], hi = a.rp[r + 1];
-    const int len = hi - lo;
-    // lane j < nb: block j's base and start
-    int ob = 0, st = 0;
-    if (lane < a.nb) {
-        const int64_t t = static_cast<int64_t>(lane) * a.n + r;
-        ob = a.obase[t];
-        st = a.starts[t];
-    }
+// Entries [kb, ke) of row r (entries [lo, hi)) to the copy: entry k of block
+// b goes to obase[b][r] + k (one further past the virtual entry in its
+// block).  Lane j < nb holds block j's base (ob) and start (st).  An entry's
+// block is taken from its position among the row's block starts, not from
+// its column: for a sorted row the two agree (the starts were searched in
+// the same columns), an unsorted one is flagged, and either way every store
+// lands in its (block, row) segment.  Column-derived blocks (a
+// double-precision division and three lane shuffles per entry) measured the
+// same.  `step`: the distance between this wavefront's slice groups.
+template <int NBM>  // at most NBM blocks (their starts in scalar registers) or any (0)
+__device__ __forceinline__ void scatter_range(const FlatSplit& a, int64_t r, int lo, int hi,
+                                              int kb, int ke, int step, int ob, int st,
+                                              int lane) {
     const int d = a.vdiag ? block_of(static_cast<int>(r), a) : -1;
-    int carry = 0;  // the column before this slice group (k > lo)
-    for (int k0 = lo; k0 < hi; k0 += 64 * kRowSU) {
+    const int nb = a.nb;
+    int sv[NBM > 0 ? NBM : 1];
+#pragma unroll
+    for (int j = 0; j < NBM; ++j) sv[j] = __builtin_amdgcn_readlane(st, j);
+    for (int k0 = kb; k0 < ke; k0 += step) {
+        const int kend = k0 + 64 * kRowSU < ke ? k0 + 64 * kRowSU : ke;
         int c[kRowSU];
         float x[kRowSU];
 #pragma unroll
         for (int u = 0; u < kRowSU; ++u) {
             const int k = k0 + u * 64 + lane;
-            c[u] = k < hi ? a.ci[k] : 0;
-            x[u] = (a.bv && k < hi) ? a.v[k] : 0.0f;
+            c[u] = k < kend ? a.ci[k] : 0;
+            x[u] = (a.bv && k < kend) ? a.v[k] : 0.0f;
         }
+        // the column before the group (its first entry's predecessor)
+        int carry = k0 > lo ? a.ci[k0 - 1] : 0;
 #pragma unroll
         for (int u = 0; u < kRowSU; ++u) {
             const int k = k0 + u * 64 + lane;
@@ -533,20 +539,21 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
             int pc = __shfl_up(c[u], 1, 64);
             if (lane == 0) pc = carry;
             carry = __shfl(c[u], 63, 64);
-            const int b = block_of(c[u], a);
-            const int sb = __shfl(st, b, 64);
-            const int sn = __shfl(st, b + 1 < 64 ? b + 1 : 63, 64);
-            const int se = b + 1 < a.nb ? sn : len;
+            // the entry's block: the number of block starts at or before it
+            const int kr = k - lo;
+            int b = 0;
+            if constexpr (NBM > 0) {
+#pragma unroll
+                for (int j = 1; j < NBM; ++j) b += kr >= sv[j] ? 1 : 0;
+            } else {
+                for (int j = 1; j < nb; ++j)
+                    b += kr >= __builtin_amdgcn_readlane(st, j) ? 1 : 0;
+            }
             const int base = __shfl(ob, b, 64);
-            if (k >= hi) continue;
+            if (k >= kend) continue;
             const int c0 = c[u];
             if (k > lo && pc > c0) atomicOr(&a.flags[0], 1);
             if (a.vdiag && c0 == r) atomicOr(&a.flags[1], 1);
-            const int kr = k - lo;
-            if (kr < sb || kr >= se) {
-                atomicOr(&a.flags[0], 1);
-                continue;
-            }
             int o = base + k;
             if (a.vdiag && c0 > r && b == d) ++o;
             if (a.bci16)
@@ -555,6 +562,50 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
                 a.bci[o] = c0;
             if (a.bv) a.bv[o] = x[u];
         }
+    }
+}
+
+// Row r's block bases and starts, lane j < nb.
+__device__ __forceinline__ void row_blocks(const FlatSplit& a, int64_t r, int lane, int& ob,
+                                           int& st) {
+    ob = 0;
+    st = 0x7FFFFFFF;  // (no block: after every entry)
+    if (lane < a.nb) {
+        const int64_t t = static_cast<int64_t>(lane) * a.n + r;
+        ob = a.obase[t];
+        st = a.starts[t];
+    }
+}
+
+// One wavefront per row, its first kRowCap entries (one wavefront walking a
+// 20,000-entry row alone bounded the whole pass: config E's A + I 0.37 ms).
+template <int NBM>
+__global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r >= a.n) return;  // uniform per wave
+    const int lo = a.rp[r], hi = a.rp[r + 1];
+    int ob, st;
+    row_blocks(a, r, lane, ob, st);
+    const int ke = hi - lo > kRowCap ? lo + kRowCap : hi;
+    scatter_range<NBM>(a, r, lo, hi, lo, ke, 64 * kRowSU, ob, st, lane);
+}
+
+// The rest of every row longer than kRowCap: a workgroup per row (rows
+// a.long_rows[0 .. flags[3]), taken in turn by a fixed grid), its
+// wavefronts taking the slice groups in turn.
+template <int NBM>
+__global__ __launch_bounds__(64 * kLongWaves) void rows_scatter_long_kernel(FlatSplit a) {
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int count = a.flags[3];
+    for (int i = blockIdx.x; i < count; i += gridDim.x) {
+        const int64_t r = a.long_rows[i];
+        const int lo = a.rp[r], hi = a.rp[r + 1];
+        int ob, st;
+        row_blocks(a, r, lane, ob, st);
+        scatter_range<NBM>(a, r, lo, hi, lo + kRowCap + w * 64 * kRowSU, hi,
+                      kLongWaves * 64 * kRowSU, ob, st, lane);
     }
 }
 
@@ -650,6 +701,14 @@ void build_block_plans(BlockedCSR& bk, int64_t max_f, int64_t chunk, hipStream_t
     else bk.resident_wgs = 0;
 }
 
+// The caller's after_split hook, once.
+void fire_after_split(BlockedCSR& bk) {
+    if (!bk.after_split) return;
+    std::function<void()> f = std::move(bk.after_split);
+    bk.after_split = nullptr;
+    f();
+}
+
 // The flat split (with or without the virtual diagonal); false when some
 // row is out of block order or, with vdiag, has a diagonal (the copy is
 // then incomplete and the caller takes another path).
@@ -705,6 +764,7 @@ bool split_flat(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
         flat_scatter_kernel<<<egrid, 256, 0, s>>>(a);
         TG_LAUNCH_CHECK();
     }
+    fire_after_split(bk);
     if (vdiag) {
         flat_diag_kernel<<<grid(n), 256, 0, s>>>(a, brp);
         TG_LAUNCH_CHECK();
@@ -736,6 +796,7 @@ bool split_rows(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
     a.starts = t.starts;
     a.ins = t.ins;
     a.flags = t.flags;
+    a.long_rows = t.nz_rows;  // (the flat split's non-empty-row list, unused here)
     // a group of G lanes per row, G the power of two above nb
     const int g = nb < 2 ? 2 : nb < 4 ? 4 : nb < 8 ? 8 : nb < 16 ? 16 : nb < 32 ? 32 : 64;
     require(nb < 64, "blocked CSR: the row split takes at most 63 blocks");
@@ -758,9 +819,20 @@ bool split_rows(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
     a.bci16 = bk.idx16 ? bk.bci.as<uint16_t>() : nullptr;
     a.bv = v ? bk.bv.as<float>() : nullptr;
     if (nnz_src > 0) {
-        rows_scatter_kernel<<<static_cast<unsigned>(ceil_div(n, 4)), 256, 0, s>>>(a);
+        const unsigned rgrid = static_cast<unsigned>(ceil_div(n, 4));
+        // the long rows: a fixed grid (their number stays on the device)
+        if (nb <= 8) {
+            rows_scatter_kernel<8><<<rgrid, 256, 0, s>>>(a);
+            TG_LAUNCH_CHECK();
+            rows_scatter_long_kernel<8><<<256, 64 * kLongWaves, 0, s>>>(a);
+        } else {
+            rows_scatter_kernel<0><<<rgrid, 256, 0, s>>>(a);
+            TG_LAUNCH_CHECK();
+            rows_scatter_long_kernel<0><<<256, 64 * kLongWaves, 0, s>>>(a);
+        }
         TG_LAUNCH_CHECK();
     }
+    fire_after_split(bk);
     if (vdiag) {
         flat_diag_kernel<<<grid(n), 256, 0, s>>>(a, brp);
         TG_LAUNCH_CHECK();
@@ -802,6 +874,7 @@ void split_general(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const
                                                   bk.idx16 ? bk.bci.as<uint16_t>() : nullptr,
                                                   v ? bk.bv.as<float>() : nullptr, nullptr);
     TG_LAUNCH_CHECK();
+    fire_after_split(bk);
     int32_t* hf = reinterpret_cast<int32_t*>(bk.host.as<int64_t>() + 4 * nb);
     TG_HIP(hipMemcpyAsync(hf, disorder, sizeof(int32_t), hipMemcpyDeviceToHost, s));
     build_block_plans(bk, max_f, chunk, s);

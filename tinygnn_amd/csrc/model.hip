@@ -135,6 +135,10 @@ struct tg_model_s {
     hipStream_t side = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     DeviceBuffer pre, pre_w, pre_dis, pre_flag;
+    // launches that transform; set during a reference-semantics call's
+    // preprocessing, whose first blocked build calls it after its scatter
+    // (BlockedCSR::after_split)
+    std::function<void()> fork_hook;
 
     tg_model_s() = default;
     tg_model_s(const tg_model_s&) = delete;
@@ -320,6 +324,7 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     } else if ((m.need_norm() || m.need_sl()) && r_sl > 0) {
         if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
         m.blk_sl->resident = m.resident && !exact && gc_sl == 32;  // the factored GCN's sums
+        m.blk_sl->after_split = m.fork_hook;
         build_blocked(*m.blk_sl, n, nnz + n, m.sl_rp.as<int32_t>(), m.sl_ci.as<int32_t>(),
                       m.need_norm() && !m.unit_sl ? m.sl_v.as<float>() : nullptr, r_sl, maxf, s,
                       chunk);
@@ -332,6 +337,7 @@ void prepare_blocked(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     if (m.need_raw_mean() && r_raw > 0) {
         if (!m.blk_raw) m.blk_raw = std::make_unique<BlockedCSR>();
         m.blk_raw->resident = m.resident && !exact;  // SAGE's mean: plain sums
+        m.blk_raw->after_split = m.fork_hook;
         build_blocked(*m.blk_raw, n, nnz, rp, ci, nullptr, r_raw, maxf, s, chunk);
         m.blk_raw->group_cols = 32;
         if (exact && !m.blk_raw->in_order) m.blk_raw.reset();
@@ -456,6 +462,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
             if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
             m.blk_sl->resident = m.resident && gcn_direct;  // (fast precision only)
             // (synchronises s: host[1] is current after the call)
+            m.blk_sl->after_split = m.fork_hook;
             const bool built =
                 build_blocked_self_loops(*m.blk_sl, n, nnz, rp, ci, r_unit, maxf, s, chunk);
             if (built && host[1] == 0) {
@@ -532,17 +539,19 @@ size_t scores_bytes(const tg_model_s& m, int64_t n) {
 // checks it against the preprocessing's outcome, and layer 0 recomputes
 // the transform when it differs.
 struct PreTransform {
-    bool on = false;
+    bool ready = false;     // planned: its buffers reserved, its layout chosen
+    bool deferred = false;  // to start inside the preprocessing (a blocked build)
+    bool on = false;        // launched
     bool tiled = false;     // GCN / SAGE: T tile-major
     bool factored = false;  // GCN: rows scaled by D^-1/2
 };
 
-PreTransform launch_pre_transform(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
-                                  const float* x, hipStream_t s) {
+// Chooses layer 0's side-stream transform and reserves its buffers (before
+// any of the call's work is in flight).
+PreTransform plan_pre_transform(tg_model_s& m, int64_t n, int64_t nnz) {
     PreTransform p;
     const Layer& l = m.layers[0];
     const bool exact = m.precision == TG_PRECISION_EXACT;
-    const int algo = exact ? TG_GEMM_INORDER : TG_GEMM_AUTO;
     const bool sage_tf =
         l.type == LType::SAGE &&
         sage_dataflow_for(exact ? TG_SAGE_CONCAT : m.sage_dataflow, l.agg, l.in, l.out, nnz) ==
@@ -572,6 +581,25 @@ PreTransform launch_pre_transform(tg_model_s& m, int64_t n, int64_t nnz, const i
         m.pre.reserve(sage_tf_floats(n, l.out) * sizeof(float));
         m.pre_w.reserve(l.in * 2 * gather_pitch(l.out) * sizeof(float));
     }
+    // whether the preprocessing builds a blocked copy (A + I's in either
+    // lane-group width, or A's for SAGE's mean) to start it from
+    const bool sl_blk = (m.need_norm() || m.need_sl()) &&
+                        (resolve_block_rows(m.block_rows, n, nnz + n, 32) > 0 ||
+                         resolve_block_rows(m.block_rows, n, nnz + n, 64) > 0);
+    const bool raw_blk = m.need_raw_mean() && resolve_block_rows(m.block_rows, n, nnz, 32) > 0;
+    p.deferred = sl_blk || raw_blk;
+    p.ready = true;
+    return p;
+}
+
+// Launches layer 0's transform planned by plan_pre_transform on the side
+// stream, after the work enqueued on s so far.
+void fork_pre_transform(tg_model_s& m, PreTransform& p, int64_t n, const int32_t* rp,
+                        const float* x, hipStream_t s) {
+    if (!p.ready || p.on) return;
+    const Layer& l = m.layers[0];
+    const bool exact = m.precision == TG_PRECISION_EXACT;
+    const int algo = exact ? TG_GEMM_INORDER : TG_GEMM_AUTO;
     hipStream_t t = m.side;
     TG_HIP(hipEventRecord(m.ev_fork, s));
     TG_HIP(hipStreamWaitEvent(t, m.ev_fork, 0));
@@ -615,7 +643,6 @@ PreTransform launch_pre_transform(tg_model_s& m, int64_t n, int64_t nnz, const i
     }
     TG_HIP(hipEventRecord(m.ev_join, t));
     p.on = true;
-    return p;
 }
 
 // Whether the side stream's transform has the layout layer 0 needs after
@@ -666,10 +693,31 @@ void forward(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, const int
     // a reference-semantics call preprocesses the adjacency every time:
     // layer 0's transform runs beside it on the side stream (a cached call's
     // one-time build keeps the single stream, and allocates no side buffers)
+    // It starts when the preprocessing's first blocked build has enqueued
+    // its scatter: the split's passes are latency-bound and slow down several
+    // times beside the GEMM, whose workgroups hold the CUs' slots; without a
+    // blocked build it starts at once.
     PreTransform pre;
     if (mode == TG_FORWARD_REFERENCE && !adjacency_cached(m, n, nnz, rp, ci, v, mode))
-        pre = launch_pre_transform(m, n, nnz, rp, x, s);
-    prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
+        pre = plan_pre_transform(m, n, nnz);
+    auto clear_hooks = [&]() {
+        m.fork_hook = nullptr;
+        if (m.blk_sl) m.blk_sl->after_split = nullptr;
+        if (m.blk_raw) m.blk_raw->after_split = nullptr;
+    };
+    clear_hooks();
+    if (pre.ready && pre.deferred)
+        m.fork_hook = [&m, &pre, n, rp, x, s]() { fork_pre_transform(m, pre, n, rp, x, s); };
+    else
+        fork_pre_transform(m, pre, n, rp, x, s);
+    try {
+        prepare_adjacency(m, n, nnz, rp, ci, v, mode, s);
+    } catch (...) {
+        clear_hooks();
+        throw;
+    }
+    clear_hooks();
+    fork_pre_transform(m, pre, n, rp, x, s);  // (no blocked build started it)
     if (pre.on) TG_HIP(hipStreamWaitEvent(s, m.ev_join, 0));
     const bool use_pre = pre_matches(m, pre);
 
