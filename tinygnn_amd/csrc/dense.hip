@@ -55,25 +55,17 @@ __device__ __forceinline__ float epi_act(float x) {
     return x;
 }
 
-// c_index as one formula: element (m, n) at (n / 32) * tile + m * row + n % 32
-// (row-major: tile = 32, row = ldc).
-struct CStrides {
-    int64_t tile, row;
-};
-__device__ __forceinline__ CStrides c_strides(const GemmArgs& g) {
-    return g.c_tile_stride > 0 ? CStrides{g.c_tile_stride, 32} : CStrides{32, g.ldc};
-}
-
 // Stores one lane's outputs of MI x NJ 16x16 MFMA tiles (D layout of
 // v_mfma_f32_16x16x4f32: lane (q, r) holds rows 4q..4q+3 of column r), the
 // tiles' rows from mb, columns from nb: C[m][n] = EPI(acc * row_scale[m] +
-// bias[n]) as epi_out computes it.  The row factors and bias terms are loaded
-// before the first store: C may alias them as far as the compiler knows, so
-// loads between the stores would each wait for a round trip.  A missing row
-// factor is 1 (x * 1 = x exactly), and the store loop has no branch but the
-// bounds (per-element loads and epilogue branches cost 6% of the config-E
-// layer-1 transform).
-template <int EPI, int MI, int NJ>
+// bias[n]) as epi_out computes it, C tile-major (TILED) or row-major.  The
+// row factors and bias terms are loaded before the first store: C may alias
+// them as far as the compiler knows, so loads between the stores would each
+// wait for a round trip.  A missing row factor is 1 (x * 1 = x exactly), and
+// the store loop has no branch but the bounds.  (Per-element loads and
+// epilogue branches cost 6% of the config-E layer-1 transform, one index
+// formula for both layouts with a run-time row stride another 2.5%.)
+template <int EPI, bool TILED, int MI, int NJ>
 __device__ __forceinline__ void store_tiles(const GemmArgs& g, const v4f (&acc)[MI][NJ],
                                             int64_t mb, int64_t nb, int q, int r) {
     float rsv[MI][4], bv[NJ];
@@ -90,23 +82,32 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& g, const v4f (&acc)[
         bv[j] = (g.bias && n < g.n) ? g.bias[n] : 0.0f;
     }
     const bool has_bias = g.bias != nullptr;
-    const CStrides cs = c_strides(g);
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const int64_t gn = nb + j * 16 + r;
             if (gn >= g.n) continue;
-            float* cc = g.c + (gn >> 5) * cs.tile + (gn & 31);
+            float* cc = TILED ? g.c + (gn >> 5) * g.c_tile_stride + (gn & 31) : g.c + gn;
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int64_t m = mb + i * 16 + 4 * q + rr;
                 if (m >= g.m) continue;
                 float x = acc[i][j][rr] * rsv[i][rr];
                 if (has_bias) x = x + bv[j];
-                cc[m * cs.row] = epi_act<EPI>(x);
+                cc[TILED ? m * 32 : m * g.ldc] = epi_act<EPI>(x);
             }
         }
+}
+
+// store_tiles for C's layout (GemmArgs::c_tile_stride).
+template <int EPI, int MI, int NJ>
+__device__ __forceinline__ void store_tiles_c(const GemmArgs& g, const v4f (&acc)[MI][NJ],
+                                              int64_t mb, int64_t nb, int q, int r) {
+    if (g.c_tile_stride > 0)
+        store_tiles<EPI, true>(g, acc, mb, nb, q, r);
+    else
+        store_tiles<EPI, false>(g, acc, mb, nb, q, r);
 }
 
 // store_tiles with the epilogue chosen at run time (one of three bodies runs).
@@ -114,11 +115,11 @@ template <int MI, int NJ>
 __device__ __forceinline__ void store_tiles_any(const GemmArgs& g, const v4f (&acc)[MI][NJ],
                                                 int64_t mb, int64_t nb, int q, int r) {
     if (g.epi == TG_EPI_RELU)
-        store_tiles<TG_EPI_RELU>(g, acc, mb, nb, q, r);
+        store_tiles_c<TG_EPI_RELU>(g, acc, mb, nb, q, r);
     else if (g.epi == TG_EPI_ELU)
-        store_tiles<TG_EPI_ELU>(g, acc, mb, nb, q, r);
+        store_tiles_c<TG_EPI_ELU>(g, acc, mb, nb, q, r);
     else
-        store_tiles<TG_EPI_NONE>(g, acc, mb, nb, q, r);
+        store_tiles_c<TG_EPI_NONE>(g, acc, mb, nb, q, r);
 }
 
 // ---------------------------------------------------------------------------
@@ -652,16 +653,15 @@ __global__ __launch_bounds__(256, 3) void gemm_mfma_kernel(GemmArgs g) {
     v4f ra0, ra1, rb0, rb1;
 
     auto fetch = [&](int64_t kt) {
-        const bool seg2 = kt >= t1;
-        const float* pa = seg2 ? pa2 : pa1;
+        const bool seg2 = kt >= t1;  // uniform, as is everything but the lanes' rows
         const int64_t ldb = seg2 ? g.ldb2 : g.ldb1;
         const int64_t K = seg2 ? g.k2 : g.k1;
         const int64_t k0 = (seg2 ? kt - t1 : kt) * kMBK;
-        const int64_t kb = k0 + bkr;
-        const float* pb = kb < K ? (seg2 ? pb2 : pb1) + k0 * ldb : (seg2 ? g.b2 : g.b1);
-        if (k0 + kMBK <= K) {  // whole k range (uniform)
-            ra0 = load4<VA>(pa + k0, 4);
-            ra1 = load4<VA>(pa + k0 + 8, 4);
+        const float* pa = (seg2 ? pa2 : pa1) + k0;
+        if (k0 + kMBK <= K) {  // whole k range
+            const float* pb = (seg2 ? pb2 : pb1) + k0 * ldb;
+            ra0 = load4<VA>(pa, 4);
+            ra1 = load4<VA>(pa + 8, 4);
             if (colfull) {
                 rb0 = load4<VB>(pb + nb0, 4);
                 rb1 = load4<VB>(pb + nb1, 4);
@@ -670,9 +670,11 @@ __global__ __launch_bounds__(256, 3) void gemm_mfma_kernel(GemmArgs g) {
                 rb1 = load4<VB>(pb + nb1, N - nb1);
             }
         } else {
+            const int64_t kb = k0 + bkr;
+            const float* pb = kb < K ? (seg2 ? pb2 : pb1) + k0 * ldb : (seg2 ? g.b2 : g.b1);
             const int64_t ka = k0 + 4 * ac;
-            ra0 = load4<1>(pa + k0, gm < M ? K - ka : 0);
-            ra1 = load4<1>(pa + k0 + 8, gm < M ? K - ka - 8 : 0);
+            ra0 = load4<1>(pa, gm < M ? K - ka : 0);
+            ra1 = load4<1>(pa + 8, gm < M ? K - ka - 8 : 0);
             rb0 = load4<1>(pb + nb0, kb < K ? N - nb0 : 0);
             rb1 = load4<1>(pb + nb1, kb < K ? N - nb1 : 0);
         }
@@ -720,7 +722,7 @@ __global__ __launch_bounds__(256, 3) void gemm_mfma_kernel(GemmArgs g) {
         if (kt + 1 < nt) stage(cb ^ 1);
         __syncthreads();
     }
-    store_tiles<EPI>(g, acc, m0 + wm, n0 + wn, q, r);
+    store_tiles_c<EPI>(g, acc, m0 + wm, n0 + wn, q, r);
 }
 
 // ---------------------------------------------------------------------------
