@@ -375,7 +375,8 @@ def test_blocking_across_modes(gpu):
         np.testing.assert_array_equal(got, want, err_msg=f"call {i} mode {mode} blocking {blocking}")
 
 
-@pytest.mark.parametrize("variant", ["unit", "diagonal", "last_weight", "unit_gat_stack"])
+@pytest.mark.parametrize("variant", ["unit", "diagonal", "last_weight", "unit_gat_stack",
+                                     "unit_dense", "diagonal_dense"])
 def test_blocked_gcn_unit_weights(gpu, restate, variant):
     """GCN over an edge list's CSR (every value 1, no diagonal): in fast
     precision the blocked aggregation is factored (D^-1/2 applied in the
@@ -386,11 +387,15 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     (past the check's 128-bit reads: nnz % 4 != 0), keeps the weighted
     blocked passes, with the same guarantees; so does exact precision
     (bit-exact).  A GAT layer before the GCN shares the blocked A + I (its
-    weighted passes in 64-column groups, the factored GCN's too)."""
+    weighted passes in 64-column groups, the factored GCN's too).  The dense
+    variants (100 entries per row on average) build A + I's copy by the row
+    split, whose search finds the diagonal."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(57)
     n = 3000
-    a = random_csr(rng, n, n, avg_deg=40, max_deg=2800, empty_frac=0.05)
+    dense = variant.endswith("_dense")
+    variant = variant.replace("_dense", "")
+    a = random_csr(rng, n, n, avg_deg=100 if dense else 40, max_deg=2800, empty_frac=0.05)
     rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
     keep = rows != a.col_ind
     src, dst = rows[keep], a.col_ind[keep].astype(np.int32)
