@@ -472,6 +472,28 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
     np.testing.assert_array_equal(exact[100].view(np.int32), exact[0].view(np.int32))
     if variant != "unit_gat_stack":
         np.testing.assert_array_equal(exact[100].view(np.int32), want.view(np.int32))
+    if variant == "last_weight":
+        # one model, reference-semantics calls over unit and weighted values
+        # in turn: after a unit answer the next check is read only after the
+        # direct split, which weighted values then drop; after a weighted
+        # answer the check is read first.  Every call gives a fresh model's
+        # bits for its values.
+        g_unit = restate.edge_list_to_csr(src, dst, n)
+        want_unit = restate.model_forward(spec, w, g_unit, x)
+        da_unit = tg.DeviceCSR(n, n, da.row_ptr, da.col_ind, gpu.ones_like(da.val))
+        fresh = tg.Model.from_spec(spec, w)
+        fresh.set_blocking(100)
+        got_unit = fresh.forward(da_unit, xt).cpu().numpy()
+        assert fresh.blocking_info()["sl_direct"]
+        assert_close(got_unit, want_unit, what="gcn unit values")
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(100)
+        calls = [(da_unit, got_unit, True), (da, outs[100], False), (da_unit, got_unit, True),
+                 (da, outs[100], False), (da, outs[100], False), (da_unit, got_unit, True)]
+        for i, (csr, expect, direct) in enumerate(calls):
+            got = m.forward(csr, xt, mode=tg.FORWARD_REFERENCE).cpu().numpy()
+            np.testing.assert_array_equal(bits(got), bits(expect), err_msg=f"call {i}")
+            assert m.blocking_info()["sl_direct"] == direct, f"call {i}"
 
 
 @pytest.mark.parametrize("avg_deg", [30, 100])

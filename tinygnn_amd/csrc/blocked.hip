@@ -435,9 +435,10 @@ __global__ __launch_bounds__(256) void flat_diag_kernel(FlatSplit a, const int32
 // ---------------------------------------------------------------------------
 constexpr int64_t kRowSplitMinAvg = 64;
 // entries of a row that its own wavefront writes; the rest of a longer row
-// is shared by a workgroup of kLongWaves wavefronts
+// is shared by the four wavefronts of one of the scatter's first kLongWgs
+// workgroups
 constexpr int kRowCap = 2048;
-constexpr int kLongWaves = 16;
+constexpr int kLongWgs = 1024;
 
 // The first position in ci[lo, hi) whose column is >= key (ci[lo, hi) sorted).
 __device__ __forceinline__ int lower_bound_col(const int32_t* __restrict__ ci, int lo, int hi,
@@ -490,7 +491,7 @@ __global__ __launch_bounds__(256) void rows_search_kernel(FlatSplit a, int32_t* 
         a.starts[t] = sj;
         cnt[t] = e - sj + (j == d ? 1 : 0);
     }
-    // rows past the per-row scatter's share, for rows_scatter_long_kernel
+    // rows past the per-row scatter's share, for the scatter's first workgroups
     if (j == 0 && len > kRowCap) a.long_rows[atomicAdd(&a.flags[3], 1)] = static_cast<int32_t>(r);
     if (a.vdiag && j == 0) {
         ins = ins < sd ? sd : (ins > sd1 ? sd1 : ins);
@@ -577,36 +578,36 @@ __device__ __forceinline__ void row_blocks(const FlatSplit& a, int64_t r, int la
     }
 }
 
-// One wavefront per row, its first kRowCap entries (one wavefront walking a
-// 20,000-entry row alone bounded the whole pass: config E's A + I 0.37 ms).
+// The scatter, one launch.  Workgroups kLongWgs and above: one wavefront
+// per row, its first kRowCap entries (one wavefront walking a 20,000-entry
+// row alone bounded the whole pass: config E's A + I 0.37 ms).  The first
+// kLongWgs workgroups: the rest of every row longer than kRowCap (rows
+// a.long_rows[0 .. flags[3]), taken in turn), the four wavefronts of a
+// workgroup taking the row's slice groups in turn.  Launched first, they run
+// beside the per-row part (a launch of their own after it: 0.14 ms of
+// config E's 0.33 ms scatter).
 template <int NBM>
 __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
     const int lane = threadIdx.x & 63;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    const int w = threadIdx.x >> 6;
+    int ob, st;
+    if (blockIdx.x < kLongWgs) {
+        const int count = a.flags[3];
+        for (int i = blockIdx.x; i < count; i += kLongWgs) {
+            const int64_t r = a.long_rows[i];
+            const int lo = a.rp[r], hi = a.rp[r + 1];
+            row_blocks(a, r, lane, ob, st);
+            scatter_range<NBM>(a, r, lo, hi, lo + kRowCap + w * 64 * kRowSU, hi,
+                               4 * 64 * kRowSU, ob, st, lane);
+        }
+        return;
+    }
+    const int64_t r = static_cast<int64_t>(blockIdx.x - kLongWgs) * 4 + w;
     if (r >= a.n) return;  // uniform per wave
     const int lo = a.rp[r], hi = a.rp[r + 1];
-    int ob, st;
     row_blocks(a, r, lane, ob, st);
     const int ke = hi - lo > kRowCap ? lo + kRowCap : hi;
     scatter_range<NBM>(a, r, lo, hi, lo, ke, 64 * kRowSU, ob, st, lane);
-}
-
-// The rest of every row longer than kRowCap: a workgroup per row (rows
-// a.long_rows[0 .. flags[3]), taken in turn by a fixed grid), its
-// wavefronts taking the slice groups in turn.
-template <int NBM>
-__global__ __launch_bounds__(64 * kLongWaves) void rows_scatter_long_kernel(FlatSplit a) {
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int count = a.flags[3];
-    for (int i = blockIdx.x; i < count; i += gridDim.x) {
-        const int64_t r = a.long_rows[i];
-        const int lo = a.rp[r], hi = a.rp[r + 1];
-        int ob, st;
-        row_blocks(a, r, lane, ob, st);
-        scatter_range<NBM>(a, r, lo, hi, lo + kRowCap + w * 64 * kRowSU, hi,
-                      kLongWaves * 64 * kRowSU, ob, st, lane);
-    }
 }
 
 }  // namespace
@@ -819,17 +820,13 @@ bool split_rows(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
     a.bci16 = bk.idx16 ? bk.bci.as<uint16_t>() : nullptr;
     a.bv = v ? bk.bv.as<float>() : nullptr;
     if (nnz_src > 0) {
-        const unsigned rgrid = static_cast<unsigned>(ceil_div(n, 4));
-        // the long rows: a fixed grid (their number stays on the device)
-        if (nb <= 8) {
-            rows_scatter_kernel<8><<<rgrid, 256, 0, s>>>(a);
-            TG_LAUNCH_CHECK();
-            rows_scatter_long_kernel<8><<<256, 64 * kLongWaves, 0, s>>>(a);
-        } else {
-            rows_scatter_kernel<0><<<rgrid, 256, 0, s>>>(a);
-            TG_LAUNCH_CHECK();
-            rows_scatter_long_kernel<0><<<256, 64 * kLongWaves, 0, s>>>(a);
-        }
+        // the long rows' workgroups first (their number stays on the device)
+        const int64_t rgrid = kLongWgs + ceil_div(n, 4);
+        require(rgrid < (int64_t(1) << 31), "blocked CSR: too many rows");
+        if (nb <= 8)
+            rows_scatter_kernel<8><<<static_cast<unsigned>(rgrid), 256, 0, s>>>(a);
+        else
+            rows_scatter_kernel<0><<<static_cast<unsigned>(rgrid), 256, 0, s>>>(a);
         TG_LAUNCH_CHECK();
     }
     fire_after_split(bk);

@@ -117,6 +117,10 @@ struct tg_model_s {
     // blk_sl was split from A directly with the diagonal placed per row, and
     // A + I itself (sl_rp, sl_ci, sl_v) was not written
     bool blk_sl_direct = false;
+    // the last unit-value check's answer: while it was yes, the next check
+    // is read after the direct split's own synchronisation (the split
+    // assuming unit values, dropped when they are not) instead of before it
+    bool unit_guess = true;
     DeviceBuffer flag;
     tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
@@ -416,6 +420,11 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         // aggregation is factored (it reads no values); unblocked, the
         // check and its synchronisation are skipped
         bool unit_v = false;
+        // the check's answer read after the direct split (below), which
+        // then assumes unit values (GCN without GAT, the direct split on,
+        // and the last check said yes): one synchronisation and the launch
+        // gaps after it fewer per call
+        bool unit_late = false;
         if (m.need_norm() && m.precision != TG_PRECISION_EXACT && will_block) {
             fill_i32(m.flag.as<int32_t>(), 1, 1, s);
             const int64_t blocks =
@@ -429,8 +438,12 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
             TG_LAUNCH_CHECK();
             TG_HIP(hipMemcpyAsync(host, m.flag.as<int32_t>(), sizeof(int32_t),
                                   hipMemcpyDeviceToHost, s));
-            TG_HIP(hipStreamSynchronize(s));
-            unit_v = host[0] == 1;
+            unit_late = m.unit_guess && m.direct_split && !m.need_sl();
+            if (!unit_late) {
+                TG_HIP(hipStreamSynchronize(s));
+                unit_v = host[0] == 1;
+                m.unit_guess = unit_v;
+            }
         }
         // A + I's values: GAT reads the structure alone; GCN needs the
         // normalised values unless its aggregation will run factored
@@ -440,7 +453,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         for (auto& l : m.layers)
             if (l.type == LType::GAT && !gat_blocked_ok(l.heads, l.out, l.concat))
                 gat_online = false;
-        const bool gcn_direct = unit_v && !m.need_sl();
+        const bool gcn_direct = (unit_v || unit_late) && !m.need_sl();
         const bool gat_direct = m.need_sl() && gat_online;
         if (m.direct_split && will_block && (gcn_direct || gat_direct)) {
             // Only blocked passes without values read A + I (the factored
@@ -461,11 +474,15 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
             }
             if (!m.blk_sl) m.blk_sl = std::make_unique<BlockedCSR>();
             m.blk_sl->resident = m.resident && gcn_direct;  // (fast precision only)
-            // (synchronises s: host[1] is current after the call)
+            // (synchronises s: host[0] and host[1] are current after the call)
             m.blk_sl->after_split = m.fork_hook;
             const bool built =
                 build_blocked_self_loops(*m.blk_sl, n, nnz, rp, ci, r_unit, maxf, s, chunk);
-            if (built && host[1] == 0) {
+            if (unit_late) {
+                unit_v = host[0] == 1;
+                m.unit_guess = unit_v;
+            }
+            if (built && host[1] == 0 && (unit_v || !gcn_direct)) {
                 m.blk_sl->group_cols = gcn_direct ? 32 : 64;
                 m.blk_sl_direct = true;
                 m.unit_sl = gcn_direct;
