@@ -602,14 +602,29 @@ def run_forward_e(args, torch, tg):
         # the timed (cached) forward's raw outputs and logits are the ones checked
         raw = y.cpu().numpy()
         logits = tg.log_softmax_(y.clone()).cpu().numpy()
+        # reference-semantics calls (the adjacency preprocessed in every
+        # call), timed as the cached ones: untimed warm-up calls, then calls
+        # back to back, each bracketed by events on the stream
+        for _ in range(args.fwd_warmup):
+            model.forward(adj, x, mode=tg.FORWARD_REFERENCE, out=y)
+        torch.cuda.synchronize()
         timer = StreamTimer(torch, stream)
-        for _ in range(3):
-            torch.cuda.synchronize()
+        for _ in range(args.fwd_steps):
             e0 = timer.start()
             model.forward(adj, x, mode=tg.FORWARD_REFERENCE, out=y)
             timer.stop(e0)
         torch.cuda.synchronize()
         refsem = float(np.median(timer.ms()))
+        # and each from an idle GPU (a synchronisation before the call: the
+        # host's time to its first launch included)
+        timer = StreamTimer(torch, stream)
+        for _ in range(5):
+            torch.cuda.synchronize()
+            e0 = timer.start()
+            model.forward(adj, x, mode=tg.FORWARD_REFERENCE, out=y)
+            timer.stop(e0)
+        torch.cuda.synchronize()
+        refsem_idle = float(np.median(timer.ms()))
         raw_r = y.cpu().numpy()
         logits_r = tg.log_softmax_(y.clone()).cpu().numpy()
         # the same model in exact precision (the reference's operation order)
@@ -630,6 +645,7 @@ def run_forward_e(args, torch, tg):
                                                  256 if name != "gat" else 64, synth.E_CLASSES,
                                                  4, blocking, l2_rate)
         r = dict(gpu_ms=round(cached, 3), gpu_ms_reference_semantics=round(refsem, 3),
+                 gpu_ms_reference_semantics_from_idle=round(refsem_idle, 3),
                  first_forward_ms=round(first_ms, 2),
                  one_time_preprocessing_ms=round(first_ms - cached, 2),
                  cpp_api=cpp,
@@ -645,7 +661,7 @@ def run_forward_e(args, torch, tg):
                                    "gathered lines x 128 B at the box's L2 read ceiling "
                                    "(l2_read: plain coalesced loads of an L2-resident buffer)")
         log(f"{name}: first forward {first_ms:.1f} ms; cached {cached:.2f} ms, reference "
-            f"semantics {refsem:.2f} ms, exact {exact_ms:.2f} ms; roofline {troof:.3f} ms, "
+            f"semantics {refsem:.2f} ms ({refsem_idle:.2f} from idle), exact {exact_ms:.2f} ms; roofline {troof:.3f} ms, "
             f"gather bound "
             f"{troof_l2 or 0:.3f} ms ({(troof_l2 or 0) / cached:.3f})")
         if ref is not None:
