@@ -500,7 +500,7 @@ __global__ __launch_bounds__(256) void rows_search_kernel(FlatSplit a, int32_t* 
     }
 }
 
-constexpr int kRowSU = 4;  // 64-entry slices in flight per wavefront
+constexpr int kRowSU = 8;  // 64-entry slices in flight per wavefront
 
 // Entries [kb, ke) of row r (entries [lo, hi)) to the copy: entry k of block
 // b goes to obase[b][r] + k (one further past the virtual entry in its
@@ -511,15 +511,34 @@ constexpr int kRowSU = 4;  // 64-entry slices in flight per wavefront
 // lands in its (block, row) segment.  Column-derived blocks (a
 // double-precision division and three lane shuffles per entry) measured the
 // same.  `step`: the distance between this wavefront's slice groups.
-template <int NBM>  // at most NBM blocks (their starts in scalar registers) or any (0)
+//
+// Each 64-entry slice finds the blocks of its first and last positions (a
+// ballot of the starts at or before them), and lanes compare their
+// positions only with the starts inside the slice (a slice in one block:
+// none).  The virtual entry's shift is positional too: in block d (the
+// diagonal's), the entries from ins[r] (the first column >= r, clamped to
+// the block's run) to the block's end, which for a sorted row without a
+// diagonal are those of columns > r.  The predecessor column (the order
+// check) comes from a wavefront shift.  (Lanes counting every start made
+// the pass VALU-bound: about 55 vector instructions per slice, config E's
+// A + I 0.19 ms of the scatter.)  Every lane of the wavefront calls it with
+// the same row (r, lo, hi, kb, ke uniform).
 __device__ __forceinline__ void scatter_range(const FlatSplit& a, int64_t r, int lo, int hi,
                                               int kb, int ke, int step, int ob, int st,
                                               int lane) {
-    const int d = a.vdiag ? block_of(static_cast<int>(r), a) : -1;
-    const int nb = a.nb;
-    int sv[NBM > 0 ? NBM : 1];
-#pragma unroll
-    for (int j = 0; j < NBM; ++j) sv[j] = __builtin_amdgcn_readlane(st, j);
+    constexpr int kNone = 0x7FFFFFFF;
+    const int row = static_cast<int>(r);
+    const int R = a.rows_per_block;
+    // positions [ins_lo, ins_lo + ins_n) move up one (the virtual entry's
+    // block from the virtual entry on); ins_n = 0: none
+    int ins_lo = 0;
+    unsigned ins_n = 0;
+    if (a.vdiag) {
+        const int d = block_of(row, a);
+        ins_lo = a.ins[r];
+        const int e = __builtin_amdgcn_readlane(st, d + 1);  // d + 1 <= nb < 64
+        ins_n = static_cast<unsigned>((e == kNone ? hi - lo : e) - ins_lo);
+    }
     for (int k0 = kb; k0 < ke; k0 += step) {
         const int kend = k0 + 64 * kRowSU < ke ? k0 + 64 * kRowSU : ke;
         int c[kRowSU];
@@ -534,34 +553,39 @@ __device__ __forceinline__ void scatter_range(const FlatSplit& a, int64_t r, int
         int carry = k0 > lo ? a.ci[k0 - 1] : 0;
 #pragma unroll
         for (int u = 0; u < kRowSU; ++u) {
-            const int k = k0 + u * 64 + lane;
-            // every lane takes part in the shuffles (a shuffle inside a
-            // condition would read the lanes it leaves out as zeros)
-            int pc = __shfl_up(c[u], 1, 64);
-            if (lane == 0) pc = carry;
-            carry = __shfl(c[u], 63, 64);
-            // the entry's block: the number of block starts at or before it
+            const int ks = k0 + u * 64;  // the slice's first entry
+            if (ks >= kend) break;
+            const int k = ks + lane;
             const int kr = k - lo;
-            int b = 0;
-            if constexpr (NBM > 0) {
-#pragma unroll
-                for (int j = 1; j < NBM; ++j) b += kr >= sv[j] ? 1 : 0;
-            } else {
-                for (int j = 1; j < nb; ++j)
-                    b += kr >= __builtin_amdgcn_readlane(st, j) ? 1 : 0;
+            // every lane takes part in the shift and the read (lanes past
+            // the end included)
+            const int pc = __builtin_amdgcn_update_dpp(carry, c[u], 0x138 /* wave_shr:1 */, 0xF,
+                                                       0xF, false);
+            carry = __builtin_amdgcn_readlane(c[u], 63);
+            // the blocks of the slice's first and last positions: the starts
+            // 1.. at or before them (lane j holds block j's start)
+            const int f = ks - lo, l = f + 63;
+            const int bl = __popcll(__ballot(st <= f) & ~1ull);
+            const int bh = __popcll(__ballot(st <= l) & ~1ull);
+            int base = __builtin_amdgcn_readlane(ob, bl);
+            int boff = bl * R;
+            for (int j = bl + 1; j <= bh; ++j) {  // starts inside the slice
+                const bool past = kr >= __builtin_amdgcn_readlane(st, j);
+                base = past ? __builtin_amdgcn_readlane(ob, j) : base;
+                boff = past ? j * R : boff;
             }
-            const int base = __shfl(ob, b, 64);
-            if (k >= kend) continue;
-            const int c0 = c[u];
-            if (k > lo && pc > c0) atomicOr(&a.flags[0], 1);
-            if (a.vdiag && c0 == r) atomicOr(&a.flags[1], 1);
-            int o = base + k;
-            if (a.vdiag && c0 > r && b == d) ++o;
-            if (a.bci16)
-                a.bci16[o] = static_cast<uint16_t>(c0 - b * a.rows_per_block);
-            else
-                a.bci[o] = c0;
-            if (a.bv) a.bv[o] = x[u];
+            if (k < kend) {
+                const int c0 = c[u];
+                if (kr > 0 && pc > c0) atomicOr(&a.flags[0], 1);
+                if (a.vdiag && c0 == row) atomicOr(&a.flags[1], 1);
+                const unsigned o = static_cast<unsigned>(base + k) +
+                                   (static_cast<unsigned>(kr - ins_lo) < ins_n ? 1u : 0u);
+                if (a.bci16)
+                    a.bci16[o] = static_cast<uint16_t>(c0 - boff);
+                else
+                    a.bci[o] = c0;
+                if (a.bv) a.bv[o] = x[u];
+            }
         }
     }
 }
@@ -586,10 +610,10 @@ __device__ __forceinline__ void row_blocks(const FlatSplit& a, int64_t r, int la
 // workgroup taking the row's slice groups in turn.  Launched first, they run
 // beside the per-row part (a launch of their own after it: 0.14 ms of
 // config E's 0.33 ms scatter).
-template <int NBM>
 __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    // the wavefront's index, uniform (and so its row, bounds and slices)
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     int ob, st;
     if (blockIdx.x < kLongWgs) {
         const int count = a.flags[3];
@@ -597,7 +621,7 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
             const int64_t r = a.long_rows[i];
             const int lo = a.rp[r], hi = a.rp[r + 1];
             row_blocks(a, r, lane, ob, st);
-            scatter_range<NBM>(a, r, lo, hi, lo + kRowCap + w * 64 * kRowSU, hi,
+            scatter_range(a, r, lo, hi, lo + kRowCap + w * 64 * kRowSU, hi,
                                4 * 64 * kRowSU, ob, st, lane);
         }
         return;
@@ -607,7 +631,7 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(FlatSplit a) {
     const int lo = a.rp[r], hi = a.rp[r + 1];
     row_blocks(a, r, lane, ob, st);
     const int ke = hi - lo > kRowCap ? lo + kRowCap : hi;
-    scatter_range<NBM>(a, r, lo, hi, lo, ke, 64 * kRowSU, ob, st, lane);
+    scatter_range(a, r, lo, hi, lo, ke, 64 * kRowSU, ob, st, lane);
 }
 
 }  // namespace
@@ -823,10 +847,7 @@ bool split_rows(BlockedCSR& bk, const SplitTemps& t, const int32_t* rp, const in
         // the long rows' workgroups first (their number stays on the device)
         const int64_t rgrid = kLongWgs + ceil_div(n, 4);
         require(rgrid < (int64_t(1) << 31), "blocked CSR: too many rows");
-        if (nb <= 8)
-            rows_scatter_kernel<8><<<static_cast<unsigned>(rgrid), 256, 0, s>>>(a);
-        else
-            rows_scatter_kernel<0><<<static_cast<unsigned>(rgrid), 256, 0, s>>>(a);
+        rows_scatter_kernel<<<static_cast<unsigned>(rgrid), 256, 0, s>>>(a);
         TG_LAUNCH_CHECK();
     }
     fire_after_split(bk);
