@@ -440,15 +440,38 @@ constexpr int64_t kRowSplitMinAvg = 64;
 constexpr int kRowCap = 2048;
 constexpr int kLongWgs = 1024;
 
-// The first position in ci[lo, hi) whose column is >= key (ci[lo, hi) sorted).
+// The first position in ci[lo, hi) whose column is >= key (ci[lo, hi)
+// sorted), by 9-ary search: each round loads 8 evenly spaced columns of the
+// range at once and keeps the ninth between the last one below the key and
+// the first one at or above it, until at most 8 are left, which are loaded
+// and counted.  Three dependent rounds of loads for a 492-entry row, five for
+// 20,000 entries, against 9 and 15 probes of a binary search (config E's
+// row search 0.12 ms with those).  Whatever the order the result stays in
+// [lo, hi] and every load inside the range.
 __device__ __forceinline__ int lower_bound_col(const int32_t* __restrict__ ci, int lo, int hi,
                                                int64_t key) {
-    while (lo < hi) {
-        const int mid = lo + ((hi - lo) >> 1);
-        if (ci[mid] < key) lo = mid + 1;
-        else hi = mid;
+    int a = lo, b = hi;  // the answer is in [a, b]
+    while (b - a > 8) {
+        // positions a + floor((i + 1) w / 9), i = 0..7, without overflow
+        const int w = b - a, w9 = w / 9, r9 = w % 9;
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            c += ci[a + (i + 1) * w9 + ((i + 1) * r9) / 9] < key ? 1 : 0;
+        const int na = c == 0 ? a : a + c * w9 + (c * r9) / 9 + 1;
+        const int nb = c == 8 ? b : a + (c + 1) * w9 + ((c + 1) * r9) / 9;
+        a = na;
+        b = nb;
     }
-    return lo;
+    int c = 0;
+    if (b > a) {  // the last (at most 8) loaded together, clamped to the range
+        int v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ci[a + i < b ? a + i : b - 1];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c += (a + i < b && v[i] < key) ? 1 : 0;
+    }
+    return a + c;
 }
 
 // Per row: starts[b][r] (relative to the row) and the counts cnt[b][r] (the
