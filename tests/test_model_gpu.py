@@ -339,17 +339,20 @@ def test_blocking_setting(gpu):
         tg.Model.from_spec(spec, w).set_blocking(-2)
 
 
-def test_blocking_across_modes(gpu):
+@pytest.mark.parametrize("model", ["gcn", "sage"])
+def test_blocking_across_modes(gpu, model):
     """Both forward modes block.  With one setting, reference-mode forwards
     (preprocessing, plans and the blocked copy rebuilt in place on every
     call) and cached ones give the same bits, call after call and in any
-    order; a new setting takes effect on the next call in either mode."""
+    order; a new setting takes effect on the next call in either mode (for
+    SAGE-mean, whose blocked passes need no row plan of A: the plan is built
+    when a setting without blocking first needs it)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(21)
     n = 2000
     a = random_csr(rng, n, n, avg_deg=30, max_deg=1500, empty_frac=0.02)
     a.val[:] = np.abs(a.val) + 0.01
-    spec = synth.spec_gcn(24, 64, 5)
+    spec = synth.spec_gcn(24, 64, 5) if model == "gcn" else synth.spec_sage(24, 64, 5)
     w = synth.model_weights(spec, seed=9)
     x = _t(gpu, rng.standard_normal((n, 24)).astype(np.float32))
     da = tg.DeviceCSR.from_numpy(n, n, a.row_ptr, a.col_ind, a.val)

@@ -125,6 +125,7 @@ struct tg_model_s {
     tg::PinnedBuffer flag_host;
     std::unique_ptr<tg_spmm_plan_s> plan_raw, plan_sl;
     bool plan_sl_built = false;  // plan_sl holds A + I's row plan (ensure_plan_sl)
+    bool plan_raw_built = false;  // plan_raw holds A's row plan (ensure_plan_raw)
     // column-blocked copies for the large aggregations (fast precision):
     // A_norm for GCN, A's structure for SAGE-mean
     std::unique_ptr<tg::BlockedCSR> blk_sl, blk_raw;
@@ -363,6 +364,30 @@ void ensure_plan_sl(tg_model_s& m, int64_t n, int64_t nnz, hipStream_t s) {
     m.plan_sl_built = true;
 }
 
+// A's row plan, where something reads it: a SAGE layer whose aggregation
+// does not block (SAGE-Max, or no blocked copy of A).  Blocked SAGE-mean
+// layers run on the block plans alone (config-E reference-semantics SAGE:
+// one plan build and its synchronisation fewer per call); the plan then
+// carries only the sizes sage_forward checks.
+void ensure_plan_raw(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp, hipStream_t s) {
+    if (!m.need_raw()) return;
+    bool needed = m.blk_raw == nullptr;
+    for (auto& l : m.layers)
+        if (l.type == LType::SAGE && l.agg != TG_AGG_MEAN) needed = true;
+    if (m.plan_raw_built) return;
+    if (!needed) {
+        m.plan_raw->m = n;
+        m.plan_raw->nnz_bound = nnz;
+        m.plan_raw->row_ptr = rp;
+        m.plan_raw->precision = m.precision;
+        return;
+    }
+    const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
+    build_plan(*m.plan_raw, n, nnz, rp, m.max_wide(), chunk, s);
+    m.plan_raw->precision = m.precision;
+    m.plan_raw_built = true;
+}
+
 // Whether the forward can keep the cached adjacency state (prepare_adjacency
 // then rebuilds at most the blocked copies).
 bool adjacency_cached(const tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
@@ -385,6 +410,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
         if (m.built_block_rows != m.block_rows) {
             prepare_blocked(m, n, nnz, rp, ci, s);
             if (m.need_norm() || m.need_sl()) ensure_plan_sl(m, n, nnz, s);
+            ensure_plan_raw(m, n, nnz, rp, s);
         }
         return;
     }
@@ -395,10 +421,10 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     const int64_t chunk = m.precision == TG_PRECISION_EXACT ? (int64_t(1) << 24) : 0;
     // plans and buffers are rebuilt in place (they only grow), so a forward
     // with the reference's per-call preprocessing allocates nothing once warm
+    // A's row plan is built by ensure_plan_raw, once the blocking is known
     if (m.need_raw()) {
         if (!m.plan_raw) m.plan_raw = std::make_unique<tg_spmm_plan_s>();
-        build_plan(*m.plan_raw, n, nnz, rp, maxf, chunk, s);
-        m.plan_raw->precision = m.precision;
+        m.plan_raw_built = false;
     } else {
         m.plan_raw.reset();
     }
@@ -536,6 +562,7 @@ void prepare_adjacency(tg_model_s& m, int64_t n, int64_t nnz, const int32_t* rp,
     // place (the block plans counted before one synchronisation)
     prepare_blocked(m, n, nnz, rp, ci, s);
     if (m.need_norm() || m.need_sl()) ensure_plan_sl(m, n, nnz, s);
+    ensure_plan_raw(m, n, nnz, rp, s);
 }
 
 // GAT's scores buffer: src and dst scores [n x heads], then the blocked
