@@ -90,14 +90,20 @@ __global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(const int32_t* 
 }
 
 // Single workgroup: exclusive scan of part[0..nb) in place, part[nb] = total.
-__global__ __launch_bounds__(1024) void scan_parts_kernel(int64_t* __restrict__ part, int64_t nb) {
-    __shared__ int64_t lds[1024 / kWave];
+// 256 threads (one wavefront per SIMD): the workgroup fits beside three
+// workgroups of the MFMA GEMM on a compute unit, where a 1,024-thread one
+// (62 registers x 4 wavefronts per SIMD) waited for the GEMM's last
+// workgroups (0.5 ms in a reference-semantics forward, its plans' scans
+// beside layer 0's transform).
+__global__ __launch_bounds__(kScanBlock) void scan_parts_kernel(int64_t* __restrict__ part,
+                                                                int64_t nb) {
+    __shared__ int64_t lds[kScanBlock / kWave];
     int64_t carry = 0;
-    for (int64_t base = 0; base < nb; base += 1024) {
+    for (int64_t base = 0; base < nb; base += kScanBlock) {
         int64_t i = base + threadIdx.x;
         int64_t v = (i < nb) ? part[i] : 0;
         int64_t tot;
-        int64_t ex = block_exclusive_scan<1024>(v, lds, &tot);
+        int64_t ex = block_exclusive_scan<kScanBlock>(v, lds, &tot);
         if (i < nb) part[i] = carry + ex;
         carry += tot;
     }
@@ -179,7 +185,7 @@ void exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* tem
     const int64_t nb = ceil_div(n, kScanTile);
     scan_reduce_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(in, n, temp);
     TG_LAUNCH_CHECK();
-    scan_parts_kernel<<<1, 1024, 0, s>>>(temp, nb);
+    scan_parts_kernel<<<1, kScanBlock, 0, s>>>(temp, nb);
     TG_LAUNCH_CHECK();
     scan_apply_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(in, out, n, temp, nb);
     TG_LAUNCH_CHECK();
