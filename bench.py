@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of TinyGNN's sparse-inference hot path on one MI355X.
 
-Metric (BASELINE.json): CSR SpMM GB/s and % of HBM peak; forward ms at the
+Metric: CSR SpMM GB/s and % of HBM peak; forward ms at the
 232,965-node / 114,615,892-edge graph.
 
 Default run (N=1):
@@ -1175,7 +1175,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(this build runs on one GPU; sharding across GPUs is not implemented)", file=sys.stderr)
         sys.exit(2)
 
     import torch

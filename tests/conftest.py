@@ -15,7 +15,7 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD GPU (MI355X) and the built HIP library")
-    config.addinivalue_line("markers", "slow: full-size (BASELINE config) cases")
+    config.addinivalue_line("markers", "slow: full-size (benchmark configuration) cases")
 
 
 def pytest_sessionstart(session):

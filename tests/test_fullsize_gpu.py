@@ -1,4 +1,4 @@
-"""Full-size parity at the BASELINE configurations D and E (marked gpu, slow).
+"""Full-size parity at the benchmark configurations D and E (marked gpu, slow).
 
 The inputs are the benchmark's own seeded workloads (``bench.py`` through
 ``tinygnn_amd.synth``): the edge lists are drawn on the GPU, copied to the

@@ -1,4 +1,4 @@
-"""Seeded synthetic workloads for the BASELINE configurations.
+"""Seeded synthetic workloads for the benchmark configurations (A to E).
 
 The reference ships no generator for these shapes, so these are this
 package's own, fixed by seed and shared by the GPU path, the CPU oracle and
@@ -176,7 +176,7 @@ def model_weights(spec, seed: int = 0) -> dict:
     return w
 
 
-# The BASELINE model stacks (layer dicts as used by tinygnn_amd.Model and the
+# The benchmark model stacks (layer dicts as used by tinygnn_amd.Model and the
 # oracle): act = layer activation, post = Model InterActivation.
 def spec_gcn(f_in, hidden, classes):
     return [dict(type="gcn", **{"in": f_in}, out=hidden, act=1, post=0),
