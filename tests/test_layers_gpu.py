@@ -125,6 +125,25 @@ def test_gat_scores_bitexact(gpu, restate, f):
         np.testing.assert_array_equal(bits(dst.cpu().numpy()[:, h]), bits(wd))
 
 
+@pytest.mark.parametrize("heads,f", [(1, 4), (4, 64), (5, 32), (16, 64), (16, 12), (17, 8)])
+def test_gat_scores_bitexact_heads(gpu, restate, heads, f):
+    """The scores at more heads and nodes: workgroups of 128 (node, head)
+    pairs whose nodes straddle them, the LDS-staged path up to 16 heads of
+    at most 64 features (f % 4 == 0), the per-thread path past them."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(heads * 1000 + f)
+    n = 1003
+    wh = rng.standard_normal((n, heads * f)).astype(np.float32)
+    al = rng.standard_normal((heads, f)).astype(np.float32)
+    ar = rng.standard_normal((heads, f)).astype(np.float32)
+    src, dst = tg.gat_scores(_t(gpu, wh), heads, f, _t(gpu, al), _t(gpu, ar))
+    src, dst = src.cpu().numpy(), dst.cpu().numpy()
+    for h in range(heads):
+        ws, wd = restate.gat_scores(wh[:, h * f:(h + 1) * f], al[h], ar[h])
+        np.testing.assert_array_equal(bits(src[:, h]), bits(ws), err_msg=f"head {h}")
+        np.testing.assert_array_equal(bits(dst[:, h]), bits(wd), err_msg=f"head {h}")
+
+
 def _gat_case(restate, rng, n, f_in, f, heads, max_deg):
     a = restate.add_self_loops(random_csr(rng, n, n, avg_deg=10, max_deg=max_deg,
                                           empty_frac=0.05))
