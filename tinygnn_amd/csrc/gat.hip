@@ -160,22 +160,30 @@ __global__ __launch_bounds__(kScorePairs) void gat_scores_lds_kernel(
     // at most 16 vectors a thread, all loaded before the first store
     constexpr int kV = 16;  // kScorePairs * 64 / 4 / kScorePairs
     const int nv = np * f4;
+    // x / d as (x * ceil(2^16 / d)) >> 16: exact for x < 4096 and d <= 16
+    // (here x < 2048), where the division instructions dominated the loop
+    const unsigned mf4 = (65536u + f4 - 1) / f4, mh = (65536u + heads - 1) / heads;
+    const int64_t node0 = p0 / heads;
+    const int r0 = static_cast<int>(p0 - node0 * heads);
     float4 xv[kV];
 #pragma unroll
     for (int u = 0; u < kV; ++u) {
         const int e = threadIdx.x + u * kScorePairs;
         if (e < nv) {
-            const int pl = e / f4, k = (e - pl * f4) * 4;
-            const int64_t p = p0 + pl;
-            xv[u] = *reinterpret_cast<const float4*>(
-                wh + (p / heads) * ldwh + (p % heads) * static_cast<int64_t>(f) + k);
+            const int pl = static_cast<int>((static_cast<unsigned>(e) * mf4) >> 16);
+            const int k = (e - pl * f4) * 4;
+            const int q = r0 + pl;  // the pair's offset from node0's first head
+            const int dn = static_cast<int>((static_cast<unsigned>(q) * mh) >> 16);
+            const int h = q - dn * heads;
+            xv[u] = *reinterpret_cast<const float4*>(wh + (node0 + dn) * ldwh + h * f + k);
         }
     }
 #pragma unroll
     for (int u = 0; u < kV; ++u) {
         const int e = threadIdx.x + u * kScorePairs;
         if (e < nv) {
-            const int pl = e / f4, k = (e - pl * f4) * 4;
+            const int pl = static_cast<int>((static_cast<unsigned>(e) * mf4) >> 16);
+            const int k = (e - pl * f4) * 4;
             float* d = sm + pl * fp + k;
             d[0] = xv[u].x; d[1] = xv[u].y; d[2] = xv[u].z; d[3] = xv[u].w;
         }
