@@ -499,6 +499,40 @@ def test_blocked_gcn_unit_weights(gpu, restate, variant):
             assert m.blocking_info()["sl_direct"] == direct, f"call {i}"
 
 
+@pytest.mark.parametrize("rows_per_block", [48, 100, 1500])
+def test_row_split_block_counts(gpu, restate, rows_per_block):
+    """The row split at 63 blocks (its maximum), 30 and 2: A + I's copy split
+    from A directly gives the bits of the copy split from the written A + I
+    (GCN, factored), both within tolerance of the oracle; rows of up to
+    9,000 entries take the row scatter's long-row workgroups."""
+    import tinygnn_amd as tg
+    rng = np.random.default_rng(17 + rows_per_block)
+    n = 3000
+    a = random_csr(rng, n, n, avg_deg=100, max_deg=9000, empty_frac=0.03)
+    rows = np.repeat(np.arange(n), np.diff(a.row_ptr)).astype(np.int32)
+    keep = rows != a.col_ind
+    g = restate.edge_list_to_csr(rows[keep], a.col_ind[keep].astype(np.int32), n)
+    spec = synth.spec_gcn(16, 64, 5)
+    w = synth.model_weights(spec, seed=3)
+    x = rng.standard_normal((n, 16)).astype(np.float32)
+    want = restate.model_forward(spec, w, g, x)
+    da = tg.DeviceCSR.from_numpy(n, n, g.row_ptr, g.col_ind, g.val)
+    xt = _t(gpu, x)
+    outs = {}
+    for direct in (True, False):
+        m = tg.Model.from_spec(spec, w)
+        m.set_blocking(rows_per_block)
+        m.set_self_loop_split(direct)
+        outs[direct] = m.forward(da, xt, mode=tg.FORWARD_REFERENCE).cpu().numpy()
+        info = m.blocking_info()
+        assert info["blocks_sl"] == -(-n // rows_per_block)
+        assert info["sl_direct"] == direct
+        again = m.forward(da, xt, mode=tg.FORWARD_CACHED).cpu().numpy()
+        np.testing.assert_array_equal(bits(again), bits(outs[direct]))
+    np.testing.assert_array_equal(bits(outs[True]), bits(outs[False]))
+    assert_close(outs[True], want, what=f"row split, {rows_per_block} rows per block")
+
+
 @pytest.mark.parametrize("avg_deg", [30, 100])
 @pytest.mark.parametrize("model", ["gcn", "gat"])
 @pytest.mark.parametrize("order", ["sorted", "unsorted", "unsorted_in_block"])
@@ -512,8 +546,8 @@ def test_direct_self_loop_split_long_rows(gpu, restate, order, model, avg_deg):
     forward take the written A + I; so does a row out of order inside one
     block (two adjacent columns around the diagonal swapped), where the
     block order holds but the diagonal's place would not be unique.  At 100
-    entries per row on average the split is the row split (binary-searched
-    block starts, the diagonal's place searched too)."""
+    entries per row on average the split is the row split (searched block
+    starts, the diagonal's place searched too)."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(91)
     n = 3000
