@@ -125,18 +125,27 @@ def test_gat_scores_bitexact(gpu, restate, f):
         np.testing.assert_array_equal(bits(dst.cpu().numpy()[:, h]), bits(wd))
 
 
-@pytest.mark.parametrize("heads,f", [(1, 4), (4, 64), (5, 32), (16, 64), (16, 12), (17, 8)])
-def test_gat_scores_bitexact_heads(gpu, restate, heads, f):
+@pytest.mark.parametrize("heads,f,pitch", [(1, 4, 0), (4, 64, 0), (5, 32, 0), (16, 64, 0),
+                                            (16, 12, 0), (17, 8, 0), (1, 41, 64), (1, 41, 44),
+                                            (1, 41, 0), (2, 41, 96)])
+def test_gat_scores_bitexact_heads(gpu, restate, heads, f, pitch):
     """The scores at more heads and nodes: workgroups of 128 (node, head)
     pairs whose nodes straddle them, the LDS-staged path up to 16 heads of
-    at most 64 features (f % 4 == 0), the per-thread path past them."""
+    at most 64 features (f % 4 == 0, or one head whose rows are padded to a
+    multiple of 4 floats: `pitch`, 0 = unpadded), the per-thread path past
+    them."""
     import tinygnn_amd as tg
     rng = np.random.default_rng(heads * 1000 + f)
     n = 1003
     wh = rng.standard_normal((n, heads * f)).astype(np.float32)
     al = rng.standard_normal((heads, f)).astype(np.float32)
     ar = rng.standard_normal((heads, f)).astype(np.float32)
-    src, dst = tg.gat_scores(_t(gpu, wh), heads, f, _t(gpu, al), _t(gpu, ar))
+    whd = _t(gpu, wh)
+    if pitch:
+        padded = gpu.full((n, pitch), float("nan"), device="cuda")
+        padded[:, :heads * f] = whd
+        whd = padded[:, :heads * f]  # rows `pitch` floats apart, NaN in the padding
+    src, dst = tg.gat_scores(whd, heads, f, _t(gpu, al), _t(gpu, ar))
     src, dst = src.cpu().numpy(), dst.cpu().numpy()
     for h in range(heads):
         ws, wd = restate.gat_scores(wh[:, h * f:(h + 1) * f], al[h], ar[h])

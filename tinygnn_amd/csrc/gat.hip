@@ -135,7 +135,8 @@ __global__ __launch_bounds__(256) void gat_scores_kernel(int64_t n, int heads, i
 }
 
 // gat_scores_kernel with the workgroup's Wh segments staged in LDS (f <= 64,
-// f % 4 == 0, 16-byte aligned rows, heads <= 16: at most 41.6 KB): 128
+// f % 4 == 0 or one head with row padding to the next multiple of 4,
+// 16-byte aligned rows, heads <= 16: at most 41.6 KB): 128
 // (node, head) pairs per workgroup,
 // their segments read with coalesced 128-bit loads (a thread's own 64-float
 // segment read by itself scatters every load over 64 lines: config E's
@@ -148,14 +149,16 @@ __global__ __launch_bounds__(kScorePairs) void gat_scores_lds_kernel(
     int64_t n, int heads, int f, const float* __restrict__ wh, int64_t ldwh,
     const float* __restrict__ al, const float* __restrict__ ar, float* __restrict__ src,
     float* __restrict__ dst) {
-    extern __shared__ float sm[];  // [kScorePairs][f + 1], then a_l, a_r: [heads][f + 1]
-    const int fp = f + 1;
+    extern __shared__ float sm[];  // [kScorePairs][fp], then a_l, a_r: [heads][fp]
+    // a segment of f4 128-bit vectors (one head whose f is not a multiple
+    // of 4: its last vector runs into the row's padding, loaded, never used)
+    const int f4 = (f + 3) / 4;
+    const int fp = 4 * f4 + 1;
     float* sa = sm + kScorePairs * fp;
     float* sb = sa + heads * fp;
     const int64_t total = n * heads;
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kScorePairs;
     const int np = static_cast<int>(total - p0 < kScorePairs ? total - p0 : kScorePairs);
-    const int f4 = f / 4;
     // the pairs' segments (a segment's f floats are whole 128-bit vectors):
     // at most 16 vectors a thread, all loaded before the first store
     constexpr int kV = 16;  // kScorePairs * 64 / 4 / kScorePairs
@@ -1226,8 +1229,10 @@ void gat_scores(int64_t n, int64_t heads, int64_t f, const float* wh, int64_t ld
     if (n == 0) return;
     require(wh && al && ar && src && dst, "GATLayer: null pointer");
     const bool al16 = reinterpret_cast<uintptr_t>(wh) % 16 == 0;
-    if (f <= 64 && f % 4 == 0 && ldwh % 4 == 0 && al16 && heads <= 16) {
-        const size_t lds = static_cast<size_t>(kScorePairs + 2 * heads) * (f + 1) * sizeof(float);
+    const int64_t f4x4 = round_up(f, 4);
+    const bool segs = f % 4 == 0 || (heads == 1 && ldwh >= f4x4);  // whole vectors per segment
+    if (f <= 64 && segs && ldwh % 4 == 0 && al16 && heads <= 16) {
+        const size_t lds = static_cast<size_t>(kScorePairs + 2 * heads) * (f4x4 + 1) * sizeof(float);
         gat_scores_lds_kernel<<<static_cast<unsigned>(ceil_div(n * heads, kScorePairs)),
                                 kScorePairs, lds, s>>>(n, static_cast<int>(heads),
                                                        static_cast<int>(f), wh, ldwh, al, ar, src,
